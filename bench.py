@@ -1,0 +1,351 @@
+"""Benchmark of the MI355X full-attention hot path.
+
+Headline (``value``): paged GQA decode step at B=32, per-sequence contexts
+uniform in [128, 2048] (seeded), 8 q / 2 kv heads, d=256, randperm page table,
+one step = K/V append + split-K partial + merge + sigmoid gate pack, captured
+in one HIP graph and replayed.  ``value`` is algorithmic HBM GB/s of the step
+(KV bytes read + q/gate/out/append/page-table bytes, split scratch excluded).
+
+Also reported (``extra``): config 1 latency, config 3 and 4 varlen prefill
+TFLOP/s, config 5 long-context decode GB/s.  ``roofline`` is the split kernel
+timed alone with HIP events on its stream; ``cpu_baseline`` is the CPU oracle
+on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HQ, HKV, D, PAGE = 8, 2, 256, 16
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ workloads
+
+def decode_workload(lens, dev, seed, kv_scale=1.0, contiguous=False):
+    B = len(lens)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    max_pages = -(-max(lens) // PAGE) + 1
+    num_pages = B * max_pages
+    if contiguous:
+        bt = torch.arange(num_pages, device=dev, dtype=torch.int32).view(B, max_pages)
+    else:
+        bt = torch.randperm(num_pages, device=dev, generator=gen).view(B, max_pages)
+        bt = bt.to(torch.int32).contiguous()
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=gen) * scale).to(torch.bfloat16)
+
+    kc = rnd(num_pages, HKV, PAGE, D, scale=kv_scale)
+    vc = rnd(num_pages, HKV, PAGE, D, scale=kv_scale)
+    return dict(
+        lens=lens, bt=bt, kc=kc, vc=vc, q=rnd(B, HQ, D), kn=rnd(B, HKV, D), vn=rnd(B, HKV, D),
+        gate=rnd(1, HQ, B, D),
+        pos=torch.tensor([n - 1 for n in lens], dtype=torch.int64, device=dev),
+    )
+
+
+def decode_bytes(lens):
+    """Algorithmic HBM bytes of one decode step (split scratch excluded):
+    KV of every attended token, q + gate + gated output, the K/V append
+    (read + write), page-table entries and pos."""
+    B = len(lens)
+    kv = sum(lens) * HKV * D * 2 * 2
+    qgo = B * 3 * HQ * D * 2
+    append = B * 2 * HKV * D * 2 * 2
+    bt = 4 * sum(-(-n // PAGE) for n in lens)
+    return kv + qgo + append + bt + 8 * B
+
+
+def split_kernel_bytes(lens):
+    """Algorithmic bytes the split kernel itself must read: KV + q + table."""
+    B = len(lens)
+    return sum(lens) * HKV * D * 2 * 2 + B * HQ * D * 2 + 4 * sum(-(-n // PAGE) for n in lens) \
+        + 8 * B
+
+
+def prefill_flops(lengths):
+    return sum(n * (n + 1) // 2 for n in lengths) * 4 * D * HQ
+
+
+# ------------------------------------------------------------------ timing
+
+def time_graph(fn, steps, warmup):
+    """Capture fn in a graph, replay warmup + steps; return ms per replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def time_events(fn, iters, warmup=3):
+    """Average ms of fn's launches measured with HIP events on the current
+    stream (the stream the kernels are launched on)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    for _ in range(iters):
+        fn()
+    en.record()
+    en.synchronize()
+    return st.elapsed_time(en) / iters
+
+
+def time_graph_events(fn, iters):
+    """fn captured in a graph of `iters` back-to-back calls, timed with events:
+    removes host launch overhead from a per-kernel figure."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(iters):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.record()
+    g.replay()
+    en.record()
+    en.synchronize()
+    return st.elapsed_time(en) / iters
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
+    ap.add_argument("--only", default="", help="comma list of extras to run")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the attention path "
+              "shards by sequence with no cross-GPU exchange, so the per-GPU figure is the "
+              "one-GPU figure.", file=sys.stderr)
+        sys.exit(2)
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    pkg._lib.load()
+
+    # ---- headline: config 2 decode step ----------------------------------------
+    gen = torch.Generator().manual_seed(2)
+    lens = torch.randint(128, 2049, (32,), generator=gen).tolist()
+    w = decode_workload(lens, dev, seed=2)
+    scratch = pkg.allocate_split_scratch(HQ, D, batch=32, device=dev)
+
+    def step():
+        ctx = pkg.call_paged_gqa_attention_decode_triton(
+            w["q"], w["kn"], w["vn"], w["kc"], w["vc"], w["bt"], w["pos"], scratch)
+        return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w["gate"])
+
+    log(f"decode config2: sum(L)={sum(lens)} B=32")
+    ms = time_graph(step, args.steps, args.warmup)
+    step_bytes = decode_bytes(lens)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+
+    # dominant kernel alone: split partial pass, events over a graph of launches
+    m_p, l_p, acc_p = scratch
+
+    def split_only():
+        torch.ops.wy_lib.paged_gqa_attention_decode_split(
+            w["q"], w["kc"], w["vc"], w["bt"], m_p, l_p, acc_p, w["pos"], 0)
+
+    split_ms = time_graph_events(split_only, 100)
+    sbytes = split_kernel_bytes(lens)
+    split_gbs = sbytes / (split_ms * 1e-3) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "decode_split_config2_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": "decode-attn HBM GB/s (B=32 paged GQA decode step, contexts U[128,2048])",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 q/k/v/gate, randperm page table)",
+        "config": {"workload": "config2: paged GQA decode step B=32, L~U[128,2048], "
+                               "8q/2kv heads, d=256, 16-token pages",
+                   "global_batch": 32, "sum_context_tokens": sum(lens),
+                   "step": "append+split+combine+gate, one HIP graph replay",
+                   "parallelism": "single GPU"},
+        "roofline": {"kernel": "paged_decode_split_kernel", "bound": "hbm",
+                     "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": sbytes,
+                     "avg_launch_us": round(split_ms * 1e3, 3)},
+    }
+    log(f"  step {ms*1e3:.2f} us  {gbs:.0f} GB/s; split {split_ms*1e3:.2f} us {split_gbs:.0f} GB/s")
+
+    extra = {}
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not args.quick and (not only or name in only)
+
+    # ---- config 1: B=1, 256 tokens, contiguous table --------------------------
+    if want("c1"):
+        w1 = decode_workload([256], dev, seed=1, contiguous=True)
+        sc1 = pkg.allocate_split_scratch(HQ, D, batch=1, device=dev)
+
+        def step1():
+            ctx = pkg.call_paged_gqa_attention_decode_triton(
+                w1["q"], w1["kn"], w1["vn"], w1["kc"], w1["vc"], w1["bt"], w1["pos"], sc1)
+            return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w1["gate"])
+
+        ms1 = time_graph(step1, 500, 50)
+        extra["config1_decode_B1_L256"] = {"us_per_step": round(ms1 * 1e3, 2),
+                                           "GB/s": round(decode_bytes([256]) / ms1 / 1e6, 1)}
+        log(f"config1: {ms1*1e3:.2f} us")
+        del w1
+
+    # ---- config 3: varlen prefill 32 x 128 -------------------------------------
+    if want("c3"):
+        extra["config3_prefill_32x128"] = prefill_bench(pkg, dev, [128] * 32, seed=3)
+    # ---- config 4: mixed lengths log-uniform [16, 4096] ------------------------
+    if want("c4"):
+        g4 = torch.Generator().manual_seed(4)
+        lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
+        lens4 = [int(x) for x in lens4.round().tolist()]
+        extra["config4_prefill_mixed"] = prefill_bench(pkg, dev, lens4, seed=4)
+    # ---- config 5: B=64 x 32768 ------------------------------------------------
+    if want("c5"):
+        w5 = decode_workload([32768] * 64, dev, seed=5, kv_scale=0.5)
+        sc5 = pkg.allocate_split_scratch(HQ, D, batch=64, device=dev)
+        m5, l5, a5 = sc5
+
+        def split5():
+            torch.ops.wy_lib.paged_gqa_attention_decode_split(
+                w5["q"], w5["kc"], w5["vc"], w5["bt"], m5, l5, a5, w5["pos"], 0)
+
+        def step5():
+            ctx = pkg.call_paged_gqa_attention_decode_triton(
+                w5["q"], w5["kn"], w5["vn"], w5["kc"], w5["vc"], w5["bt"], w5["pos"], sc5)
+            return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w5["gate"])
+
+        ms5 = time_graph(step5, 20, 3)
+        sp5 = time_events(split5, 20)
+        b5 = decode_bytes(w5["lens"])
+        extra["config5_decode_B64_L32768"] = {
+            "us_per_step": round(ms5 * 1e3, 1), "GB/s": round(b5 / ms5 / 1e6, 1),
+            "split_us": round(sp5 * 1e3, 1),
+            "split_GB/s": round(split_kernel_bytes(w5["lens"]) / sp5 / 1e6, 1),
+            "frac_of_hbm_peak": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4)}
+        log(f"config5: {ms5*1e3:.1f} us")
+        del w5, sc5
+        torch.cuda.empty_cache()
+
+    if extra:
+        result["extra"] = extra
+
+    # ---- CPU baseline: oracle on a bounded sample of config 2 -------------------
+    if not args.quick and (not only or "cpu" in only):
+        result["cpu_baseline"] = cpu_baseline(w, lens)
+
+    print(json.dumps(result), flush=True)
+
+
+def prefill_bench(pkg, dev, lengths, seed):
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    total = sum(lengths)
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, generator=gen).to(torch.bfloat16)
+
+    q, k, v = rnd(total, HQ, D), rnd(total, HKV, D), rnd(total, HKV, D)
+    cu_list = [0]
+    for n in lengths:
+        cu_list.append(cu_list[-1] + n)
+    cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
+    mx = max(lengths)
+
+    def run():
+        return pkg.gqa_attention_varlen_causal(q, k, v, cu, mx)
+
+    ms = time_graph_events(run, 20)
+    fl = prefill_flops(lengths)
+    tf = fl / (ms * 1e-3) / 1e12
+    min_bytes = total * (HQ * D * 2 * 2 + HKV * D * 2 * 2)
+    attain = min(MFMA_BF16_PEAK_TFLOPS, fl / (min_bytes / (HBM_PEAK_GBS * 1e9)) / 1e12)
+    log(f"prefill {len(lengths)} seqs total {total}: {ms*1e3:.1f} us {tf:.1f} TFLOP/s")
+    return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "GFLOP": round(fl / 1e9, 3),
+            "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "attainable_TFLOP/s": round(attain, 1), "frac_of_attainable": round(tf / attain, 4),
+            "total_tokens": total, "lengths": lengths if len(lengths) <= 32 else None}
+
+
+def cpu_baseline(w, lens):
+    """CPU oracle (fp32 torch, the build's own restatement) on the first
+    sequences of the config-2 workload, repeated for >= 10 s."""
+    from oracle import attention_oracle as orc
+
+    cores = torch.get_num_threads()
+    nseq = 8
+    sample = lens[:nseq]
+    q = w["q"][:nseq].cpu()
+    kc, vc = w["kc"].cpu(), w["vc"].cpu()
+    bt = w["bt"][:nseq].cpu()
+    orc.paged_decode(q, kc, vc, bt, sample)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        orc.paged_decode(q, kc, vc, bt, sample)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    gbs = split_kernel_bytes(sample) / dt / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{nseq} of the 32 config-2 sequences (sum L={sum(sample)}), "
+                      f"{reps} reps, {dt*1e3:.2f} ms each",
+            "ms_per_sample": round(dt * 1e3, 3)}
+
+
+if __name__ == "__main__":
+    main()

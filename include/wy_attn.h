@@ -1,0 +1,160 @@
+/*
+ * wy_attn.h -- C ABI of the MI355X (gfx950) full-attention hot path of the
+ * Qwen3.5 inference engine.
+ *
+ * Every entry point takes plain device pointers, element strides (int64, in
+ * elements, not bytes), sizes and a hipStream_t passed as `void *`.  No torch
+ * types cross this boundary.  Each call only enqueues work on `stream`; it
+ * never synchronises and never allocates, so it may be captured into a HIP
+ * graph.  Return value: 0 on success, a negative WY_E_* code for a rejected
+ * argument (nothing was launched), or a positive hipError_t from the launch.
+ *
+ * Tensor conventions (bf16 is raw IEEE bfloat16 bits, uint16_t):
+ *   page pool   k_cache / v_cache [num_pages, H_kv, PAGE=16, D] bf16
+ *   block_table [B, max_pages] int32, logical page -> physical page
+ *   pos         [B] int64, tokens already cached per sequence
+ *   cu_seqlens  [B+1] int32, prefix sums of packed sequence lengths
+ *
+ * Each function names the reference interface it replaces
+ * (sujuyu/qwen3_5-triton-inference-engine, file:line).
+ */
+#ifndef WY_ATTN_H
+#define WY_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WY_PAGE_SIZE 16
+#define WY_MAX_SPLITS 128
+
+/* Error codes (negative).  Positive values are hipError_t. */
+#define WY_OK 0
+#define WY_E_NULL (-1)        /* a required pointer is NULL                     */
+#define WY_E_SHAPE (-2)       /* a size is out of the supported range           */
+#define WY_E_LAYOUT (-3)      /* a stride / alignment the kernel cannot address */
+#define WY_E_UNSUPPORTED (-4) /* head_dim / group size without a kernel         */
+
+/* Human-readable text for a return code (static storage). */
+const char *wy_status_string(int code);
+
+/* Library version and the code-object target it was built for ("gfx950"). */
+const char *wy_build_info(void);
+
+/*
+ * K/V append for one decode step.
+ *   k_cache[bt[b, pos[b]/16], h, pos[b]%16, :] = k_new[b, h, :]   (same for V)
+ * kc_strides/vc_strides: 4 strides of the pools; kn_strides/vn_strides: 3
+ * strides of k_new/v_new [B, H_kv, D].  Bit-exact copy.
+ * Replaces wy_lib::paged_kv_append
+ *   (triton_kernels/gqa_attention_decode_paged.py:254-305, kernel :176-250).
+ */
+int wy_paged_kv_append(void *k_cache, void *v_cache, const int64_t *kc_strides,
+                       const int64_t *vc_strides, const void *k_new,
+                       const void *v_new, const int64_t *kn_strides,
+                       const int64_t *vn_strides, const int32_t *block_table,
+                       int64_t bt_stride0, const int64_t *pos, int batch,
+                       int num_kv_heads, int head_dim, void *stream);
+
+/*
+ * Packed varlen K/V scatter into the page pool (prefill).
+ *   for b, t < n_b: k_cache[bt[b, t/16], h, t%16, :] = k[h, cu[b]+t, :]
+ * k/v packed [H_kv, total, D] with strides k_strides/v_strides (any order).
+ * Slots past a sequence's end and unreferenced pages are left untouched.
+ * Replaces wy_lib::paged_kv_fill_varlen
+ *   (triton_kernels/gqa_attention_decode_paged.py:492-561, kernel :398-489)
+ * and the single-sequence paged_kv_fill (:355-375) with batch = 1.
+ */
+int wy_paged_kv_fill_varlen(void *k_cache, void *v_cache,
+                            const int64_t *kc_strides, const int64_t *vc_strides,
+                            const void *k_packed, const void *v_packed,
+                            const int64_t *k_strides, const int64_t *v_strides,
+                            const int32_t *block_table, int64_t bt_stride0,
+                            const int32_t *cu_seqlens, int batch,
+                            int num_kv_heads, int head_dim, int max_seqlen,
+                            void *stream);
+
+/*
+ * Split-K paged GQA decode, partial pass.  For sequence b, KV head h and split
+ * s it reduces pages [s*pps, min((s+1)*pps, npg)) of the sequence, with
+ * npg = ceil((pos[b]+1)/16) and pps = max(ceil(npg/128), min_pages_per_split),
+ * into m_partial/l_partial [B, H_q, 128] and acc_partial [B, H_q, 128, D]
+ * (fp32, unnormalised online-softmax state, natural-log base).  Splits at or
+ * past the active count are not written.  q [B, H_q, D] bf16, scale 1/sqrt(D).
+ * Replaces wy_lib::paged_gqa_attention_decode_split
+ *   (triton_kernels/gqa_attention_decode_paged.py:822-891, kernel :624-733).
+ */
+int wy_paged_decode_split(const void *q, const int64_t *q_strides,
+                          const void *k_cache, const void *v_cache,
+                          const int64_t *kc_strides, const int64_t *vc_strides,
+                          const int32_t *block_table, int64_t bt_stride0,
+                          const int64_t *pos, float *m_partial, float *l_partial,
+                          float *acc_partial, const int64_t *ml_strides,
+                          const int64_t *acc_strides, int batch, int num_q_heads,
+                          int num_kv_heads, int head_dim, int max_pages,
+                          int min_pages_per_split, void *stream);
+
+/*
+ * Split-K merge: out[b, hq, :] = sum_s a_s acc_s / sum_s a_s l_s with
+ * a_s = exp(m_s - max m), over the active splits of sequence b (same
+ * partition formula as wy_paged_decode_split).  out [B, H_q, D] bf16 with
+ * strides out_strides.
+ * Replaces wy_lib::paged_gqa_attention_decode_combine
+ *   (triton_kernels/gqa_attention_decode_paged.py:901-939, kernel :747-817).
+ */
+int wy_paged_decode_combine(const float *m_partial, const float *l_partial,
+                            const float *acc_partial, const int64_t *ml_strides,
+                            const int64_t *acc_strides, const int64_t *pos,
+                            void *out, const int64_t *out_strides, int batch,
+                            int num_q_heads, int head_dim,
+                            int min_pages_per_split, void *stream);
+
+/*
+ * Packed varlen causal GQA prefill attention on bf16 MFMA.
+ *   out[t, hq, :] = softmax_{j<=i}(q_i . k_j / sqrt(D)) V  within each sequence
+ * q/out [total, H_q, D], k/v [total, H_kv, D] bf16 (innermost stride must be
+ * 1, rows 16-byte aligned).  max_seqlen is the host-side longest length.
+ * Replaces wy_lib::gqa_attention_varlen_causal
+ *   (triton_kernels/gqa_attention_varlen_causal.py:214-278, kernel :101-210).
+ */
+int wy_varlen_causal_prefill(const void *q, const int64_t *q_strides,
+                             const void *k, const int64_t *k_strides,
+                             const void *v, const int64_t *v_strides, void *out,
+                             const int64_t *out_strides,
+                             const int32_t *cu_seqlens, int batch,
+                             int num_q_heads, int num_kv_heads, int head_dim,
+                             int max_seqlen, void *stream);
+
+/*
+ * Partial rotate-half RoPE on dims [0, rotary_dim) of x [B, H, T, D] bf16;
+ * dims [rotary_dim, D) are copied bit-exactly.  angle = float(pos) * inv_freq[j]
+ * in fp32.  position_ids [B, T] is int32 (pos_is_int64 = 0) or int64 (= 1).
+ * x_strides / out_strides / pos_strides are element strides.
+ * Replaces wy_lib::partial_rope
+ *   (triton_kernels/partial_rope.py:145-198, kernel :34-132).
+ */
+int wy_partial_rope(const void *x, const int64_t *x_strides, void *out,
+                    const int64_t *out_strides, const void *position_ids,
+                    const int64_t *pos_strides, int pos_is_int64,
+                    const float *inv_freq, int batch, int num_heads,
+                    int num_tokens, int head_dim, int rotary_dim, void *stream);
+
+/*
+ * Sigmoid output gate + head packing:
+ *   out[t, h*D + d] = bf16(float(x[0,h,t,d]) * sigmoid(float(gate[0,h,t,d])))
+ * x, gate [1, H, T, D] bf16 with any strides; out [T, H*D] contiguous.
+ * Replaces wy_lib::attention_gate_pack
+ *   (triton_kernels/attention_gate_pack.py:77-126, kernel :20-63).
+ */
+int wy_attention_gate_pack(const void *x, const int64_t *x_strides,
+                           const void *gate, const int64_t *gate_strides,
+                           void *out, int num_heads, int num_tokens,
+                           int head_dim, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WY_ATTN_H */

@@ -1,0 +1,57 @@
+"""MI355X (gfx950) full-attention hot path of the Qwen3.5 inference engine.
+
+Hand-written HIP kernels behind the reference engine's ``wy_lib::`` torch ops.
+Module names mirror the reference's ``triton_kernels/`` files so a caller
+switches by import path only; ``install_as_triton_kernels()`` makes the
+reference's own import lines resolve to these modules.
+"""
+
+from __future__ import annotations
+
+import sys
+
+from . import _lib
+from .attention import (
+    PackedBatch,
+    build_packed_batch,
+    decode_attention_step,
+    prefill_attention_packed,
+)
+from .attention_gate_pack import attention_gate_pack
+from .cache import AttnCaches, allocate_attn_caches
+from .gqa_attention_decode_paged import (
+    MAX_SPLITS,
+    MIN_PAGES_PER_SPLIT,
+    PAGE_SIZE,
+    allocate_paged_kv_cache,
+    allocate_split_scratch,
+    call_paged_gqa_attention_decode_triton,
+    paged_gqa_attention_decode_combine,
+    paged_gqa_attention_decode_split,
+    paged_kv_append,
+    paged_kv_fill,
+    paged_kv_fill_varlen,
+    physical_rows,
+)
+from .gqa_attention_varlen_causal import build_cu_seqlens, gqa_attention_varlen_causal
+from .paging import PagePool, SequencePages, allocate_block_table
+from .partial_rope import partial_rope, rope_inv_freq
+
+
+def install_as_triton_kernels() -> None:
+    """Alias the reference module paths (``triton_kernels.<op>`` and
+    ``engine.paging``) to this package's modules in ``sys.modules``."""
+    from . import (attention_gate_pack, gqa_attention_decode_paged,
+                   gqa_attention_varlen_causal, paging, partial_rope)
+    for name, mod in (
+        ("triton_kernels.gqa_attention_decode_paged", gqa_attention_decode_paged),
+        ("triton_kernels.gqa_attention_varlen_causal", gqa_attention_varlen_causal),
+        ("triton_kernels.partial_rope", partial_rope),
+        ("triton_kernels.attention_gate_pack", attention_gate_pack),
+        ("engine.paging", paging),
+    ):
+        sys.modules[name] = mod
+
+
+def library_loaded() -> bool:
+    return _lib._lib is not None

@@ -1,0 +1,87 @@
+"""ctypes binding of ``lib/libwy_attn.so`` (declared in include/wy_attn.h).
+
+This module is the only place that touches the C ABI.  There is no fallback:
+if the library is missing or a call returns an error, a RuntimeError is
+raised.  Strides cross the boundary as int64 arrays in elements, streams as
+the raw ``hipStream_t`` of torch's current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libwy_attn.so"
+
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+# name -> argtypes (all return int status)
+_SIGNATURES = {
+    "wy_paged_kv_append": [_vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _c_i64p, _vp,
+                           _i64, _vp, _i, _i, _i, _vp],
+    "wy_paged_kv_fill_varlen": [_vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _c_i64p,
+                                _vp, _i64, _vp, _i, _i, _i, _i, _vp],
+    "wy_paged_decode_split": [_vp, _c_i64p, _vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp,
+                              _vp, _vp, _vp, _c_i64p, _c_i64p, _i, _i, _i, _i, _i, _i,
+                              _vp],
+    "wy_paged_decode_combine": [_vp, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _i,
+                                _i, _i, _i, _vp],
+    "wy_varlen_causal_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
+                                 _vp, _i, _i, _i, _i, _i, _vp],
+    "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,
+                        _i, _vp],
+    "wy_attention_gate_pack": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _i, _vp],
+}
+
+EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build the HIP extension first "
+            "(python qwen3_5-triton-inference-engine_amd/build.py)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    lib.wy_status_string.argtypes = [ctypes.c_int]
+    lib.wy_status_string.restype = ctypes.c_char_p
+    lib.wy_build_info.argtypes = []
+    lib.wy_build_info.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def strides(t: torch.Tensor):
+    s = t.stride()
+    return (ctypes.c_int64 * len(s))(*s)
+
+
+def ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.wy_status_string(rc).decode()
+        raise RuntimeError(f"{name} failed with code {rc}: {msg}")

@@ -1,0 +1,169 @@
+// Page-pool writers: the per-step K/V append and the packed varlen scatter.
+//
+// Both are pure data movement, bit-exact by construction.  The address of a
+// token row in the pool follows the page-table contract of
+// engine/paging.py:23 (reference):
+//     row(t, h) = (block_table[t // 16] * H + h) * 16 + t % 16
+// expressed here through the pool's four strides so any pool layout with a
+// unit innermost stride takes the 16-byte path.
+#include "wy_common.h"
+
+using namespace wy;
+
+namespace {
+
+// ---------------------------------------------------------------- append --
+// One 64-lane wavefront per (sequence, KV head); lanes move 16-byte chunks of
+// the K row and then the V row.  Reference: gqa_attention_decode_paged.py:176-250.
+template <bool kVec>
+__global__ __launch_bounds__(64) void paged_kv_append_kernel(
+    bf16_t *__restrict__ kc, bf16_t *__restrict__ vc, int64_t kc_p, int64_t kc_h,
+    int64_t kc_s, int64_t kc_d, int64_t vc_p, int64_t vc_h, int64_t vc_s,
+    int64_t vc_d, const bf16_t *__restrict__ kn, const bf16_t *__restrict__ vn,
+    int64_t kn_b, int64_t kn_h, int64_t kn_d, int64_t vn_b, int64_t vn_h,
+    int64_t vn_d, const int32_t *__restrict__ bt, int64_t bt_b,
+    const int64_t *__restrict__ pos, int D) {
+  const int b = blockIdx.x, h = blockIdx.y;
+  const int64_t p = pos[b];
+  const int64_t lp = p / kPage, slot = p % kPage;
+  const int64_t phys = int64_t(bt[b * bt_b + lp]);
+  bf16_t *kdst = kc + phys * kc_p + h * kc_h + slot * kc_s;
+  bf16_t *vdst = vc + phys * vc_p + h * vc_h + slot * vc_s;
+  const bf16_t *ksrc = kn + b * kn_b + h * kn_h;
+  const bf16_t *vsrc = vn + b * vn_b + h * vn_h;
+  if constexpr (kVec) {
+    const int chunks = D / 8;
+    for (int i = threadIdx.x; i < 2 * chunks; i += 64) {
+      if (i < chunks)
+        st16(kdst + i * 8, ld16(ksrc + i * 8));
+      else
+        st16(vdst + (i - chunks) * 8, ld16(vsrc + (i - chunks) * 8));
+    }
+  } else {
+    for (int d = threadIdx.x; d < D; d += 64) {
+      kdst[d * kc_d] = ksrc[d * kn_d];
+      vdst[d * vc_d] = vsrc[d * vn_d];
+    }
+  }
+}
+
+// ----------------------------------------------------------- varlen fill --
+// One 256-thread workgroup per (logical page, KV head, sequence): it moves the
+// page's valid rows of K and V (at most 16 x D each).  Pages past the
+// sequence's length exit at once.  Rows past the sequence end inside the last
+// page are neither read nor written.
+// Reference: gqa_attention_decode_paged.py:398-489.
+template <bool kVec>
+__global__ __launch_bounds__(256) void paged_kv_fill_varlen_kernel(
+    bf16_t *__restrict__ kc, bf16_t *__restrict__ vc, int64_t kc_p, int64_t kc_h,
+    int64_t kc_s, int64_t kc_d, int64_t vc_p, int64_t vc_h, int64_t vc_s,
+    int64_t vc_d, const bf16_t *__restrict__ k, const bf16_t *__restrict__ v,
+    int64_t k_h, int64_t k_t, int64_t k_d, int64_t v_h, int64_t v_t, int64_t v_d,
+    const int32_t *__restrict__ bt, int64_t bt_b, const int32_t *__restrict__ cu,
+    int D) {
+  const int lp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int start = cu[b];
+  const int n = cu[b + 1] - start;
+  const int t0 = lp * kPage;
+  if (t0 >= n) return;
+  const int rows = min(kPage, n - t0);
+  const int64_t phys = int64_t(bt[b * bt_b + lp]);
+  bf16_t *kdst = kc + phys * kc_p + h * kc_h;
+  bf16_t *vdst = vc + phys * vc_p + h * vc_h;
+  const int64_t tok0 = int64_t(start) + t0;
+  const bf16_t *ksrc = k + h * k_h + tok0 * k_t;
+  const bf16_t *vsrc = v + h * v_h + tok0 * v_t;
+  if constexpr (kVec) {
+    const int cpr = D / 8;  // 16-byte chunks per row
+    const int total = rows * cpr;
+    for (int i = threadIdx.x; i < 2 * total; i += 256) {
+      const bool is_v = i >= total;
+      const int j = is_v ? i - total : i;
+      const int r = j / cpr, c = (j - r * cpr) * 8;
+      if (!is_v)
+        st16(kdst + r * kc_s + c, ld16(ksrc + r * k_t + c));
+      else
+        st16(vdst + r * vc_s + c, ld16(vsrc + r * v_t + c));
+    }
+  } else {
+    const int total = rows * D;
+    for (int i = threadIdx.x; i < total; i += 256) {
+      const int r = i / D, d = i - r * D;
+      kdst[r * kc_s + d * kc_d] = ksrc[r * k_t + d * k_d];
+      vdst[r * vc_s + d * vc_d] = vsrc[r * v_t + d * v_d];
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int wy_paged_kv_append(void *k_cache, void *v_cache, const int64_t *kcs,
+                                  const int64_t *vcs, const void *k_new,
+                                  const void *v_new, const int64_t *kns,
+                                  const int64_t *vns, const int32_t *block_table,
+                                  int64_t bt_stride0, const int64_t *pos, int batch,
+                                  int num_kv_heads, int head_dim, void *stream) {
+  if (!k_cache || !v_cache || !kcs || !vcs || !k_new || !v_new || !kns || !vns ||
+      !block_table || !pos)
+    return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || head_dim <= 0) return WY_E_SHAPE;
+  if (batch == 0) return WY_OK;
+  const bool vec = head_dim % 8 == 0 && kcs[3] == 1 && vcs[3] == 1 && kns[2] == 1 &&
+                   vns[2] == 1 && kcs[0] % 8 == 0 && kcs[1] % 8 == 0 &&
+                   kcs[2] % 8 == 0 && vcs[0] % 8 == 0 && vcs[1] % 8 == 0 &&
+                   vcs[2] % 8 == 0 && kns[0] % 8 == 0 && kns[1] % 8 == 0 &&
+                   vns[0] % 8 == 0 && vns[1] % 8 == 0 && wyh::aligned16(k_cache) &&
+                   wyh::aligned16(v_cache) && wyh::aligned16(k_new) &&
+                   wyh::aligned16(v_new);
+  dim3 grid(batch, num_kv_heads);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define WY_APPEND_ARGS                                                            \
+  static_cast<bf16_t *>(k_cache), static_cast<bf16_t *>(v_cache), kcs[0], kcs[1], \
+      kcs[2], kcs[3], vcs[0], vcs[1], vcs[2], vcs[3],                             \
+      static_cast<const bf16_t *>(k_new), static_cast<const bf16_t *>(v_new),     \
+      kns[0], kns[1], kns[2], vns[0], vns[1], vns[2], block_table, bt_stride0, pos, \
+      head_dim
+  if (vec)
+    paged_kv_append_kernel<true><<<grid, 64, 0, s>>>(WY_APPEND_ARGS);
+  else
+    paged_kv_append_kernel<false><<<grid, 64, 0, s>>>(WY_APPEND_ARGS);
+#undef WY_APPEND_ARGS
+  return wyh::launch_status();
+}
+
+extern "C" int wy_paged_kv_fill_varlen(void *k_cache, void *v_cache,
+                                       const int64_t *kcs, const int64_t *vcs,
+                                       const void *k_packed, const void *v_packed,
+                                       const int64_t *ks, const int64_t *vs,
+                                       const int32_t *block_table,
+                                       int64_t bt_stride0, const int32_t *cu_seqlens,
+                                       int batch, int num_kv_heads, int head_dim,
+                                       int max_seqlen, void *stream) {
+  if (!k_cache || !v_cache || !kcs || !vcs || !k_packed || !v_packed || !ks || !vs ||
+      !block_table || !cu_seqlens)
+    return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen < 0)
+    return WY_E_SHAPE;
+  if (batch == 0 || max_seqlen == 0) return WY_OK;
+  const bool vec = head_dim % 8 == 0 && kcs[3] == 1 && vcs[3] == 1 && ks[2] == 1 &&
+                   vs[2] == 1 && kcs[0] % 8 == 0 && kcs[1] % 8 == 0 &&
+                   kcs[2] % 8 == 0 && vcs[0] % 8 == 0 && vcs[1] % 8 == 0 &&
+                   vcs[2] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
+                   vs[0] % 8 == 0 && vs[1] % 8 == 0 && wyh::aligned16(k_cache) &&
+                   wyh::aligned16(v_cache) && wyh::aligned16(k_packed) &&
+                   wyh::aligned16(v_packed);
+  dim3 grid((max_seqlen + kPage - 1) / kPage, num_kv_heads, batch);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define WY_FILL_ARGS                                                              \
+  static_cast<bf16_t *>(k_cache), static_cast<bf16_t *>(v_cache), kcs[0], kcs[1], \
+      kcs[2], kcs[3], vcs[0], vcs[1], vcs[2], vcs[3],                             \
+      static_cast<const bf16_t *>(k_packed), static_cast<const bf16_t *>(v_packed), \
+      ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], block_table, bt_stride0,          \
+      cu_seqlens, head_dim
+  if (vec)
+    paged_kv_fill_varlen_kernel<true><<<grid, 256, 0, s>>>(WY_FILL_ARGS);
+  else
+    paged_kv_fill_varlen_kernel<false><<<grid, 256, 0, s>>>(WY_FILL_ARGS);
+#undef WY_FILL_ARGS
+  return wyh::launch_status();
+}

@@ -1,0 +1,325 @@
+"""Paged KV cache + split-K GQA decode attention on MI355X HIP kernels.
+
+Drop-in for ``triton_kernels/gqa_attention_decode_paged.py`` of the reference
+engine: same ``wy_lib::`` op names, schemas, argument meaning and assertions,
+same module-level names (``PAGE_SIZE``, ``MAX_SPLITS``, allocators,
+``physical_rows``, ``paged_kv_fill``, ``call_paged_gqa_attention_decode_triton``).
+
+Layout (unchanged from the reference, gqa_attention_decode_paged.py:29-36)::
+
+    k_cache / v_cache   [num_pages, H_kv, 16, D]  bf16, one pool shared by all sequences
+    block_table         [B, max_pages]            int32, logical -> physical page
+    pos                 [B]                       int64, tokens already cached
+    q / k_new / v_new   [B, H, D]                 bf16
+
+Split partition.  The reference splits every sequence into
+``ceil(npg / ceil(npg/128))`` page-aligned chunks.  The HIP pair here uses
+``pps = max(ceil(npg/128), MIN_PAGES_PER_SPLIT)`` pages per split in both the
+split and the combine op, so short contexts do not write one 4 KiB fp32
+partial per 16-token page.  The scratch tensors keep the reference shapes;
+their contents are a private contract between the two ops.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+PAGE_SIZE = 16
+MAX_SPLITS = 128
+
+# Lower bound on pages per split shared by split and combine (see module doc).
+MIN_PAGES_PER_SPLIT = 4
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+# --------------------------------------------------------------------------- allocation
+
+def allocate_paged_kv_cache(
+    num_pages: int,
+    num_kv_heads: int,
+    head_dim: int,
+    *,
+    device: torch.device | str = "cuda",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Zeroed ``[num_pages, H_kv, PAGE, D]`` bf16 K and V pools
+    (reference gqa_attention_decode_paged.py:100-111)."""
+    shape = (num_pages, num_kv_heads, PAGE_SIZE, head_dim)
+    k = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+    v = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+    return k, v
+
+
+def allocate_split_scratch(
+    num_q_heads: int,
+    head_dim: int,
+    *,
+    batch: int = 1,
+    device: torch.device | str = "cuda",
+):
+    """Split-K workspace shared by all attention layers: m, l ``[B, H_q, 128]``
+    and acc ``[B, H_q, 128, D]`` fp32 (reference :591-609)."""
+    m = torch.zeros((batch, num_q_heads, MAX_SPLITS), dtype=torch.float32, device=device)
+    l = torch.zeros((batch, num_q_heads, MAX_SPLITS), dtype=torch.float32, device=device)
+    acc = torch.zeros(
+        (batch, num_q_heads, MAX_SPLITS, head_dim), dtype=torch.float32, device=device
+    )
+    return m, l, acc
+
+
+def physical_rows(
+    block_table: torch.Tensor,
+    token_index: torch.Tensor,
+    num_kv_heads: int,
+) -> torch.Tensor:
+    """Logical token index -> row of ``k_cache.view(-1, D)``, shape ``[T, H]``:
+    ``row(t, h) = (block_table[t // 16] * H + h) * 16 + t % 16``
+    (reference :127-144, engine/paging.py:23).  Index arithmetic only; the
+    HIP kernels compute the same address from the pool strides."""
+    logical_page = token_index // PAGE_SIZE
+    slot = token_index % PAGE_SIZE
+    phys = block_table.index_select(0, logical_page.to(torch.int32)).to(torch.int64)
+    heads = torch.arange(num_kv_heads, device=block_table.device, dtype=torch.int64)
+    return (phys[:, None] * num_kv_heads + heads[None, :]) * PAGE_SIZE + slot[:, None]
+
+
+# --------------------------------------------------------------------------- append
+
+@torch.library.custom_op(
+    "wy_lib::paged_kv_append", mutates_args=("k_cache", "v_cache"), device_types="cuda"
+)
+def paged_kv_append(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    block_table: torch.Tensor,
+    pos: torch.Tensor,
+) -> None:
+    """Write the new token's K/V at slot ``pos[b]`` of sequence b's page
+    (reference :254-305).  Bit-exact copy, one launch for K and V."""
+    batch, num_kv_heads, head_dim = k_new.shape
+    assert k_cache.shape[1] == num_kv_heads and k_cache.shape[3] == head_dim
+    assert k_cache.shape[2] == PAGE_SIZE
+    assert v_cache.shape == k_cache.shape
+    assert k_new.shape == v_new.shape
+    assert k_cache.dtype == v_cache.dtype == torch.bfloat16
+    assert k_new.dtype == v_new.dtype == torch.bfloat16
+    assert block_table.dtype == torch.int32 and block_table.shape[0] == batch
+    assert pos.dtype == torch.int64 and pos.shape == (batch,)
+    assert head_dim & (head_dim - 1) == 0
+    assert block_table.stride(1) == 1 and pos.is_contiguous()
+    _lib.call(
+        "wy_paged_kv_append",
+        _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.strides(k_cache), _lib.strides(v_cache),
+        _lib.ptr(k_new), _lib.ptr(v_new), _lib.strides(k_new), _lib.strides(v_new),
+        _lib.ptr(block_table), block_table.stride(0), _lib.ptr(pos),
+        batch, num_kv_heads, head_dim, _lib.stream(k_cache.device),
+    )
+
+
+@paged_kv_append.register_fake
+def _paged_kv_append_fake(k_cache, v_cache, k_new, v_new, block_table, pos) -> None:
+    return None
+
+
+# ---------------------------------------------------------------------- varlen fill
+
+@torch.library.custom_op(
+    "wy_lib::paged_kv_fill_varlen", mutates_args=("k_cache", "v_cache"), device_types="cuda"
+)
+def paged_kv_fill_varlen(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_packed: torch.Tensor,
+    v_packed: torch.Tensor,
+    block_table: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: int,
+) -> None:
+    """Scatter packed ``[H_kv, total, D]`` K/V (any strides) into each
+    sequence's pages in one launch (reference :492-561).  Bit-exact; slots
+    past a sequence's end and unreferenced pages stay untouched."""
+    num_kv_heads, total_tokens, head_dim = k_packed.shape
+    assert v_packed.shape == k_packed.shape
+    assert k_cache.shape[1] == num_kv_heads and k_cache.shape[3] == head_dim
+    assert k_cache.shape[2] == PAGE_SIZE
+    assert v_cache.shape == k_cache.shape
+    assert k_cache.dtype == v_cache.dtype == torch.bfloat16
+    assert k_packed.dtype == v_packed.dtype == torch.bfloat16
+    assert block_table.dtype == torch.int32 and block_table.ndim == 2
+    assert cu_seqlens.dtype == torch.int32 and cu_seqlens.ndim == 1
+    batch = cu_seqlens.shape[0] - 1
+    assert block_table.shape[0] == batch, (
+        f"block_table has {block_table.shape[0]} rows but cu_seqlens describes {batch} sequences"
+    )
+    assert block_table.shape[1] >= _cdiv(max_seqlen, PAGE_SIZE), (
+        f"block_table rows hold {block_table.shape[1]} pages, too few for {max_seqlen} tokens"
+    )
+    assert head_dim & (head_dim - 1) == 0
+    assert block_table.stride(1) == 1 and cu_seqlens.is_contiguous()
+    _lib.call(
+        "wy_paged_kv_fill_varlen",
+        _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.strides(k_cache), _lib.strides(v_cache),
+        _lib.ptr(k_packed), _lib.ptr(v_packed), _lib.strides(k_packed),
+        _lib.strides(v_packed), _lib.ptr(block_table), block_table.stride(0),
+        _lib.ptr(cu_seqlens), batch, num_kv_heads, head_dim, max_seqlen,
+        _lib.stream(k_cache.device),
+    )
+
+
+@paged_kv_fill_varlen.register_fake
+def _paged_kv_fill_varlen_fake(
+    k_cache, v_cache, k_packed, v_packed, block_table, cu_seqlens, max_seqlen
+) -> None:
+    return None
+
+
+def paged_kv_fill(
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_prefill: torch.Tensor,
+    v_prefill: torch.Tensor,
+    block_table: torch.Tensor,
+) -> None:
+    """Single-sequence prefill scatter of ``[H, T, D]`` K/V through one
+    block-table row (reference :355-375).  Runs the varlen HIP kernel with
+    ``cu_seqlens = [0, T]``."""
+    num_kv_heads, token_num, head_dim = k_prefill.shape
+    assert v_prefill.shape == k_prefill.shape
+    bt = block_table.reshape(1, -1)
+    cu = torch.tensor([0, token_num], dtype=torch.int32, device=k_cache.device)
+    paged_kv_fill_varlen(k_cache, v_cache, k_prefill, v_prefill, bt, cu, token_num)
+
+
+# --------------------------------------------------------------------------- split
+
+@torch.library.custom_op(
+    "wy_lib::paged_gqa_attention_decode_split",
+    mutates_args=("m_partial", "l_partial", "acc_partial"),
+    device_types="cuda",
+)
+def paged_gqa_attention_decode_split(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    m_partial: torch.Tensor,
+    l_partial: torch.Tensor,
+    acc_partial: torch.Tensor,
+    pos: torch.Tensor,
+    seq_bucket: int,
+) -> None:
+    """Partial pass of split-K paged decode (reference :822-891).  Grid is a
+    function of shapes only; ``pos``/``block_table`` are read on the device,
+    so the op is graph-capturable.  ``seq_bucket`` was an autotune key in the
+    reference and is accepted and ignored."""
+    batch, num_q_heads, head_dim = q.shape
+    num_pages, num_kv_heads, page, cache_dim = k_cache.shape
+    assert page == PAGE_SIZE and cache_dim == head_dim
+    assert v_cache.shape == k_cache.shape
+    assert q.dtype == torch.bfloat16 and k_cache.dtype == torch.bfloat16
+    assert block_table.dtype == torch.int32 and block_table.shape[0] == batch
+    assert m_partial.shape == (batch, num_q_heads, MAX_SPLITS)
+    assert acc_partial.shape == (batch, num_q_heads, MAX_SPLITS, head_dim)
+    assert pos.dtype == torch.int64 and pos.shape == (batch,)
+    assert num_q_heads % num_kv_heads == 0
+    assert l_partial.shape == m_partial.shape and l_partial.stride() == m_partial.stride()
+    assert m_partial.dtype == l_partial.dtype == acc_partial.dtype == torch.float32
+    assert block_table.stride(1) == 1 and pos.is_contiguous()
+    _lib.call(
+        "wy_paged_decode_split",
+        _lib.ptr(q), _lib.strides(q), _lib.ptr(k_cache), _lib.ptr(v_cache),
+        _lib.strides(k_cache), _lib.strides(v_cache), _lib.ptr(block_table),
+        block_table.stride(0), _lib.ptr(pos), _lib.ptr(m_partial), _lib.ptr(l_partial),
+        _lib.ptr(acc_partial), _lib.strides(m_partial), _lib.strides(acc_partial),
+        batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
+        MIN_PAGES_PER_SPLIT, _lib.stream(q.device),
+    )
+
+
+@paged_gqa_attention_decode_split.register_fake
+def _paged_split_fake(
+    q, k_cache, v_cache, block_table, m_partial, l_partial, acc_partial, pos, seq_bucket
+) -> None:
+    return None
+
+
+@torch.library.custom_op(
+    "wy_lib::paged_gqa_attention_decode_combine", mutates_args=(), device_types="cuda"
+)
+def paged_gqa_attention_decode_combine(
+    m_partial: torch.Tensor,
+    l_partial: torch.Tensor,
+    acc_partial: torch.Tensor,
+    pos: torch.Tensor,
+) -> torch.Tensor:
+    """Merge the active splits into ``[B, H_q, D]`` bf16 (reference :901-939)."""
+    batch, num_q_heads, _, head_dim = acc_partial.shape
+    assert l_partial.stride() == m_partial.stride()
+    assert pos.dtype == torch.int64 and pos.shape == (batch,) and pos.is_contiguous()
+    out = torch.empty(
+        (batch, num_q_heads, head_dim), dtype=torch.bfloat16, device=acc_partial.device
+    )
+    _lib.call(
+        "wy_paged_decode_combine",
+        _lib.ptr(m_partial), _lib.ptr(l_partial), _lib.ptr(acc_partial),
+        _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(pos), _lib.ptr(out),
+        _lib.strides(out), batch, num_q_heads, head_dim, MIN_PAGES_PER_SPLIT,
+        _lib.stream(acc_partial.device),
+    )
+    return out
+
+
+@paged_gqa_attention_decode_combine.register_fake
+def _paged_combine_fake(m_partial, l_partial, acc_partial, pos) -> torch.Tensor:
+    batch, num_q_heads, _, head_dim = acc_partial.shape
+    return torch.empty(
+        (batch, num_q_heads, head_dim), dtype=torch.bfloat16, device=acc_partial.device
+    )
+
+
+def _seq_bucket(seq_len: int) -> int:
+    """Kept for interface parity with the reference (:950); the HIP kernels
+    have fixed launch configurations, so the bucket selects nothing."""
+    if seq_len <= 64:
+        return 64
+    if seq_len <= 256:
+        return 256
+    if seq_len <= 1024:
+        return 1024
+    if seq_len <= 4096:
+        return 4096
+    return 4097
+
+
+def call_paged_gqa_attention_decode_triton(
+    q: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    pos: torch.Tensor,
+    scratch: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+) -> torch.Tensor:
+    """Append + split + combine; returns ``[B, H_q, D]`` bf16 (reference
+    :963-994).  The name is kept so callers switch by import only."""
+    if scratch is None:
+        scratch = allocate_split_scratch(
+            q.shape[1], q.shape[2], batch=q.shape[0], device=q.device
+        )
+    m_partial, l_partial, acc_partial = scratch
+    paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, pos)
+    hint = k_cache.shape[0] * PAGE_SIZE
+    paged_gqa_attention_decode_split(
+        q, k_cache, v_cache, block_table, m_partial, l_partial, acc_partial, pos, hint
+    )
+    return paged_gqa_attention_decode_combine(m_partial, l_partial, acc_partial, pos)
+
+
+paged_gqa_attention_decode = call_paged_gqa_attention_decode_triton

@@ -1,0 +1,174 @@
+"""CPU-side checks: the C-ABI library loads and exports every entry point of
+include/wy_attn.h, argument rejection happens before any device work, host
+paging logic, fixture integrity.  No kernel runs here."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_oracle as orc
+from tests.golden import cases as C
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "wy_attn.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(wy_\w+)\(", text, re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    assert "wy_paged_decode_split" in names and "wy_varlen_causal_prefill" in names
+    assert len(names) >= 9
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_declared()) == set(pkg._lib.EXPORTED)
+    assert lib.wy_build_info().decode().endswith("gfx950")
+
+
+def test_null_and_unsupported_arguments_are_rejected(pkg):
+    lib = pkg._lib.load()
+    s4 = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    s3 = (ctypes.c_int64 * 3)(1, 1, 1)
+    rc = lib.wy_paged_kv_append(None, None, s4, s4, None, None, s3, s3, None, 0, None,
+                                1, 2, 256, None)
+    assert rc == -1
+    assert "NULL" in lib.wy_status_string(rc).decode()
+    dummy = ctypes.c_void_p(16)
+    # head_dim 128 has no decode kernel: rejected before launch
+    rc = lib.wy_paged_decode_split(dummy, s3, dummy, dummy, s4, s4, dummy, 1, dummy, dummy,
+                                   dummy, dummy, s3, s4, 1, 8, 2, 128, 4, 4, None)
+    assert rc == -4
+    rc = lib.wy_varlen_causal_prefill(dummy, s3, dummy, s3, dummy, s3, dummy, s3, dummy,
+                                      1, 8, 2, 64, 16, None)
+    assert rc == -4
+    rc = lib.wy_partial_rope(dummy, s4, dummy, s4, dummy, (ctypes.c_int64 * 2)(1, 1), 0,
+                             dummy, 1, 1, 1, 256, 65, None)
+    assert rc == -2  # odd rotary_dim
+
+
+def test_ops_refuse_cpu_tensors(pkg):
+    x = torch.zeros(1, 2, 3, 256, dtype=torch.bfloat16)
+    with pytest.raises(Exception):
+        pkg.attention_gate_pack(x, x)
+    with pytest.raises(Exception):
+        pkg.partial_rope(x, torch.zeros(1, 3, dtype=torch.int64), torch.zeros(32), 64)
+
+
+def test_op_schemas_match_reference():
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    schemas = {
+        "paged_kv_append": "(Tensor(a0!) k_cache, Tensor(a1!) v_cache, Tensor k_new, "
+                           "Tensor v_new, Tensor block_table, Tensor pos) -> ()",
+        "gqa_attention_varlen_causal": "(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, "
+                                       "SymInt max_seqlen) -> Tensor",
+        "attention_gate_pack": "(Tensor x, Tensor gate) -> Tensor",
+    }
+    for name, sig in schemas.items():
+        op = getattr(torch.ops.wy_lib, name).default
+        s = str(op._schema)
+        assert s.startswith(f"wy_lib::{name}"), s
+        args = s[len(f"wy_lib::{name}"):]
+        assert args.replace("SymInt", "int") == sig.replace("SymInt", "int"), s
+    for name in ("paged_kv_fill_varlen", "paged_gqa_attention_decode_split",
+                 "paged_gqa_attention_decode_combine", "partial_rope"):
+        assert hasattr(torch.ops.wy_lib, name)
+
+
+def test_fake_impls_give_reference_shapes(pkg):
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty(1, 8, 5, 256, dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.wy_lib.attention_gate_pack(x, x).shape == (5, 2048)
+        acc = torch.empty(3, 8, 128, 256, device="cuda")
+        m = torch.empty(3, 8, 128, device="cuda")
+        pos = torch.empty(3, dtype=torch.int64, device="cuda")
+        out = torch.ops.wy_lib.paged_gqa_attention_decode_combine(m, m, acc, pos)
+        assert out.shape == (3, 8, 256) and out.dtype == torch.bfloat16
+
+
+# ------------------------------------------------------------------ host paging
+
+def test_page_pool_and_sequence_pages(pkg):
+    pool = pkg.PagePool(10)
+    sp = pkg.SequencePages(4, batch=2, device="cpu")
+    sp.reserve(17, pool, seq=0)            # 2 pages from the tail: [8, 9]
+    assert sp.pages[0] == [8, 9] and sp.block_table[0, :2].tolist() == [8, 9]
+    sp.reserve(20, pool, seq=0)            # still 2 pages: no-op
+    assert pool.num_free == 8
+    sp.reserve(48, pool, seq=1)
+    assert sp.capacity(1) == 48 and pool.num_free == 5
+    with pytest.raises(AssertionError):
+        sp.reserve(16 * 5, pool, seq=1)    # beyond block-table capacity
+    sp.release(pool)
+    assert pool.num_free == 10 and int(sp.block_table.abs().sum()) == 0
+    with pytest.raises(AssertionError):
+        pool.alloc(11)
+
+
+def test_attn_caches_sizing(pkg):
+    c = pkg.allocate_attn_caches(2, 100, batch=3, device="cpu")
+    assert c.k_caches[0].shape == (3 * 8, 2, 16, 256)   # (ceil(100/16)+1) * 3 pages
+    assert c.split_scratch[2].shape == (3, 8, 128, 256)
+    c.reserve(100)
+    with pytest.raises(AssertionError):
+        c.reserve(101)
+    c.reset()
+    assert c.page_pool.num_free == 24
+
+
+def test_build_packed_batch(pkg):
+    pb = pkg.build_packed_batch([3, 6, 2], device="cpu")
+    assert pb.cu_seqlens.tolist() == [0, 3, 9, 11]
+    assert pb.position_ids.tolist() == [[0, 1, 2, 0, 1, 2, 3, 4, 5, 0, 1]]
+    assert pb.slice_of(1) == slice(3, 9) and pb.max_seqlen == 6
+
+
+# ------------------------------------------------------------------ fixtures
+
+def _golden():
+    return np.load(ROOT / "tests" / "golden" / "golden.npz", allow_pickle=False)
+
+
+def test_golden_inputs_regenerate_bit_identically():
+    g = _golden()
+    d = C.decode_case()
+    assert str(g["decode_inputs_sha"]) == C.digest(*d.values())
+    p = C.prefill_case()
+    assert str(g["prefill_inputs_sha"]) == C.digest(p["q"], p["k"], p["v"], p["cu"])
+    r = C.rope_case()
+    assert str(g["rope_inputs_sha"]) == C.digest(r["x"], r["pos"], r["inv_freq"])
+    gg = C.gate_case()
+    assert str(g["gate_inputs_sha"]) == C.digest(gg["x"], gg["gate"])
+    f = C.fill_case()
+    assert str(g["fill_inputs_sha"]) == C.digest(f["k"], f["v"], f["kc"], f["vc"], f["bt"], f["cu"])
+
+
+def test_oracle_reproduces_golden():
+    g = _golden()
+    d = C.decode_case()
+    kc, vc = d["kc"].clone(), d["vc"].clone()
+    orc.paged_kv_append(kc, vc, d["kn"], d["vn"], d["bt"], d["pos"])
+    assert str(g["decode_pool_after_sha"]) == C.digest(kc, vc)
+    np.testing.assert_allclose(orc.paged_decode(d["q"], kc, vc, d["bt"], d["pos"] + 1).numpy(),
+                               g["decode_out"], rtol=1e-5, atol=1e-5)
+    p = C.prefill_case()
+    np.testing.assert_allclose(orc.varlen_causal(p["q"], p["k"], p["v"], p["cu"]).numpy(),
+                               g["prefill_out"], rtol=1e-5, atol=1e-5)
+    f = C.fill_case()
+    kc, vc = f["kc"].clone(), f["vc"].clone()
+    orc.paged_kv_fill_varlen(kc, vc, f["k"], f["v"], f["bt"], f["cu"])
+    assert str(g["fill_pool_after_sha"]) == C.digest(kc, vc)
