@@ -154,6 +154,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
+    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-split", "pmc-copy"],
+                    help="pmc-*: eager launches only, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the attention path "
@@ -180,9 +182,9 @@ def main():
         return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w["gate"])
 
     log(f"decode config2: sum(L)={sum(lens)} B=32")
-    ms = time_graph(step, args.steps, args.warmup)
+    ms = time_graph(step, args.steps, args.warmup) if args.mode == "bench" else 0.0
     step_bytes = decode_bytes(lens)
-    gbs = step_bytes / (ms * 1e-3) / 1e9
+    gbs = step_bytes / (ms * 1e-3) / 1e9 if ms else 0.0
 
     # dominant kernel alone: split partial pass, events over a graph of launches
     m_p, l_p, acc_p = scratch
@@ -190,6 +192,21 @@ def main():
     def split_only():
         torch.ops.wy_lib.paged_gqa_attention_decode_split(
             w["q"], w["kc"], w["vc"], w["bt"], m_p, l_p, acc_p, w["pos"], 0)
+
+    if args.mode == "pmc-split":
+        for _ in range(10):
+            split_only()
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "pmc-split", "algorithmic_bytes": split_kernel_bytes(lens)}))
+        return
+    if args.mode == "pmc-copy":
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "pmc-copy", "bytes_read": 256 << 20, "bytes_written": 256 << 20}))
+        return
 
     split_ms = time_graph_events(split_only, 100)
     sbytes = split_kernel_bytes(lens)
