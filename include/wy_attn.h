@@ -112,6 +112,35 @@ int wy_paged_decode_combine(const float *m_partial, const float *l_partial,
                             int min_pages_per_split, void *stream);
 
 /*
+ * Whole decode step in one launch: K/V append + split-K partial + merge
+ * (+ optional sigmoid gate).  The new token's K/V rows are taken from
+ * k_new/v_new [B, H_kv, D] and written to their page by the workgroup that
+ * owns that page; the last workgroup of each (b, kv head) to finish merges
+ * the splits (counters [B*H_kv] int32 must be zero before the first call and
+ * are left zero by every call).  gate (may be NULL) [B, H_q, D] with strides
+ * gate_strides: out = bf16(bf16(ctx) * sigmoid(gate)), the rounding of the
+ * reference's combine followed by its gate pack.  out [B, H_q, D] bf16.
+ * Concurrent calls sharing one counters/scratch set race.
+ * Replaces the sequence paged_kv_append -> paged_gqa_attention_decode_split
+ * -> paged_gqa_attention_decode_combine (-> attention_gate_pack) of
+ *   call_paged_gqa_attention_decode_triton
+ *   (triton_kernels/gqa_attention_decode_paged.py:963-994) and
+ *   engine/runner.py:508-517.
+ */
+int wy_paged_decode_step(const void *q, const int64_t *q_strides, const void *k_new,
+                         const void *v_new, const int64_t *kn_strides,
+                         const int64_t *vn_strides, void *k_cache, void *v_cache,
+                         const int64_t *kc_strides, const int64_t *vc_strides,
+                         const int32_t *block_table, int64_t bt_stride0,
+                         const int64_t *pos, float *m_partial, float *l_partial,
+                         float *acc_partial, const int64_t *ml_strides,
+                         const int64_t *acc_strides, int32_t *counters,
+                         const void *gate, const int64_t *gate_strides, void *out,
+                         const int64_t *out_strides, int batch, int num_q_heads,
+                         int num_kv_heads, int head_dim, int max_pages,
+                         int min_pages_per_split, void *stream);
+
+/*
  * Packed varlen causal GQA prefill attention on bf16 MFMA.
  *   out[t, hq, :] = softmax_{j<=i}(q_i . k_j / sqrt(D)) V  within each sequence
  * q/out [total, H_q, D], k/v [total, H_kv, D] bf16 (innermost stride must be

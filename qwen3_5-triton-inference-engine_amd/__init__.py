@@ -26,7 +26,9 @@ from .gqa_attention_decode_paged import (
     allocate_paged_kv_cache,
     allocate_split_scratch,
     call_paged_gqa_attention_decode_triton,
+    SplitScratch,
     paged_gqa_attention_decode_combine,
+    paged_gqa_attention_decode_fused,
     paged_gqa_attention_decode_split,
     paged_kv_append,
     paged_kv_fill,

@@ -31,6 +31,9 @@ _SIGNATURES = {
                               _vp],
     "wy_paged_decode_combine": [_vp, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _i,
                                 _i, _i, _i, _vp],
+    "wy_paged_decode_step": [_vp, _c_i64p, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p,
+                             _c_i64p, _vp, _i64, _vp, _vp, _vp, _vp, _c_i64p, _c_i64p, _vp,
+                             _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _i, _i, _i, _vp],
     "wy_varlen_causal_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
                                  _vp, _i, _i, _i, _i, _i, _vp],
     "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,
@@ -66,13 +69,15 @@ def load() -> ctypes.CDLL:
     return lib
 
 
-def strides(t: torch.Tensor):
+def strides(t):
+    if t is None:
+        return None
     s = t.stride()
     return (ctypes.c_int64 * len(s))(*s)
 
 
-def ptr(t: torch.Tensor) -> int:
-    return t.data_ptr()
+def ptr(t):
+    return None if t is None else t.data_ptr()
 
 
 def stream(device: torch.device) -> int:

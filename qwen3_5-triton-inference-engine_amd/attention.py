@@ -24,6 +24,7 @@ import torch
 from .attention_gate_pack import attention_gate_pack
 from .gqa_attention_decode_paged import (
     call_paged_gqa_attention_decode_triton,
+    paged_gqa_attention_decode_fused,
     paged_kv_fill_varlen,
 )
 from .gqa_attention_varlen_causal import gqa_attention_varlen_causal
@@ -144,6 +145,14 @@ def decode_attention_step(
     q_new = q4[:, :, 0, :].contiguous()
     k_new = k4[:, :, 0, :].contiguous()
     v_new = v.reshape(batch, nkv, d).contiguous()
+    counters = getattr(scratch, "counters", None)
+    if counters is not None:
+        # one launch: append + split + merge + gate
+        m, l, acc = scratch
+        out = paged_gqa_attention_decode_fused(
+            q_new, k_new, v_new, k_cache, v_cache, block_table, pos, m, l, acc, counters,
+            gate.view(batch, nh, d))
+        return out.view(batch, nh * d)
     ctx = call_paged_gqa_attention_decode_triton(
         q_new, k_new, v_new, k_cache, v_cache, block_table, pos, scratch
     )

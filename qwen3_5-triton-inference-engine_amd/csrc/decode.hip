@@ -36,6 +36,29 @@ constexpr int kD = 256;   // head_dim
 constexpr int kG = 4;     // query heads per KV head
 constexpr int kWaves = 4; // wavefronts per workgroup
 
+struct DecodeArgs {
+  const bf16_t *q;
+  int64_t qs_b, qs_h, qs_d;
+  bf16_t *kc, *vc;  // written only by the fused kernel (new token's row)
+  int64_t kc_p, kc_h, kc_s, vc_p, vc_h, vc_s;
+  const int32_t *bt;
+  int64_t bt_b;
+  const int64_t *pos;
+  float *mp, *lp, *ap;
+  int64_t ml_b, ml_h, ml_s, a_b, a_h, a_s;
+  float scale;
+  int min_pps;
+  int hkv;
+  // fused step only
+  const bf16_t *kn, *vn;
+  int64_t kn_b, kn_h, vn_b, vn_h;
+  int32_t *counters;  // [B * H_kv], zero between launches (self-resetting)
+  const bf16_t *gate; // optional sigmoid gate [B, H_q, D]
+  int64_t g_b, g_h, g_d;
+  bf16_t *out;        // [B, H_q, D]
+  int64_t o_b, o_h, o_d;
+};
+
 __device__ __forceinline__ int split_pps(int npg, int min_pps) {
   const int p = (npg + kMaxSplits - 1) / kMaxSplits;
   return p > min_pps ? p : min_pps;
@@ -45,7 +68,7 @@ __device__ __forceinline__ float readlane0(float v) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
-// Max / sum over the 16 lanes of each row of 16 (lanes 0..15 hold the scores).
+// Max / sum over each row of 16 lanes (lanes 0..15 hold the scores).
 __device__ __forceinline__ float max16(float v) {
   v = fmaxf(v, __shfl_xor(v, 1));
   v = fmaxf(v, __shfl_xor(v, 2));
@@ -61,106 +84,179 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
-struct PageRegs {
-  u32x4_t k[8];  // MFMA B operand, one per 32-dim step
-  u32x4_t v[8];  // row-contiguous V, tokens 2i + lane/32
-};
+__device__ __forceinline__ float sigmoidf(float g) { return 1.0f / (1.0f + __expf(-g)); }
 
-__device__ __forceinline__ void load_page(PageRegs &r, const bf16_t *kbase,
-                                          const bf16_t *vbase, int64_t kc_s,
-                                          int64_t vc_s, int lane) {
-  const bf16_t *kp = kbase + (lane & 15) * kc_s + (lane >> 4) * 8;
+// ctx = bf16(A / L), then optionally bf16(ctx * sigmoid(gate)): the same two
+// roundings as the reference's combine kernel followed by its gate pack.
+__device__ __forceinline__ void store_out4(const DecodeArgs &a, int b, int hq, int d,
+                                           float4 A, float L) {
+  float o[4] = {round_bf16(A.x / L), round_bf16(A.y / L), round_bf16(A.z / L),
+                round_bf16(A.w / L)};
+  if (a.gate) {
+    const bf16_t *g = a.gate + b * a.g_b + hq * a.g_h;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r.k[i] = ld16(kp + 32 * i);
-  const bf16_t *vp = vbase + (lane >> 5) * vc_s + (lane & 31) * 8;
+    for (int e = 0; e < 4; ++e) o[e] = o[e] * sigmoidf(bf16_to_f32(g[(d + e) * a.g_d]));
+  }
+  bf16_t *orow = a.out + b * a.o_b + hq * a.o_h;
+  if (a.o_d == 1) {
+    const u32x2_t w = {pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+    *reinterpret_cast<u32x2_t *>(orow + d) = w;
+  } else {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r.v[i] = ld16(vp + 2 * i * vc_s);
+    for (int e = 0; e < 4; ++e) orow[(d + e) * a.o_d] = bf16_t(f32_to_bf16_bits(o[e]));
+  }
 }
 
-__global__ __launch_bounds__(256) void paged_decode_split_kernel(
-    const bf16_t *__restrict__ q, int64_t qs_b, int64_t qs_h, int64_t qs_d,
-    const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vc, int64_t kc_p,
-    int64_t kc_h, int64_t kc_s, int64_t vc_p, int64_t vc_h, int64_t vc_s,
-    const int32_t *__restrict__ bt, int64_t bt_b, const int64_t *__restrict__ pos,
-    float *__restrict__ mp, float *__restrict__ lp, float *__restrict__ ap,
-    int64_t ml_b, int64_t ml_h, int64_t ml_s, int64_t a_b, int64_t a_h, int64_t a_s,
-    float scale, int min_pps) {
-  __shared__ float4 sm_p[kWaves][kPage];          // bf16-rounded P, [token][head]
-  __shared__ float sm_ml[kWaves][2][kG];          // per-wave m, l
-  __shared__ float4 sm_acc[kWaves][kG][kD / 4];   // per-wave unnormalised acc
+// Merge the nact split states of (b, hq) with one wavefront; lane owns dims
+// 4*lane..4*lane+3.  Shared by the combine kernel and the fused step.
+__device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lane) {
+  const float *mrow = a.mp + b * a.ml_b + hq * a.ml_h;
+  const float *lrow = a.lp + b * a.ml_b + hq * a.ml_h;
+  const float *arow = a.ap + b * a.a_b + hq * a.a_h + lane * 4;
+  float mx = -INFINITY;
+  for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, mrow[s * a.ml_s]);
+  mx = wave_max(mx);
+  float L = 0.f;
+  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+  int s = 0;
+  for (; s + 4 <= nact; s += 4) {
+    float4 x[4];
+    float w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      x[u] = *reinterpret_cast<const float4 *>(arow + (s + u) * a.a_s);
+      w[u] = __expf(mrow[(s + u) * a.ml_s] - mx);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      L += w[u] * lrow[(s + u) * a.ml_s];
+      A.x += w[u] * x[u].x;
+      A.y += w[u] * x[u].y;
+      A.z += w[u] * x[u].z;
+      A.w += w[u] * x[u].w;
+    }
+  }
+  for (; s < nact; ++s) {
+    const float4 x = *reinterpret_cast<const float4 *>(arow + s * a.a_s);
+    const float w = __expf(mrow[s * a.ml_s] - mx);
+    L += w * lrow[s * a.ml_s];
+    A.x += w * x.x;
+    A.y += w * x.y;
+    A.z += w * x.z;
+    A.w += w * x.w;
+  }
+  store_out4(a, b, hq, lane * 4, A, L);
+}
+
+// Split partial pass.  kFused additionally (i) takes the new token's K/V
+// from k_new/v_new and writes them into their page (the append), and (ii)
+// lets the last workgroup of each (b, h) to finish merge all splits and write
+// the (optionally gated) output, so one launch is a whole decode step.
+template <bool kFused>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void paged_decode_split_kernel(const DecodeArgs a) {
+  __shared__ float4 sm_p[kWaves][kPage];         // bf16-rounded P, [token][head]
+  __shared__ float sm_ml[kWaves][2][kG];         // per-wave m, l
+  __shared__ float4 sm_acc[kWaves][kG][kD / 4];  // per-wave unnormalised acc
+  __shared__ int sm_last;
+  __shared__ __align__(16) bf16_t sm_q[kG][kD + 8];
 
   const int b = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
-  const int seq_len = int(pos[b]) + 1;
+  const int seq_len = int(a.pos[b]) + 1;
   const int npg = (seq_len + kPage - 1) / kPage;
-  const int pps = split_pps(npg, min_pps);
+  const int pps = split_pps(npg, a.min_pps);
   const int p0 = s * pps;
   if (p0 >= npg) return;  // inactive split: uniform over the workgroup
   const int p1 = min(p0 + pps, npg);
+  const int nact = (npg + pps - 1) / pps;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n16 = lane & 15, g4 = lane >> 4;
 
-  // q rows of the group as the MFMA A operand (rows 4..15 are zero).
-  bf16x8_t qa[8];
-  {
-    const int row = lane & 15, g = lane >> 4;
-    const bf16_t *qrow = q + b * qs_b + (h * kG + (row & 3)) * qs_h;
+  // The group's 4 query rows, staged once in LDS; each page rebuilds the MFMA
+  // A operand from it (rows 4..15 of the operand are zero).
+  if (threadIdx.x < kG * kD / 8) {
+    const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
+    const bf16_t *qrow = a.q + b * a.qs_b + (h * kG + r) * a.qs_h;
+    u32x4_t w;
+    if (a.qs_d == 1) {
+      w = ld16(qrow + c);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      u32x4_t w = {0u, 0u, 0u, 0u};
-      if (row < kG) {
-        const int d0 = 32 * i + 8 * g;
-        if (qs_d == 1) {
-          w = ld16(qrow + d0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            w[e] = uint32_t(qrow[(d0 + 2 * e) * qs_d]) |
-                   (uint32_t(qrow[(d0 + 2 * e + 1) * qs_d]) << 16);
-        }
-      }
-      qa[i] = __builtin_bit_cast(bf16x8_t, w);
+      for (int e = 0; e < 4; ++e)
+        w[e] = uint32_t(qrow[(c + 2 * e) * a.qs_d]) |
+               (uint32_t(qrow[(c + 2 * e + 1) * a.qs_d]) << 16);
     }
+    st16(&sm_q[r][c], w);
   }
+  __syncthreads();
 
-  float m_run[kG], l_run[kG], acc[kG][8];
+  float m_run[kG], l_run[kG], acc[kG][4];
 #pragma unroll
   for (int r = 0; r < kG; ++r) {
     m_run[r] = -INFINITY;
     l_run[r] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
+    for (int e = 0; e < 4; ++e) acc[r][e] = 0.f;
   }
 
-  const bf16_t *kh = kc + h * kc_h;
-  const bf16_t *vh = vc + h * vc_h;
-  const int32_t *btrow = bt + b * bt_b;
+  const bf16_t *kh = a.kc + h * a.kc_h;
+  const bf16_t *vh = a.vc + h * a.vc_h;
+  const int32_t *btrow = a.bt + b * a.bt_b;
+  const int last_page = (seq_len - 1) / kPage;
+  const int last_slot = (seq_len - 1) % kPage;
 
-  int p = p0 + wave;
-  PageRegs cur;
-  if (p < p1) {
+  for (int p = p0 + wave; p < p1; p += kWaves) {
     const int64_t phys = btrow[p];
-    load_page(cur, kh + phys * kc_p, vh + phys * vc_p, kc_s, vc_s, lane);
-  }
-  for (; p < p1; p += kWaves) {
-    PageRegs nxt;
-    const int pn = p + kWaves;
-    if (pn < p1) {
-      const int64_t physn = btrow[pn];
-      load_page(nxt, kh + physn * kc_p, vh + physn * vc_p, kc_s, vc_s, lane);
+    const bf16_t *kp = kh + phys * a.kc_p + n16 * a.kc_s + g4 * 8;
+    const bf16_t *vp = vh + phys * a.vc_p + lane * 4;
+    const bool new_page = kFused && p == last_page;
+    const bf16_t *knrow = nullptr, *vnrow = nullptr;
+    if constexpr (kFused) {
+      if (new_page) {
+        knrow = a.kn + b * a.kn_b + h * a.kn_h;
+        vnrow = a.vn + b * a.vn_b + h * a.vn_h;
+        if (n16 == last_slot) kp = knrow + g4 * 8;  // the new token's key row
+      }
+    }
+    u32x4_t kr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = ld16(kp + 32 * i);
+    u32x2_t vr[kPage];
+#pragma unroll
+    for (int i = 0; i < kPage; ++i) vr[i] = *reinterpret_cast<const u32x2_t *>(vp + i * a.vc_s);
+    // the new token's value row (the cached row at that slot is stale)
+    u32x2_t vnew = {0u, 0u};
+    if constexpr (kFused) {
+      if (new_page) vnew = *reinterpret_cast<const u32x2_t *>(vnrow + lane * 4);
+    }
+    if constexpr (kFused) {
+      if (new_page) {  // the append: one 512-byte row of K (lanes 0..31) and V (32..63)
+        const int c = (lane & 31) * 8;
+        if (lane < 32)
+          st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(knrow + c));
+        else
+          st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, ld16(vnrow + c));
+      }
     }
 
     // ---- scores: 4 heads x 16 tokens in lanes 0..15 ------------------------
     f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          qa[i], __builtin_bit_cast(bf16x8_t, cur.k[i]), sc, 0, 0, 0);
-    const bool valid = p * kPage + (lane & 15) < seq_len;
+    for (int i = 0; i < 8; ++i) {
+      const u32x4_t qw = n16 < kG ? ld16(&sm_q[n16 & 3][32 * i + 8 * g4])
+                                  : u32x4_t{0u, 0u, 0u, 0u};
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qw),
+                                                   __builtin_bit_cast(bf16x8_t, kr[i]), sc,
+                                                   0, 0, 0);
+    }
+    const int valid_rows = seq_len - p * kPage;  // >= 1
+    const bool valid = n16 < valid_rows;
     float pr[kG], alpha[kG];
 #pragma unroll
     for (int r = 0; r < kG; ++r) {
-      const float x = valid ? sc[r] * scale : -INFINITY;
+      const float x = valid ? sc[r] * a.scale : -INFINITY;
       const float mx = readlane0(max16(x));
       const float m_new = fmaxf(m_run[r], mx);
       alpha[r] = __expf(m_run[r] - m_new);
@@ -174,49 +270,43 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(
                                      round_bf16(pr[2]), round_bf16(pr[3]));
     __builtin_amdgcn_wave_barrier();
 
-    // Rows past the sequence end in the last page may hold anything (even NaN):
-    // zero them so 0 * garbage cannot reach the accumulator.
-    if ((p + 1) * kPage > seq_len) {
+    // Rows past the sequence end may hold anything (even NaN): zero them so
+    // 0 * garbage cannot reach the accumulator.
+    if (valid_rows < kPage) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (p * kPage + 2 * i + (lane >> 5) >= seq_len) cur.v[i] = u32x4_t{0u, 0u, 0u, 0u};
+      for (int i = 0; i < kPage; ++i)
+        if (i >= valid_rows) vr[i] = u32x2_t{0u, 0u};
     }
-    // ---- acc = acc * alpha + P V (lane: dims (lane%32)*8.., tokens of parity lane/32)
+    // ---- acc = acc * alpha + P V (lane: dims 4*lane..+3, all 16 tokens) ----------
 #pragma unroll
     for (int r = 0; r < kG; ++r)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r][e] *= alpha[r];
+      for (int e = 0; e < 4; ++e) acc[r][e] *= alpha[r];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 pv = sm_p[wave][2 * i + (lane >> 5)];
+    for (int i = 0; i < kPage; ++i) {
+      const float4 pv = sm_p[wave][i];
       const float pw[kG] = {pv.x, pv.y, pv.z, pv.w};
+      u32x2_t vi = vr[i];
+      if constexpr (kFused) {
+        if (new_page && i == last_slot) vi = vnew;
+      }
+      const float v0 = bf16_lo(vi[0]), v1 = bf16_hi(vi[0]);
+      const float v2 = bf16_lo(vi[1]), v3 = bf16_hi(vi[1]);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float v0 = bf16_lo(cur.v[i][w]), v1 = bf16_hi(cur.v[i][w]);
-#pragma unroll
-        for (int r = 0; r < kG; ++r) {
-          acc[r][2 * w] = fmaf(pw[r], v0, acc[r][2 * w]);
-          acc[r][2 * w + 1] = fmaf(pw[r], v1, acc[r][2 * w + 1]);
-        }
+      for (int r = 0; r < kG; ++r) {
+        acc[r][0] = fmaf(pw[r], v0, acc[r][0]);
+        acc[r][1] = fmaf(pw[r], v1, acc[r][1]);
+        acc[r][2] = fmaf(pw[r], v2, acc[r][2]);
+        acc[r][3] = fmaf(pw[r], v3, acc[r][3]);
       }
     }
     __builtin_amdgcn_wave_barrier();
-    if (pn < p1) cur = nxt;
   }
 
-  // ---- fold the two token parities, then the four waves ---------------------
+  // ---- merge the four wave states through LDS ---------------------------------
 #pragma unroll
   for (int r = 0; r < kG; ++r)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[r][e] += __shfl_xor(acc[r][e], 32);
-  if (lane < 32) {
-#pragma unroll
-    for (int r = 0; r < kG; ++r) {
-      sm_acc[wave][r][lane * 2] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
-      sm_acc[wave][r][lane * 2 + 1] =
-          make_float4(acc[r][4], acc[r][5], acc[r][6], acc[r][7]);
-    }
-  }
+    sm_acc[wave][r][lane] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < kG; ++r) {
@@ -226,8 +316,7 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(
   }
   __syncthreads();
 
-  const int r = threadIdx.x >> 6;  // query head within the group
-  const int c4 = threadIdx.x & 63; // float4 column
+  const int r = wave;  // query head within the group handled by this wave
   float M = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][0][r]);
@@ -235,81 +324,114 @@ __global__ __launch_bounds__(256) void paged_decode_split_kernel(
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    const float a = __expf(sm_ml[w][0][r] - M);
-    L += a * sm_ml[w][1][r];
-    const float4 x = sm_acc[w][r][c4];
-    A.x += a * x.x;
-    A.y += a * x.y;
-    A.z += a * x.z;
-    A.w += a * x.w;
+    const float e = __expf(sm_ml[w][0][r] - M);
+    L += e * sm_ml[w][1][r];
+    const float4 x = sm_acc[w][r][lane];
+    A.x += e * x.x;
+    A.y += e * x.y;
+    A.z += e * x.z;
+    A.w += e * x.w;
   }
   const int hq = h * kG + r;
-  *reinterpret_cast<float4 *>(ap + b * a_b + hq * a_h + s * a_s + c4 * 4) = A;
-  if (c4 == 0) {
-    mp[b * ml_b + hq * ml_h + s * ml_s] = M;
-    lp[b * ml_b + hq * ml_h + s * ml_s] = L;
+  if constexpr (kFused) {
+    if (nact == 1) {  // the only split: finish here, no scratch round trip
+      store_out4(a, b, hq, lane * 4, A, L);
+      return;
+    }
+  }
+  *reinterpret_cast<float4 *>(a.ap + b * a.a_b + hq * a.a_h + s * a.a_s + lane * 4) = A;
+  if (lane == 0) {
+    a.mp[b * a.ml_b + hq * a.ml_h + s * a.ml_s] = M;
+    a.lp[b * a.ml_b + hq * a.ml_h + s * a.ml_s] = L;
+  }
+  if constexpr (kFused) {
+    // Publish this split, count it; the last of the nact splits merges.
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int *cnt = a.counters + b * a.hkv + h;
+      const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+      const int last = done == nact - 1;
+      if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sm_last = last;
+    }
+    __syncthreads();
+    if (!sm_last) return;
+    __threadfence();
+    merge_head(a, b, hq, nact, lane);
   }
 }
 
-// One wavefront per (sequence, query head); lane owns 4 of the 256 dims.
-__global__ __launch_bounds__(64) void paged_decode_combine_kernel(
-    const float *__restrict__ mp, const float *__restrict__ lp,
-    const float *__restrict__ ap, int64_t ml_b, int64_t ml_h, int64_t ml_s,
-    int64_t a_b, int64_t a_h, int64_t a_s, const int64_t *__restrict__ pos,
-    bf16_t *__restrict__ out, int64_t o_b, int64_t o_h, int64_t o_d, int min_pps) {
-  const int b = blockIdx.x, hq = blockIdx.y, lane = threadIdx.x;
-  const int seq_len = int(pos[b]) + 1;
+// One wavefront per (sequence, query head).
+__global__ __launch_bounds__(64) void paged_decode_combine_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x, hq = blockIdx.y;
+  const int seq_len = int(a.pos[b]) + 1;
   const int npg = (seq_len + kPage - 1) / kPage;
-  const int pps = split_pps(npg, min_pps);
-  const int nact = (npg + pps - 1) / pps;
-  const float *mrow = mp + b * ml_b + hq * ml_h;
-  const float *lrow = lp + b * ml_b + hq * ml_h;
-  const float *arow = ap + b * a_b + hq * a_h + lane * 4;
+  const int pps = split_pps(npg, a.min_pps);
+  merge_head(a, b, hq, (npg + pps - 1) / pps, threadIdx.x);
+}
 
-  float mx = -INFINITY;
-  for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, mrow[s * ml_s]);
-  mx = wave_max(mx);
+bool cache_layout_ok(const void *kc, const void *vc, const int64_t *kcs, const int64_t *vcs) {
+  return kcs[3] == 1 && vcs[3] == 1 && kcs[2] % 8 == 0 && vcs[2] % 8 == 0 &&
+         kcs[1] % 8 == 0 && vcs[1] % 8 == 0 && kcs[0] % 8 == 0 && vcs[0] % 8 == 0 &&
+         wyh::aligned16(kc) && wyh::aligned16(vc);
+}
 
-  float L = 0.f;
-  float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  int s = 0;
-  for (; s + 4 <= nact; s += 4) {
-    float4 x[4];
-    float a[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      x[u] = *reinterpret_cast<const float4 *>(arow + (s + u) * a_s);
-      a[u] = __expf(mrow[(s + u) * ml_s] - mx);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      L += a[u] * lrow[(s + u) * ml_s];
-      A.x += a[u] * x[u].x;
-      A.y += a[u] * x[u].y;
-      A.z += a[u] * x[u].z;
-      A.w += a[u] * x[u].w;
-    }
-  }
-  for (; s < nact; ++s) {
-    const float4 x = *reinterpret_cast<const float4 *>(arow + s * a_s);
-    const float a = __expf(mrow[s * ml_s] - mx);
-    L += a * lrow[s * ml_s];
-    A.x += a * x.x;
-    A.y += a * x.y;
-    A.z += a * x.z;
-    A.w += a * x.w;
-  }
-  bf16_t *orow = out + b * o_b + hq * o_h;
-  const int d = lane * 4;
-  if (o_d == 1) {
-    u32x2_t w = {pack_bf16x2(A.x / L, A.y / L), pack_bf16x2(A.z / L, A.w / L)};
-    *reinterpret_cast<u32x2_t *>(orow + d) = w;
-  } else {
-    orow[(d + 0) * o_d] = bf16_t(f32_to_bf16_bits(A.x / L));
-    orow[(d + 1) * o_d] = bf16_t(f32_to_bf16_bits(A.y / L));
-    orow[(d + 2) * o_d] = bf16_t(f32_to_bf16_bits(A.z / L));
-    orow[(d + 3) * o_d] = bf16_t(f32_to_bf16_bits(A.w / L));
-  }
+bool scratch_layout_ok(const void *acc, const int64_t *as) {
+  return as[3] == 1 && as[2] % 4 == 0 && as[1] % 4 == 0 && as[0] % 4 == 0 &&
+         wyh::aligned16(acc);
+}
+
+bool q_layout_ok(const void *q, const int64_t *qs) {
+  return qs[2] != 1 || (qs[0] % 8 == 0 && qs[1] % 8 == 0 && wyh::aligned16(q));
+}
+
+bool out_layout_ok(const void *out, const int64_t *os) {
+  return os[2] != 1 || (os[0] % 4 == 0 && os[1] % 4 == 0 &&
+                        (reinterpret_cast<uintptr_t>(out) & 7u) == 0);
+}
+
+int split_grid_z(int max_pages, int min_pps) {
+  const int z = (max_pages + min_pps - 1) / min_pps;
+  return z > kMaxSplits ? kMaxSplits : z;
+}
+
+DecodeArgs base_args(const void *q, const int64_t *qs, const void *k_cache,
+                     const void *v_cache, const int64_t *kcs, const int64_t *vcs,
+                     const int32_t *block_table, int64_t bt_stride0, const int64_t *pos,
+                     float *m_partial, float *l_partial, float *acc_partial,
+                     const int64_t *mls, const int64_t *as, int num_kv_heads, int head_dim,
+                     int min_pps) {
+  DecodeArgs a = {};
+  a.q = static_cast<const bf16_t *>(q);
+  a.qs_b = qs[0];
+  a.qs_h = qs[1];
+  a.qs_d = qs[2];
+  a.kc = static_cast<bf16_t *>(const_cast<void *>(k_cache));
+  a.vc = static_cast<bf16_t *>(const_cast<void *>(v_cache));
+  a.kc_p = kcs[0];
+  a.kc_h = kcs[1];
+  a.kc_s = kcs[2];
+  a.vc_p = vcs[0];
+  a.vc_h = vcs[1];
+  a.vc_s = vcs[2];
+  a.bt = block_table;
+  a.bt_b = bt_stride0;
+  a.pos = pos;
+  a.mp = m_partial;
+  a.lp = l_partial;
+  a.ap = acc_partial;
+  a.ml_b = mls[0];
+  a.ml_h = mls[1];
+  a.ml_s = mls[2];
+  a.a_b = as[0];
+  a.a_h = as[1];
+  a.a_s = as[2];
+  a.scale = 1.0f / sqrtf(float(head_dim));
+  a.min_pps = min_pps;
+  a.hkv = num_kv_heads;
+  return a;
 }
 
 }  // namespace
@@ -329,22 +451,15 @@ extern "C" int wy_paged_decode_split(const void *q, const int64_t *qs, const voi
   if (batch < 0 || num_kv_heads <= 0 || max_pages <= 0 || min_pages_per_split <= 0)
     return WY_E_SHAPE;
   if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
-  if (kcs[3] != 1 || vcs[3] != 1 || kcs[2] % 8 || vcs[2] % 8 || kcs[1] % 8 ||
-      vcs[1] % 8 || kcs[0] % 8 || vcs[0] % 8 || as[3] != 1 || as[2] % 4 ||
-      as[1] % 4 || as[0] % 4 || !wyh::aligned16(k_cache) || !wyh::aligned16(v_cache) ||
-      !wyh::aligned16(acc_partial) ||
-      (qs[2] == 1 && (qs[0] % 8 || qs[1] % 8 || !wyh::aligned16(q))))
+  if (!cache_layout_ok(k_cache, v_cache, kcs, vcs) || !scratch_layout_ok(acc_partial, as) ||
+      !q_layout_ok(q, qs))
     return WY_E_LAYOUT;
   if (batch == 0) return WY_OK;
-  int splits = (max_pages + min_pages_per_split - 1) / min_pages_per_split;
-  if (splits > kMaxSplits) splits = kMaxSplits;
-  dim3 grid(batch, num_kv_heads, splits);
-  paged_decode_split_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const bf16_t *>(q), qs[0], qs[1], qs[2],
-      static_cast<const bf16_t *>(k_cache), static_cast<const bf16_t *>(v_cache), kcs[0],
-      kcs[1], kcs[2], vcs[0], vcs[1], vcs[2], block_table, bt_stride0, pos, m_partial,
-      l_partial, acc_partial, mls[0], mls[1], mls[2], as[0], as[1], as[2],
-      1.0f / sqrtf(float(head_dim)), min_pages_per_split);
+  const DecodeArgs a = base_args(q, qs, k_cache, v_cache, kcs, vcs, block_table, bt_stride0,
+                                 pos, m_partial, l_partial, acc_partial, mls, as,
+                                 num_kv_heads, head_dim, min_pages_per_split);
+  dim3 grid(batch, num_kv_heads, split_grid_z(max_pages, min_pages_per_split));
+  paged_decode_split_kernel<false><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return wyh::launch_status();
 }
 
@@ -358,14 +473,75 @@ extern "C" int wy_paged_decode_combine(const float *m_partial, const float *l_pa
     return WY_E_NULL;
   if (batch < 0 || num_q_heads <= 0 || min_pages_per_split <= 0) return WY_E_SHAPE;
   if (head_dim != kD) return WY_E_UNSUPPORTED;
-  if (as[3] != 1 || as[2] % 4 || as[1] % 4 || as[0] % 4 || !wyh::aligned16(acc_partial) ||
-      (os[2] == 1 && (os[0] % 4 || os[1] % 4 ||
-                      (reinterpret_cast<uintptr_t>(out) & 7u))))
+  if (!scratch_layout_ok(acc_partial, as) || !out_layout_ok(out, os)) return WY_E_LAYOUT;
+  if (batch == 0) return WY_OK;
+  DecodeArgs a = {};
+  a.mp = const_cast<float *>(m_partial);
+  a.lp = const_cast<float *>(l_partial);
+  a.ap = const_cast<float *>(acc_partial);
+  a.ml_b = mls[0];
+  a.ml_h = mls[1];
+  a.ml_s = mls[2];
+  a.a_b = as[0];
+  a.a_h = as[1];
+  a.a_s = as[2];
+  a.pos = pos;
+  a.min_pps = min_pages_per_split;
+  a.out = static_cast<bf16_t *>(out);
+  a.o_b = os[0];
+  a.o_h = os[1];
+  a.o_d = os[2];
+  dim3 grid(batch, num_q_heads);
+  paged_decode_combine_kernel<<<grid, 64, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_paged_decode_step(const void *q, const int64_t *qs, const void *k_new,
+                                    const void *v_new, const int64_t *kns,
+                                    const int64_t *vns, void *k_cache, void *v_cache,
+                                    const int64_t *kcs, const int64_t *vcs,
+                                    const int32_t *block_table, int64_t bt_stride0,
+                                    const int64_t *pos, float *m_partial, float *l_partial,
+                                    float *acc_partial, const int64_t *mls,
+                                    const int64_t *as, int32_t *counters, const void *gate,
+                                    const int64_t *gs, void *out, const int64_t *os,
+                                    int batch, int num_q_heads, int num_kv_heads,
+                                    int head_dim, int max_pages, int min_pages_per_split,
+                                    void *stream) {
+  if (!q || !qs || !k_new || !v_new || !kns || !vns || !k_cache || !v_cache || !kcs ||
+      !vcs || !block_table || !pos || !m_partial || !l_partial || !acc_partial || !mls ||
+      !as || !counters || !out || !os || (gate && !gs))
+    return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || max_pages <= 0 || min_pages_per_split <= 0)
+    return WY_E_SHAPE;
+  if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
+  if (!cache_layout_ok(k_cache, v_cache, kcs, vcs) || !scratch_layout_ok(acc_partial, as) ||
+      !q_layout_ok(q, qs) || !out_layout_ok(out, os) || kns[2] != 1 || vns[2] != 1 ||
+      kns[0] % 8 || kns[1] % 8 || vns[0] % 8 || vns[1] % 8 || !wyh::aligned16(k_new) ||
+      !wyh::aligned16(v_new))
     return WY_E_LAYOUT;
   if (batch == 0) return WY_OK;
-  dim3 grid(batch, num_q_heads);
-  paged_decode_combine_kernel<<<grid, 64, 0, static_cast<hipStream_t>(stream)>>>(
-      m_partial, l_partial, acc_partial, mls[0], mls[1], mls[2], as[0], as[1], as[2], pos,
-      static_cast<bf16_t *>(out), os[0], os[1], os[2], min_pages_per_split);
+  DecodeArgs a = base_args(q, qs, k_cache, v_cache, kcs, vcs, block_table, bt_stride0, pos,
+                           m_partial, l_partial, acc_partial, mls, as, num_kv_heads,
+                           head_dim, min_pages_per_split);
+  a.kn = static_cast<const bf16_t *>(k_new);
+  a.vn = static_cast<const bf16_t *>(v_new);
+  a.kn_b = kns[0];
+  a.kn_h = kns[1];
+  a.vn_b = vns[0];
+  a.vn_h = vns[1];
+  a.counters = counters;
+  a.gate = static_cast<const bf16_t *>(gate);
+  if (gate) {
+    a.g_b = gs[0];
+    a.g_h = gs[1];
+    a.g_d = gs[2];
+  }
+  a.out = static_cast<bf16_t *>(out);
+  a.o_b = os[0];
+  a.o_h = os[1];
+  a.o_d = os[2];
+  dim3 grid(batch, num_kv_heads, split_grid_z(max_pages, min_pages_per_split));
+  paged_decode_split_kernel<true><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return wyh::launch_status();
 }

@@ -22,6 +22,8 @@ their contents are a private contract between the two ops.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 
 from . import _lib
@@ -54,6 +56,18 @@ def allocate_paged_kv_cache(
     return k, v
 
 
+class SplitScratch(tuple):
+    """``(m, l, acc)`` as in the reference, plus ``counters``: one int32 per
+    (sequence, query head) slot used by the one-launch decode step to elect
+    the workgroup that merges the splits.  Counters start at zero and every
+    step leaves them at zero.  Unpacks like the reference's 3-tuple."""
+
+    def __new__(cls, m, l, acc, counters):
+        obj = super().__new__(cls, (m, l, acc))
+        obj.counters = counters
+        return obj
+
+
 def allocate_split_scratch(
     num_q_heads: int,
     head_dim: int,
@@ -62,13 +76,15 @@ def allocate_split_scratch(
     device: torch.device | str = "cuda",
 ):
     """Split-K workspace shared by all attention layers: m, l ``[B, H_q, 128]``
-    and acc ``[B, H_q, 128, D]`` fp32 (reference :591-609)."""
+    and acc ``[B, H_q, 128, D]`` fp32 (reference :591-609), plus the merge
+    counters of the fused step (``.counters``, ``[B * H_q]`` int32 zeros)."""
     m = torch.zeros((batch, num_q_heads, MAX_SPLITS), dtype=torch.float32, device=device)
     l = torch.zeros((batch, num_q_heads, MAX_SPLITS), dtype=torch.float32, device=device)
     acc = torch.zeros(
         (batch, num_q_heads, MAX_SPLITS, head_dim), dtype=torch.float32, device=device
     )
-    return m, l, acc
+    counters = torch.zeros((batch * num_q_heads,), dtype=torch.int32, device=device)
+    return SplitScratch(m, l, acc, counters)
 
 
 def physical_rows(
@@ -283,6 +299,68 @@ def _paged_combine_fake(m_partial, l_partial, acc_partial, pos) -> torch.Tensor:
     )
 
 
+@torch.library.custom_op(
+    "wy_lib::paged_gqa_attention_decode_fused",
+    mutates_args=("k_cache", "v_cache", "m_partial", "l_partial", "acc_partial", "counters"),
+    device_types="cuda",
+)
+def paged_gqa_attention_decode_fused(
+    q: torch.Tensor,
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    pos: torch.Tensor,
+    m_partial: torch.Tensor,
+    l_partial: torch.Tensor,
+    acc_partial: torch.Tensor,
+    counters: torch.Tensor,
+    gate: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """append + split + combine (+ gate) in one launch; returns ``[B, H_q, D]``
+    bf16.  Same result as the three reference ops in sequence (and, with
+    ``gate``, followed by ``attention_gate_pack``): identical device code for
+    the attention math and the same two bf16 roundings.  ``gate`` is
+    ``[B, H_q, D]`` (any strides)."""
+    batch, num_q_heads, head_dim = q.shape
+    num_pages, num_kv_heads, page, cache_dim = k_cache.shape
+    assert page == PAGE_SIZE and cache_dim == head_dim
+    assert v_cache.shape == k_cache.shape
+    assert k_new.shape == v_new.shape == (batch, num_kv_heads, head_dim)
+    assert q.dtype == k_new.dtype == v_new.dtype == k_cache.dtype == v_cache.dtype == torch.bfloat16
+    assert block_table.dtype == torch.int32 and block_table.shape[0] == batch
+    assert block_table.stride(1) == 1
+    assert pos.dtype == torch.int64 and pos.shape == (batch,) and pos.is_contiguous()
+    assert m_partial.shape == (batch, num_q_heads, MAX_SPLITS)
+    assert l_partial.shape == m_partial.shape and l_partial.stride() == m_partial.stride()
+    assert acc_partial.shape == (batch, num_q_heads, MAX_SPLITS, head_dim)
+    assert counters.dtype == torch.int32 and counters.is_contiguous()
+    assert counters.numel() >= batch * num_kv_heads
+    assert num_q_heads % num_kv_heads == 0
+    if gate is not None:
+        assert gate.shape == q.shape and gate.dtype == torch.bfloat16
+    out = torch.empty((batch, num_q_heads, head_dim), dtype=torch.bfloat16, device=q.device)
+    _lib.call(
+        "wy_paged_decode_step",
+        _lib.ptr(q), _lib.strides(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.strides(k_new),
+        _lib.strides(v_new), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.strides(k_cache),
+        _lib.strides(v_cache), _lib.ptr(block_table), block_table.stride(0), _lib.ptr(pos),
+        _lib.ptr(m_partial), _lib.ptr(l_partial), _lib.ptr(acc_partial),
+        _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(counters),
+        _lib.ptr(gate), _lib.strides(gate), _lib.ptr(out), _lib.strides(out),
+        batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
+        MIN_PAGES_PER_SPLIT, _lib.stream(q.device),
+    )
+    return out
+
+
+@paged_gqa_attention_decode_fused.register_fake
+def _paged_fused_fake(q, k_new, v_new, k_cache, v_cache, block_table, pos, m_partial,
+                      l_partial, acc_partial, counters, gate=None) -> torch.Tensor:
+    return torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+
+
 def _seq_bucket(seq_len: int) -> int:
     """Kept for interface parity with the reference (:950); the HIP kernels
     have fixed launch configurations, so the bucket selects nothing."""
@@ -308,18 +386,32 @@ def call_paged_gqa_attention_decode_triton(
     scratch: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Append + split + combine; returns ``[B, H_q, D]`` bf16 (reference
-    :963-994).  The name is kept so callers switch by import only."""
+    :963-994).  The name is kept so callers switch by import only.  With a
+    scratch from ``allocate_split_scratch`` (it carries merge counters) the
+    three steps run as one launch; a plain ``(m, l, acc)`` tuple takes the
+    three-op path."""
     if scratch is None:
         scratch = allocate_split_scratch(
             q.shape[1], q.shape[2], batch=q.shape[0], device=q.device
         )
     m_partial, l_partial, acc_partial = scratch
+    counters = getattr(scratch, "counters", None)
+    if counters is not None and _fused_ok(k_new, v_new):
+        return paged_gqa_attention_decode_fused(
+            q, k_new, v_new, k_cache, v_cache, block_table, pos, m_partial, l_partial,
+            acc_partial, counters)
     paged_kv_append(k_cache, v_cache, k_new, v_new, block_table, pos)
     hint = k_cache.shape[0] * PAGE_SIZE
     paged_gqa_attention_decode_split(
         q, k_cache, v_cache, block_table, m_partial, l_partial, acc_partial, pos, hint
     )
     return paged_gqa_attention_decode_combine(m_partial, l_partial, acc_partial, pos)
+
+
+def _fused_ok(k_new: torch.Tensor, v_new: torch.Tensor) -> bool:
+    """The one-launch step reads k_new/v_new rows as 16-byte chunks."""
+    return all(t.stride(2) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0
+               and t.data_ptr() % 16 == 0 for t in (k_new, v_new))
 
 
 paged_gqa_attention_decode = call_paged_gqa_attention_decode_triton

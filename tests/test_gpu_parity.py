@@ -443,3 +443,66 @@ def test_prefill_then_decode_consistency(pkg, dev):
         q[last].to(dev), k[last].to(dev), v[last].to(dev), kg, vg, bt.to(dev),
         torch.tensor(lengths, dtype=torch.int64, device=dev))
     close(ctx, full.cpu()[last].float(), max_abs=2e-2, mean_abs=2e-3, what="decode vs prefill row")
+
+
+# ------------------------------------------------------------------ fused decode step
+
+@pytest.mark.parametrize("lens", [[1], [17, 64, 65], [256], [5000, 3, 700], [2048 * 4 + 3]])
+def test_fused_step_equals_three_op_path(pkg, dev, lens):
+    """One-launch step == append + split + combine (same device math, same
+    rounding): bit-identical output and pools; counters return to zero."""
+    say(f"fused vs 3-op lens={lens}")
+    gen = torch.Generator().manual_seed(sum(lens))
+    B = len(lens)
+    max_pages = -(-max(lens) // 16) + 1
+    num_pages = B * max_pages + 3
+    bt = rand_table(B, max_pages, num_pages, gen)
+    kc, vc = bf((num_pages, HKV, 16, D), gen), bf((num_pages, HKV, 16, D), gen)
+    q, kn, vn = bf((B, HQ, D), gen), bf((B, HKV, D), gen), bf((B, HKV, D), gen)
+    pos = torch.tensor([n - 1 for n in lens], device=dev)
+    sc = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    k1, v1 = kc.to(dev), vc.to(dev)
+    fused = pkg.call_paged_gqa_attention_decode_triton(q.to(dev), kn.to(dev), vn.to(dev), k1,
+                                                       v1, bt.to(dev), pos, sc)
+    k2, v2 = kc.to(dev), vc.to(dev)
+    plain = pkg.call_paged_gqa_attention_decode_triton(q.to(dev), kn.to(dev), vn.to(dev), k2,
+                                                       v2, bt.to(dev), pos, tuple(sc))
+    torch.cuda.synchronize()
+    assert torch.equal(fused.cpu(), plain.cpu())
+    assert torch.equal(k1.cpu(), k2.cpu()) and torch.equal(v1.cpu(), v2.cpu())
+    assert int(sc.counters.abs().sum()) == 0
+    orc.paged_kv_append(kc, vc, kn, vn, bt, pos.cpu())
+    close(fused, orc.paged_decode(q, kc, vc, bt, pos.cpu() + 1), what=f"fused {lens}")
+
+
+def test_decode_attention_step_with_gate(pkg, dev):
+    """Runner glue (RoPE + fused append/attention/gate) vs the reference op
+    sequence computed by the oracle, on the runner's strided fused-GEMV views."""
+    say("decode_attention_step gated")
+    gen = torch.Generator().manual_seed(41)
+    lens = [33, 1000, 129, 2]
+    B = len(lens)
+    max_pages = 70
+    num_pages = B * max_pages
+    bt = rand_table(B, max_pages, num_pages, gen)
+    kc, vc = bf((num_pages, HKV, 16, D), gen), bf((num_pages, HKV, 16, D), gen)
+    fused_gemv = bf((B, 5120), gen)  # [q 2048 | gate 2048 | k 512 | v 512]
+    pos = torch.tensor([n - 1 for n in lens])
+    inv = C.inv_freq()
+    fg = fused_gemv.to(dev)
+    kg, vg = kc.to(dev), vc.to(dev)
+    sc = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    out = pkg.decode_attention_step(fg[:, :2048].view(B, HQ, D), fg[:, 4096:4608].view(B, HKV, D),
+                                    fg[:, 4608:], fg[:, 2048:4096], inv.to(dev), 64, pos.to(dev),
+                                    kg, vg, bt.to(dev), sc)
+    # reference sequence on the CPU oracle
+    q = orc.partial_rope(fused_gemv[:, :2048].view(B, HQ, 1, D), pos.view(B, 1), inv, 64)[:, :, 0]
+    k = orc.partial_rope(fused_gemv[:, 4096:4608].view(B, HKV, 1, D), pos.view(B, 1), inv, 64)[:, :, 0]
+    v = fused_gemv[:, 4608:].reshape(B, HKV, D)
+    orc.paged_kv_append(kc, vc, k, v, bt, pos)
+    assert torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc)
+    ctx = orc.paged_decode(q, kc, vc, bt, pos + 1).to(torch.bfloat16)
+    gate4 = fused_gemv[:, 2048:4096].reshape(B, HQ, D).permute(1, 0, 2).unsqueeze(0)
+    ref = orc.gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), gate4)
+    assert out.shape == (B, 2048)
+    close(out, ref, what="gated step")
