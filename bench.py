@@ -154,7 +154,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
-    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-split", "pmc-copy"],
+    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy"],
                     help="pmc-*: eager launches only, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -176,28 +176,24 @@ def main():
     w = decode_workload(lens, dev, seed=2)
     scratch = pkg.allocate_split_scratch(HQ, D, batch=32, device=dev)
 
+    m_p, l_p, acc_p = scratch
+    gate3 = w["gate"][0].permute(1, 0, 2)  # [B, Hq, D] view
+
     def step():
+        return torch.ops.wy_lib.paged_gqa_attention_decode_fused(
+            w["q"], w["kn"], w["vn"], w["kc"], w["vc"], w["bt"], w["pos"], m_p, l_p, acc_p,
+            scratch.counters, gate3)
+
+    def step_three_ops():
         ctx = pkg.call_paged_gqa_attention_decode_triton(
-            w["q"], w["kn"], w["vn"], w["kc"], w["vc"], w["bt"], w["pos"], scratch)
+            w["q"], w["kn"], w["vn"], w["kc"], w["vc"], w["bt"], w["pos"], tuple(scratch))
         return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w["gate"])
 
-    log(f"decode config2: sum(L)={sum(lens)} B=32")
-    ms = time_graph(step, args.steps, args.warmup) if args.mode == "bench" else 0.0
-    step_bytes = decode_bytes(lens)
-    gbs = step_bytes / (ms * 1e-3) / 1e9 if ms else 0.0
-
-    # dominant kernel alone: split partial pass, events over a graph of launches
-    m_p, l_p, acc_p = scratch
-
-    def split_only():
-        torch.ops.wy_lib.paged_gqa_attention_decode_split(
-            w["q"], w["kc"], w["vc"], w["bt"], m_p, l_p, acc_p, w["pos"], 0)
-
-    if args.mode == "pmc-split":
+    if args.mode == "pmc-step":
         for _ in range(10):
-            split_only()
+            step()
         torch.cuda.synchronize()
-        print(json.dumps({"mode": "pmc-split", "algorithmic_bytes": split_kernel_bytes(lens)}))
+        print(json.dumps({"mode": "pmc-step", "algorithmic_bytes": decode_bytes(lens)}))
         return
     if args.mode == "pmc-copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -205,14 +201,20 @@ def main():
         for _ in range(10):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"mode": "pmc-copy", "bytes_read": 256 << 20, "bytes_written": 256 << 20}))
+        print(json.dumps({"mode": "pmc-copy", "bytes_read": 256 << 20,
+                          "bytes_written": 256 << 20}))
         return
 
-    split_ms = time_graph_events(split_only, 100)
-    sbytes = split_kernel_bytes(lens)
-    split_gbs = sbytes / (split_ms * 1e-3) / 1e9
+    log(f"decode config2: sum(L)={sum(lens)} B=32")
+    ms = time_graph(step, args.steps, args.warmup)
+    step_bytes = decode_bytes(lens)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    # the step is one kernel: time it alone, back to back inside one graph
+    kern_ms = time_graph_events(step, 100)
+    kern_gbs = step_bytes / (kern_ms * 1e-3) / 1e9
+    ms3 = time_graph(step_three_ops, args.steps, args.warmup)
     traffic = None
-    tfile = ROOT / "profiles" / "decode_split_config2_traffic.json"
+    tfile = ROOT / "profiles" / "decode_step_config2_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
 
@@ -233,15 +235,16 @@ def main():
         "config": {"workload": "config2: paged GQA decode step B=32, L~U[128,2048], "
                                "8q/2kv heads, d=256, 16-token pages",
                    "global_batch": 32, "sum_context_tokens": sum(lens),
-                   "step": "append+split+combine+gate, one HIP graph replay",
+                   "step": "one-launch append+split+merge+gate, HIP graph replay",
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "paged_decode_split_kernel", "bound": "hbm",
-                     "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": sbytes,
-                     "avg_launch_us": round(split_ms * 1e3, 3)},
+        "roofline": {"kernel": "paged_decode_split_kernel<true> (fused step)", "bound": "hbm",
+                     "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": step_bytes,
+                     "avg_launch_us": round(kern_ms * 1e3, 3)},
+        "three_op_path_us_per_step": round(ms3 * 1e3, 2),
     }
-    log(f"  step {ms*1e3:.2f} us  {gbs:.0f} GB/s; split {split_ms*1e3:.2f} us {split_gbs:.0f} GB/s")
+    log(f"  step {ms*1e3:.2f} us {gbs:.0f} GB/s; kernel {kern_ms*1e3:.2f} us; 3-op {ms3*1e3:.2f} us")
 
     extra = {}
     only = set(filter(None, args.only.split(",")))
@@ -254,10 +257,12 @@ def main():
         w1 = decode_workload([256], dev, seed=1, contiguous=True)
         sc1 = pkg.allocate_split_scratch(HQ, D, batch=1, device=dev)
 
+        g1 = w1["gate"][0].permute(1, 0, 2)
+
         def step1():
-            ctx = pkg.call_paged_gqa_attention_decode_triton(
-                w1["q"], w1["kn"], w1["vn"], w1["kc"], w1["vc"], w1["bt"], w1["pos"], sc1)
-            return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w1["gate"])
+            return torch.ops.wy_lib.paged_gqa_attention_decode_fused(
+                w1["q"], w1["kn"], w1["vn"], w1["kc"], w1["vc"], w1["bt"], w1["pos"], *sc1,
+                sc1.counters, g1)
 
         ms1 = time_graph(step1, 500, 50)
         extra["config1_decode_B1_L256"] = {"us_per_step": round(ms1 * 1e3, 2),
@@ -284,10 +289,12 @@ def main():
             torch.ops.wy_lib.paged_gqa_attention_decode_split(
                 w5["q"], w5["kc"], w5["vc"], w5["bt"], m5, l5, a5, w5["pos"], 0)
 
+        g5 = w5["gate"][0].permute(1, 0, 2)
+
         def step5():
-            ctx = pkg.call_paged_gqa_attention_decode_triton(
-                w5["q"], w5["kn"], w5["vn"], w5["kc"], w5["vc"], w5["bt"], w5["pos"], sc5)
-            return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w5["gate"])
+            return torch.ops.wy_lib.paged_gqa_attention_decode_fused(
+                w5["q"], w5["kn"], w5["vn"], w5["kc"], w5["vc"], w5["bt"], w5["pos"], *sc5,
+                sc5.counters, g5)
 
         ms5 = time_graph(step5, 20, 3)
         sp5 = time_events(split5, 20)

@@ -107,43 +107,76 @@ __device__ __forceinline__ void store_out4(const DecodeArgs &a, int b, int hq, i
   }
 }
 
+// Device-coherent (agent-scope) scalar / 8-byte accesses.  On gfx950 each
+// XCD has its own L2, so split partials handed from one workgroup to another
+// inside a launch go through these instead of plain cached accesses; no
+// cache-wide writeback or invalidate is then needed.
+__device__ __forceinline__ void st_coherent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent4(float *p, float4 v) {
+  uint64_t *q = reinterpret_cast<uint64_t *>(p);
+  __hip_atomic_store(q, (uint64_t(__float_as_uint(v.y)) << 32) | __float_as_uint(v.x),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, (uint64_t(__float_as_uint(v.w)) << 32) | __float_as_uint(v.z),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool kCoherent>
+__device__ __forceinline__ float ld_f(const float *p) {
+  if constexpr (kCoherent)
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+template <bool kCoherent>
+__device__ __forceinline__ float4 ld_f4(const float *p) {
+  if constexpr (kCoherent) {
+    uint64_t *q = reinterpret_cast<uint64_t *>(const_cast<float *>(p));
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float(uint32_t(lo)), __uint_as_float(uint32_t(lo >> 32)),
+                       __uint_as_float(uint32_t(hi)), __uint_as_float(uint32_t(hi >> 32)));
+  } else {
+    return *reinterpret_cast<const float4 *>(p);
+  }
+}
+
 // Merge the nact split states of (b, hq) with one wavefront; lane owns dims
-// 4*lane..4*lane+3.  Shared by the combine kernel and the fused step.
+// 4*lane..4*lane+3.  Shared by the combine kernel and the fused step.  The
+// split weights are formed lane-parallel (lane s holds split s, nact <= 128)
+// and the accumulator rows are fetched 8 at a time, so the merge costs a few
+// memory round trips rather than one per split.
+template <bool kCoherent>
 __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lane) {
   const float *mrow = a.mp + b * a.ml_b + hq * a.ml_h;
   const float *lrow = a.lp + b * a.ml_b + hq * a.ml_h;
   const float *arow = a.ap + b * a.a_b + hq * a.a_h + lane * 4;
-  float mx = -INFINITY;
-  for (int s = lane; s < nact; s += 64) mx = fmaxf(mx, mrow[s * a.ml_s]);
-  mx = wave_max(mx);
-  float L = 0.f;
+  const bool has0 = lane < nact, has1 = lane + 64 < nact;
+  const float m0 = has0 ? ld_f<kCoherent>(mrow + lane * a.ml_s) : -INFINITY;
+  const float m1 = has1 ? ld_f<kCoherent>(mrow + (lane + 64) * a.ml_s) : -INFINITY;
+  const float l0 = has0 ? ld_f<kCoherent>(lrow + lane * a.ml_s) : 0.f;
+  const float l1 = has1 ? ld_f<kCoherent>(lrow + (lane + 64) * a.ml_s) : 0.f;
+  const float mx = wave_max(fmaxf(m0, m1));
+  const float w0 = has0 ? __expf(m0 - mx) : 0.f;
+  const float w1 = has1 ? __expf(m1 - mx) : 0.f;
+  const float L = wave_sum(w0 * l0 + w1 * l1);
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  int s = 0;
-  for (; s + 4 <= nact; s += 4) {
-    float4 x[4];
-    float w[4];
+  for (int s0 = 0; s0 < nact; s0 += 8) {
+    float4 x[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      x[u] = *reinterpret_cast<const float4 *>(arow + (s + u) * a.a_s);
-      w[u] = __expf(mrow[(s + u) * a.ml_s] - mx);
-    }
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < nact) x[u] = ld_f4<kCoherent>(arow + (s0 + u) * a.a_s);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      L += w[u] * lrow[(s + u) * a.ml_s];
-      A.x += w[u] * x[u].x;
-      A.y += w[u] * x[u].y;
-      A.z += w[u] * x[u].z;
-      A.w += w[u] * x[u].w;
+    for (int u = 0; u < 8; ++u) {
+      const int sp = s0 + u;
+      if (sp < nact) {
+        const float w = __shfl(sp < 64 ? w0 : w1, sp & 63);
+        A.x += w * x[u].x;
+        A.y += w * x[u].y;
+        A.z += w * x[u].z;
+        A.w += w * x[u].w;
+      }
     }
-  }
-  for (; s < nact; ++s) {
-    const float4 x = *reinterpret_cast<const float4 *>(arow + s * a.a_s);
-    const float w = __expf(mrow[s * a.ml_s] - mx);
-    L += w * lrow[s * a.ml_s];
-    A.x += w * x.x;
-    A.y += w * x.y;
-    A.z += w * x.z;
-    A.w += w * x.w;
   }
   store_out4(a, b, hq, lane * 4, A, L);
 }
@@ -339,18 +372,29 @@ void paged_decode_split_kernel(const DecodeArgs a) {
       return;
     }
   }
-  *reinterpret_cast<float4 *>(a.ap + b * a.a_b + hq * a.a_h + s * a.a_s + lane * 4) = A;
-  if (lane == 0) {
-    a.mp[b * a.ml_b + hq * a.ml_h + s * a.ml_s] = M;
-    a.lp[b * a.ml_b + hq * a.ml_h + s * a.ml_s] = L;
-  }
-  if constexpr (kFused) {
-    // Publish this split, count it; the last of the nact splits merges.
-    __threadfence();
+  float *adst = a.ap + b * a.a_b + hq * a.a_h + s * a.a_s + lane * 4;
+  float *mdst = a.mp + b * a.ml_b + hq * a.ml_h + s * a.ml_s;
+  float *ldst = a.lp + b * a.ml_b + hq * a.ml_h + s * a.ml_s;
+  if constexpr (!kFused) {
+    *reinterpret_cast<float4 *>(adst) = A;
+    if (lane == 0) {
+      *mdst = M;
+      *ldst = L;
+    }
+  } else {
+    // Publish this split with device-coherent stores, wait for them to
+    // complete (workgroup-scope release), then count it.  The workgroup that
+    // brings the count to nact merges, reading the partials coherently.
+    st_coherent4(adst, A);
+    if (lane == 0) {
+      st_coherent(mdst, M);
+      st_coherent(ldst, L);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     if (threadIdx.x == 0) {
       int *cnt = a.counters + b * a.hkv + h;
-      const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL,
+      const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
       const int last = done == nact - 1;
       if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -358,8 +402,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     }
     __syncthreads();
     if (!sm_last) return;
-    __threadfence();
-    merge_head(a, b, hq, nact, lane);
+    merge_head<true>(a, b, hq, nact, lane);
   }
 }
 
@@ -369,7 +412,7 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(const DecodeAr
   const int seq_len = int(a.pos[b]) + 1;
   const int npg = (seq_len + kPage - 1) / kPage;
   const int pps = split_pps(npg, a.min_pps);
-  merge_head(a, b, hq, (npg + pps - 1) / pps, threadIdx.x);
+  merge_head<false>(a, b, hq, (npg + pps - 1) / pps, threadIdx.x);
 }
 
 bool cache_layout_ok(const void *kc, const void *vc, const int64_t *kcs, const int64_t *vcs) {

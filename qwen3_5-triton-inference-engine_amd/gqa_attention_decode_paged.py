@@ -14,7 +14,7 @@ Layout (unchanged from the reference, gqa_attention_decode_paged.py:29-36)::
 
 Split partition.  The reference splits every sequence into
 ``ceil(npg / ceil(npg/128))`` page-aligned chunks.  The HIP pair here uses
-``pps = max(ceil(npg/128), MIN_PAGES_PER_SPLIT)`` pages per split in both the
+``pps = max(ceil(npg/128), min_pages_per_split(B))`` pages per split in both the
 split and the combine op, so short contexts do not write one 4 KiB fp32
 partial per 16-token page.  The scratch tensors keep the reference shapes;
 their contents are a private contract between the two ops.
@@ -32,7 +32,17 @@ PAGE_SIZE = 16
 MAX_SPLITS = 128
 
 # Lower bound on pages per split shared by split and combine (see module doc).
+# Small batches keep 4 pages (64 tokens) per split so a lone sequence still
+# spreads over many workgroups; large batches already fill the GPU and gain
+# more from fewer partials to merge (16 pages = 256 tokens).  Both ops derive
+# it from the batch size alone, a static shape, so the pair stays graph-safe.
 MIN_PAGES_PER_SPLIT = 4
+MIN_PAGES_PER_SPLIT_LARGE_BATCH = 16
+LARGE_BATCH = 16
+
+
+def min_pages_per_split(batch: int) -> int:
+    return MIN_PAGES_PER_SPLIT_LARGE_BATCH if batch >= LARGE_BATCH else MIN_PAGES_PER_SPLIT
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -254,7 +264,7 @@ def paged_gqa_attention_decode_split(
         block_table.stride(0), _lib.ptr(pos), _lib.ptr(m_partial), _lib.ptr(l_partial),
         _lib.ptr(acc_partial), _lib.strides(m_partial), _lib.strides(acc_partial),
         batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
-        MIN_PAGES_PER_SPLIT, _lib.stream(q.device),
+        min_pages_per_split(batch), _lib.stream(q.device),
     )
 
 
@@ -285,7 +295,7 @@ def paged_gqa_attention_decode_combine(
         "wy_paged_decode_combine",
         _lib.ptr(m_partial), _lib.ptr(l_partial), _lib.ptr(acc_partial),
         _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(pos), _lib.ptr(out),
-        _lib.strides(out), batch, num_q_heads, head_dim, MIN_PAGES_PER_SPLIT,
+        _lib.strides(out), batch, num_q_heads, head_dim, min_pages_per_split(batch),
         _lib.stream(acc_partial.device),
     )
     return out
@@ -350,7 +360,7 @@ def paged_gqa_attention_decode_fused(
         _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(counters),
         _lib.ptr(gate), _lib.strides(gate), _lib.ptr(out), _lib.strides(out),
         batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
-        MIN_PAGES_PER_SPLIT, _lib.stream(q.device),
+        min_pages_per_split(batch), _lib.stream(q.device),
     )
     return out
 
