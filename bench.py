@@ -154,7 +154,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
-    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy"],
+    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill"],
                     help="pmc-*: eager launches only, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -194,6 +194,24 @@ def main():
             step()
         torch.cuda.synchronize()
         print(json.dumps({"mode": "pmc-step", "algorithmic_bytes": decode_bytes(lens)}))
+        return
+    if args.mode == "pmc-prefill":
+        g4 = torch.Generator().manual_seed(4)
+        lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
+        lens4 = [int(x) for x in lens4.round().tolist()]
+        gq = torch.Generator(device=dev).manual_seed(4)
+        tot = sum(lens4)
+        qp = torch.randn(tot, HQ, D, device=dev, generator=gq).to(torch.bfloat16)
+        kp = torch.randn(tot, HKV, D, device=dev, generator=gq).to(torch.bfloat16)
+        vp = torch.randn(tot, HKV, D, device=dev, generator=gq).to(torch.bfloat16)
+        cu_l = [0]
+        for n_ in lens4:
+            cu_l.append(cu_l[-1] + n_)
+        cu4 = torch.tensor(cu_l, dtype=torch.int32, device=dev)
+        for _ in range(3):
+            pkg.gqa_attention_varlen_causal(qp, kp, vp, cu4, max(lens4))
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "pmc-prefill", "flops": prefill_flops(lens4)}))
         return
     if args.mode == "pmc-copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)

@@ -31,12 +31,25 @@ constexpr int kBQ = 32;           // query tokens per workgroup
 constexpr int kBN = 64;           // kv tokens per tile
 constexpr int kKPitch = kD + 8;   // bf16 elements per K row in LDS (528 B)
 constexpr int kVPitch = kBN + 4;  // bf16 elements per V^T row in LDS (136 B)
-constexpr int kLdsBytes = kBN * kKPitch * 2 + kD * kVPitch * 2;
+constexpr int kQBytes = kG * kBQ * kKPitch * 2;  // the four heads' query rows
+constexpr int kLdsBytes = kQBytes + kBN * kKPitch * 2 + kD * kVPitch * 2;
+constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 
 struct TileRegs {
   u32x4_t k[8];      // K rows: chunk u = tid + 256 j -> row u/32, dims (u%32)*8
   u32x4_t v[4][2];   // V token pairs: unit u = tid + 256 j -> pair u%32, dims (u/32)*8
 };
+
+// Rows past the sequence end are loaded from the last valid row (a safe
+// address) and replaced by zeros with a select: no divergent branch around
+// the loads, so they all stay in flight together.
+__device__ __forceinline__ u32x4_t ld16_row_or_zero(const bf16_t *base, int64_t stride, int t,
+                                                    int n, int c) {
+  const int tc = t < n ? t : n - 1;
+  const u32x4_t x = ld16(base + int64_t(tc) * stride + c);
+  const u32x4_t z = {0u, 0u, 0u, 0u};
+  return t < n ? x : z;
+}
 
 __device__ __forceinline__ void load_tile(TileRegs &r, const bf16_t *kseq, int64_t ks_t,
                                           const bf16_t *vseq, int64_t vs_t, int kv0,
@@ -44,19 +57,14 @@ __device__ __forceinline__ void load_tile(TileRegs &r, const bf16_t *kseq, int64
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int u = tid + 256 * j;
-    const int row = u >> 5, c = (u & 31) * 8;
-    const int t = kv0 + row;
-    r.k[j] = t < n ? ld16(kseq + int64_t(t) * ks_t + c) : u32x4_t{0u, 0u, 0u, 0u};
+    r.k[j] = ld16_row_or_zero(kseq, ks_t, kv0 + (u >> 5), n, (u & 31) * 8);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int u = tid + 256 * j;
     const int tp = u & 31, c = (u >> 5) * 8;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int t = kv0 + 2 * tp + e;
-      r.v[j][e] = t < n ? ld16(vseq + int64_t(t) * vs_t + c) : u32x4_t{0u, 0u, 0u, 0u};
-    }
+    for (int e = 0; e < 2; ++e) r.v[j][e] = ld16_row_or_zero(vseq, vs_t, kv0 + 2 * tp + e, n, c);
   }
 }
 
@@ -77,9 +85,9 @@ __device__ __forceinline__ void store_tile(const TileRegs &r, bf16_t *sk, bf16_t
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const uint32_t a = r.v[j][0][w], b = r.v[j][1][w];
-      // dim c+2w: low halves; dim c+2w+1: high halves.
-      col[(2 * w) * (kVPitch / 2)] = (a & 0xffffu) | (b << 16);
-      col[(2 * w + 1) * (kVPitch / 2)] = (a >> 16) | (b & 0xffff0000u);
+      // dim c+2w: low halves of (a, b); dim c+2w+1: high halves (v_perm_b32).
+      col[(2 * w) * (kVPitch / 2)] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+      col[(2 * w + 1) * (kVPitch / 2)] = __builtin_amdgcn_perm(b, a, 0x07060302u);
     }
   }
 }
@@ -90,7 +98,8 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t *__restrict__ out,
     int64_t os_t, int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2) {
   extern __shared__ __align__(16) unsigned char smem[];
-  bf16_t *sk = reinterpret_cast<bf16_t *>(smem);
+  bf16_t *sq = reinterpret_cast<bf16_t *>(smem);
+  bf16_t *sk = sq + kG * kBQ * kKPitch;
   bf16_t *svt = sk + kBN * kKPitch;
 
   const int b = blockIdx.x, h = blockIdx.y;
@@ -108,15 +117,20 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
   const int hq = h * kG + wave;
   const int qrow = q0 + col;
 
-  // q row as the B operand of S^T, one 16-byte slice per 16-dim k-step.
-  bf16x8_t qb_op[16];
+  // The group's query rows (4 heads x 32 tokens) staged once in LDS; each
+  // 16-dim k-step of S^T reads its B-operand slice from there, which keeps
+  // the registers free for the accumulators and for read-ahead.
   {
-    const bf16_t *qp = q + (int64_t(start) + qrow) * qs_t + hq * qs_h + g * 8;
+    const bf16_t *qs = q + int64_t(start) * qs_t + h * kG * qs_h;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk)
-      qb_op[kk] = __builtin_bit_cast(
-          bf16x8_t, qrow < n ? ld16(qp + 16 * kk) : u32x4_t{0u, 0u, 0u, 0u});
+    for (int j = 0; j < 16; ++j) {
+      const int u = tid + 256 * j;            // 4096 chunks of 16 bytes
+      const int c = (u & 31) * 8, row = (u >> 5) & 31, hh = u >> 10;
+      st16(sq + (hh * kBQ + row) * kKPitch + c,
+           ld16_row_or_zero(qs + hh * qs_h, qs_t, q0 + row, n, c));
+    }
   }
+  const bf16_t *qrow_lds = sq + (wave * kBQ + col) * kKPitch + g * 8;
 
   f32x16_t o[8];
 #pragma unroll
@@ -145,11 +159,16 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) s[mt][e] = 0.f;
-      const bf16_t *krow = sk + (mt * 32 + col) * kKPitch + g * 8;
+    }
 #pragma unroll
-      for (int kk = 0; kk < 16; ++kk)
+    for (int kk = 0; kk < 16; ++kk) {
+      const bf16x8_t qb = __builtin_bit_cast(bf16x8_t, ld16(qrow_lds + 16 * kk));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const bf16_t *krow = sk + (mt * 32 + col) * kKPitch + g * 8;
         s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8_t, ld16(krow + 16 * kk)), qb_op[kk], s[mt], 0, 0, 0);
+            __builtin_bit_cast(bf16x8_t, ld16(krow + 16 * kk)), qb, s[mt], 0, 0, 0);
+      }
     }
 
     // ---- online softmax on the lane's row ------------------------------------
@@ -160,17 +179,22 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float x = s[mt][e] * qk_scale_log2;
-        if (need_mask) {
+        if (need_mask) {  // uniform branch; the per-element test is a select
           const int tok = kv0 + mt * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-          if (tok > qrow || tok >= n) x = -INFINITY;
+          x = (tok > qrow || tok >= n) ? -INFINITY : x;
         }
         s[mt][e] = x;
         mx = fmaxf(mx, x);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // Lazy rescaling: the running max moves only when the row max grows by
+    // more than 2^8, so P <= 256 and the O/l rescale (a pass over 128
+    // accumulators) is rare.  O/l is exact for any reference value m.
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+    const bool grow = m_new > m_run + kRescaleLog2;
+    const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    if (grow) m_run = m_new;
+    const float m_sub = m_run == -INFINITY ? 0.f : m_run;
     float psum = 0.f;
     u32x4_t pb[4];  // P^T B operands, k-steps 0..3 of the 64-token tile
 #pragma unroll
@@ -179,16 +203,18 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          const float a = exp2f(s[mt][8 * kk + 2 * w] - m_new);
-          const float c = exp2f(s[mt][8 * kk + 2 * w + 1] - m_new);
+          const float a = __builtin_amdgcn_exp2f(s[mt][8 * kk + 2 * w] - m_sub);
+          const float c = __builtin_amdgcn_exp2f(s[mt][8 * kk + 2 * w + 1] - m_sub);
           psum += a + c;
           pb[2 * mt + kk][w] = pack_bf16x2(a, c);
         }
     l_part = l_part * alpha + psum;
+    if (__any(grow)) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+      for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+    }
 
     // ---- O^T += V^T P^T --------------------------------------------------------
 #pragma unroll

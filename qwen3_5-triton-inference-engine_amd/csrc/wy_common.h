@@ -31,12 +31,17 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
+// Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even:
+// one v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 // Round a float to the nearest bf16 value and return it as float.
 __device__ __forceinline__ float round_bf16(float f) {
-  return __uint_as_float(f32_to_bf16_bits(f) << 16);
+  return __uint_as_float(pack_bf16x2(f, 0.f) << 16);
 }
 
 __device__ __forceinline__ u32x4_t ld16(const void *p) {
