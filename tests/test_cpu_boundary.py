@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "wy_attn.h"
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(wy_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|size_t|const char \*)\s*(wy_\w+)\(", text, re.M)))
 
 
 def test_header_declares_expected_entry_points():
@@ -50,7 +50,7 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
                                    dummy, dummy, s3, s4, 1, 8, 2, 128, 4, 4, None)
     assert rc == -4
     rc = lib.wy_varlen_causal_prefill(dummy, s3, dummy, s3, dummy, s3, dummy, s3, dummy,
-                                      1, 8, 2, 64, 16, None)
+                                      1, 8, 2, 64, 16, 16, dummy, 1 << 20, None)
     assert rc == -4
     rc = lib.wy_partial_rope(dummy, s4, dummy, s4, dummy, (ctypes.c_int64 * 2)(1, 1), 0,
                              dummy, 1, 1, 1, 256, 65, None)
