@@ -20,16 +20,21 @@
 // of V^T, one 16-byte LDS read.  Row max / sum are lane-local plus one xor-32
 // exchange.  Softmax in base 2 with 1/sqrt(D) folded into log2(e); P is
 // rounded to bf16 for PV as in the reference kernel
-// (gqa_attention_varlen_causal.py:146-203); the running max is moved lazily
-// (only when a row max grows by more than 2^8), exact after the final 1/l.
+// (gqa_attention_varlen_causal.py:146-203).  The exponentials use a per-row
+// reference fixed by the first KV tile instead of a running max, so O is
+// never rescaled inside the loop (exact after the final 1/l); a row whose
+// scores outgrow it by more than 2^64 sends the block through an exact
+// two-pass recomputation.
 //
 // K and V^T tiles travel global -> LDS with global_load_lds_dwordx4 (no
 // registers), double-buffered: tile t+1 is in flight while tile t is
-// consumed, one barrier per tile.  LDS rows are XOR-swizzled by 16-byte
-// chunk (chunk ^ (row & 7)) so the MFMA operand reads are conflict-free.
+// consumed, one barrier per tile.  LDS rows are padded by one 16-byte slot
+// so the MFMA operand reads are conflict-free.
 // Rows past a sequence's end are loaded from its last row (a safe address)
 // and masked in the scores; V^T past the end is zero from the pre-pass.
 // Query blocks are launched heaviest first (LPT): blockIdx.z counts down.
+#include <type_traits>
+
 #include "wy_common.h"
 
 using namespace wy;
@@ -40,11 +45,23 @@ constexpr int kD = 256;
 constexpr int kG = 4;
 constexpr int kBQ = 32;                  // query tokens per workgroup
 constexpr int kBN = 64;                  // kv tokens per tile
-constexpr int kTileK = kBN * kD * 2;     // bytes of one K tile  (32 KiB)
-constexpr int kTileV = kD * kBN * 2;     // bytes of one V^T tile (32 KiB)
-constexpr int kStage = kTileK + kTileV;  // one pipeline stage
-constexpr int kLdsBytes = 2 * kStage;    // double buffered: 128 KiB
-constexpr float kRescaleLog2 = 8.0f;     // lazy-rescale threshold (log2 units)
+// LDS rows carry one 16-byte pad slot: K rows are 32 + 1 slots (528 B), V^T
+// rows 8 + 1 slots (144 B).  Eight consecutive rows then start on eight
+// different 4-bank groups, so the MFMA operand reads are conflict-free, and
+// every k-step's operand sits at a constant offset from the lane's row.
+constexpr int kKSlots = kD / 8 + 1;      // 33 slots per K row
+constexpr int kVSlots = kBN / 8 + 1;     // 9 slots per V^T row
+constexpr int kKPitch = kKSlots * 16;    // 528 B
+constexpr int kVPitch = kVSlots * 16;    // 144 B
+constexpr int kTileK = kBN * kKPitch;    // 33792 B
+constexpr int kTileV = kD * kVPitch;     // 36864 B
+constexpr int kKDma = kTileK / 1024 + (kTileK % 1024 != 0);  // 1 KiB DMA blocks: 33
+constexpr int kVDma = kTileV / 1024;                          // 36
+constexpr int kLdsBytes = 2 * (kTileK + kVDma * 1024);  // two K + two V^T slots: 138 KiB
+// Exponentials are taken against a per-row reference fixed by the first KV
+// tile; a later score may exceed it by up to 2^kHeadroomLog2 (P stays finite
+// in bf16 and fp32).  Beyond that the block is recomputed exactly.
+constexpr float kHeadroomLog2 = 64.0f;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef const __attribute__((address_space(1))) void gbl_void_t;
@@ -102,7 +119,8 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const bf16_t *__restrict__
 }
 
 // ------------------------------------------------------------------ attention
-__global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h,
     const bf16_t *__restrict__ k, int64_t ks_t, int64_t ks_h,
     const bf16_t *__restrict__ vt, int64_t t_pad, bf16_t *__restrict__ out, int64_t os_t,
@@ -129,31 +147,63 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
   const int kv_end = min(q0 + kBQ, n);  // exclusive bound of keys any row can see
   const int n_tiles = (kv_end + kBN - 1) / kBN;
 
-  // Issue one tile's K and V^T (64 KiB) into stage `st`: 64 wave-wide 1 KiB
-  // DMA instructions, 16 per wave.
-  auto issue_tile = [&](int t, int st) {
-    unsigned char *sk = smem + st * kStage;
-    unsigned char *sv = sk + kTileK;
+  // LDS: a two-slot ring of K tiles, then a two-slot ring of V^T tiles.  K
+  // runs one tile ahead of V: iteration t computes S^T of tile t+1 (MFMA)
+  // while the VALU turns S^T of tile t into P, then runs PV of tile t.
+  unsigned char *const k_ring = smem;
+  unsigned char *const v_ring = smem + 2 * kTileK;
+
+  // DMA one tile into a ring slot as wave-wide 1 KiB blocks (lane j fills
+  // 16-byte slot 64*blk + j; pad slots get the row's first chunk, unread).
+  // Wave w issues blocks w, w+4, ...; the per-lane source offsets of those
+  // blocks are tile-invariant and computed once here.
+  constexpr int kKPerWave = (kKDma + 3) / 4;  // 9
+  constexpr int kVPerWave = kVDma / 4;        // 9
+  int k_tok[kKPerWave], k_cb[kKPerWave];      // token row within the tile, chunk byte offset
+  uint32_t v_off[kVPerWave];                  // byte offset of the lane's V^T chunk
+#pragma unroll
+  for (int i = 0; i < kKPerWave; ++i) {
+    const int sl = 64 * (wave + 4 * i) + lane;
+    const int row = sl / kKSlots;
+    const int c = sl - row * kKSlots;
+    k_tok[i] = k_row_token(row < kBN ? row : kBN - 1);
+    k_cb[i] = (c < kD / 8 ? c : 0) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < kVPerWave; ++i) {
+    const int sl = 64 * (wave + 4 * i) + lane;
+    const int dim = sl / kVSlots;
+    const int c = sl - dim * kVSlots;
+    v_off[i] = uint32_t(dim) * uint32_t(t_pad) * 2u + uint32_t(c < kBN / 8 ? c : 0) * 16u;
+  }
+  const int64_t k_row_bytes = ks_t * 2;
+  // Issue K blocks [i0, i1) of this wave for tile t into `slot`.
+  auto issue_k = [&](int t, int slot, int i0, int i1) {
     const int kv0 = t * kBN;
+    const unsigned char *src = reinterpret_cast<const unsigned char *>(kseq) + kv0 * k_row_bytes;
+    const int last_rel = n - 1 - kv0;  // rows past the end re-read the last row
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int blk = wave * 8 + i;          // 1 KiB block = K rows 2blk, 2blk+1
-      const int row = 2 * blk + (lane >> 5);
-      const int c = (lane & 31) ^ (row & 7); // global chunk stored at LDS chunk lane&31
-      int tok = kv0 + k_row_token(row);
-      tok = tok < n ? tok : n - 1;
-      lds_dma16(kseq + int64_t(tok) * ks_t + c * 8, sk + blk * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int blk = wave * 8 + i;          // 1 KiB block = V^T rows 8blk .. 8blk+7
-      const int dim = 8 * blk + (lane >> 3);
-      const int c = (lane & 7) ^ (dim & 7);
-      lds_dma16(vtseq + int64_t(dim) * t_pad + kv0 + c * 8, sv + blk * 1024);
+    for (int i = i0; i < i1; ++i) {
+      if (wave + 4 * i < kKDma) {
+        const int tr = min(k_tok[i], last_rel);
+        lds_dma16(src + tr * k_row_bytes + k_cb[i],
+                  k_ring + slot * kTileK + (wave + 4 * i) * 1024);
+      }
     }
   };
+  auto issue_v = [&](int t, int slot, int i0, int i1) {
+    const unsigned char *src = reinterpret_cast<const unsigned char *>(vtseq) + t * kBN * 2;
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+      lds_dma16(src + v_off[i], v_ring + slot * kVDma * 1024 + (wave + 4 * i) * 1024);
+  };
+  auto issue_first = [&] {
+    issue_k(0, 0, 0, kKPerWave);
+    issue_v(0, 0, 0, kVPerWave);
+    if (n_tiles > 1) issue_k(1, 1, 0, kKPerWave);
+  };
 
-  issue_tile(0, 0);
+  issue_first();
 
   // q row as the B operand of S^T, one 16-byte slice per 16-dim k-step.
   bf16x8_t qb_op[16];
@@ -168,95 +218,154 @@ __global__ __launch_bounds__(256) void varlen_causal_prefill_kernel(
     }
   }
 
-  f32x16_t o[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
-  float m_run = -INFINITY, l_part = 0.f;
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int kv0 = t * kBN;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA for tile t
-    __syncthreads();  // all of tile t landed; everyone is done with tile t-1
-    if (t + 1 < n_tiles) issue_tile(t + 1, (t + 1) & 1);
-    const unsigned char *sk = smem + (t & 1) * kStage;
-    const unsigned char *sv = sk + kTileK;
-
-    // ---- S^T for two 32-row slabs of the K tile -----------------------------
-    f32x16_t s[2];
+  // S^T of the tile in K slot `slot`: register r of slab mt = token 32mt+16g+r.
+  // dma(kb) is called after k-step block kb so the next tiles' DMA issue is
+  // spread between the MFMAs instead of stalling the wave in one burst.
+  auto qk = [&](int slot, f32x16_t(&sc)[2], auto &&dma) {
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[mt][e] = 0.f;
+      for (int e = 0; e < 16; ++e) sc[mt][e] = 0.f;
+    const unsigned char *kr = k_ring + slot * kTileK + col * kKPitch + g * 16;
+    u32x4_t ka[2][8];
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
+    for (int i = 0; i < 8; ++i) ka[0][i] = ld16(kr + (i & 1) * 32 * kKPitch + (i >> 1) * 32);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int cur = kb & 1;
+      if (kb + 1 < 4) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          ka[cur ^ 1][i] = ld16(kr + (i & 1) * 32 * kKPitch + (4 * (kb + 1) + (i >> 1)) * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, ka[cur][i]), qb_op[4 * kb + (i >> 1)], sc[i & 1], 0,
+            0, 0);
+      dma(kb);
+    }
+  };
+  auto no_dma = [](int) {};
+
+  f32x16_t o[8];
+  float l_part = 0.f;
+  float m_ref = 0.f;  // per-row reference max (log2 units) of the exponentials
+  const int row_lim = min(qrow, n - 1);  // last key this row may attend to
+
+  // One pass over the KV tiles.  kMode 0: m_ref = row max of the first tile
+  // (it always holds the row's first token), later tiles accumulate against
+  // it and only check that no score exceeds it by more than 2^kHeadroom;
+  // returns whether one did.  kMode 1: exact row max only (no PV).  kMode 2:
+  // accumulate against the exact m_ref of a preceding kMode-1 pass.
+  // There is no rescaling of O inside the loop.
+  auto run_pass = [&](auto mode) -> bool {
+    constexpr int kMode = decltype(mode)::value;
+    bool over = false;
+    float m_acc = -INFINITY;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    f32x16_t s_cur[2];
+    qk(0, s_cur, no_dma);
+    for (int t = 0; t < n_tiles; ++t) {
+      const int kv0 = t * kBN;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K(t+1), V(t) landed
+      __syncthreads();  // and every wave is done with S^T(t) and PV(t-1)
+      const bool k_next = t + 2 < n_tiles, v_next = t + 1 < n_tiles;  // uniform
+
+      // S^T of tile t+1 (on the last tile this reads a stale slot; unused),
+      // with the DMA of K(t+2) and V(t+1) issued between its k-steps.
+      f32x16_t s_nxt[2];
+      qk((t + 1) & 1, s_nxt, [&](int kb) {
+        if (kb == 0 && k_next) issue_k(t + 2, t & 1, 0, 5);
+        if (kb == 1 && k_next) issue_k(t + 2, t & 1, 5, kKPerWave);
+        if (kb == 2 && v_next) issue_v(t + 1, (t + 1) & 1, 0, 5);
+        if (kb == 3 && v_next) issue_v(t + 1, (t + 1) & 1, 5, kVPerWave);
+      });
+
+      // ---- P of tile t (VALU; overlaps the MFMAs above) -------------------
+      float mx = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
-        const int row = mt * 32 + col;
-        const u32x4_t a = ld16(sk + row * (kD * 2) + (((2 * kk + g) ^ (row & 7)) << 4));
-        s[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                        qb_op[kk], s[mt], 0, 0, 0);
-      }
-    }
-
-    // ---- online softmax on the lane's row ------------------------------------
-    // register r of slab mt holds token kv0 + 32mt + 16g + r
-    const bool need_mask = kv0 + kBN > q0 || kv0 + kBN > n;  // uniform
-    float mx = -INFINITY;
+        const int thr = row_lim - (kv0 + 32 * mt + 16 * g);  // keep registers e <= thr
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float x = s[mt][e] * qk_scale_log2;
-        if (need_mask) {
-          const int tok = kv0 + 32 * mt + 16 * g + e;
-          x = (tok > qrow || tok >= n) ? -INFINITY : x;
+        for (int e = 0; e < 16; ++e) {
+          const float x = e > thr ? -INFINITY : s_cur[mt][e] * qk_scale_log2;
+          s_cur[mt][e] = x;
+          mx = fmaxf(mx, x);
         }
-        s[mt][e] = x;
-        mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const bool grow = m_new > m_run + kRescaleLog2;
-    const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-    if (grow) m_run = m_new;
-    const float m_sub = m_run == -INFINITY ? 0.f : m_run;
-    float psum = 0.f;
-    u32x4_t pb[4];  // P^T B operands: k-step 2mt+kk = tokens 32mt+16g+8kk .. +7
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float a = __builtin_amdgcn_exp2f(s[mt][8 * kk + 2 * w] - m_sub);
-          const float c = __builtin_amdgcn_exp2f(s[mt][8 * kk + 2 * w + 1] - m_sub);
-          psum += a + c;
-          pb[2 * mt + kk][w] = pack_bf16x2(a, c);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if constexpr (kMode == 1) {
+        m_acc = fmaxf(m_acc, mx);
+      } else {
+        if constexpr (kMode == 0) {
+          m_ref = t == 0 ? mx : m_ref;
+          over |= mx > m_ref + kHeadroomLog2;
         }
-    l_part = l_part * alpha + psum;
-    if (__any(grow)) {
+        float psum = 0.f;
+        u32x4_t pb[4];  // P^T B operands: k-step 2mt+kk = tokens 32mt+16g+8kk .. +7
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-    }
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const float a = __builtin_amdgcn_exp2f(s_cur[mt][8 * kk + 2 * w] - m_ref);
+              const float c = __builtin_amdgcn_exp2f(s_cur[mt][8 * kk + 2 * w + 1] - m_ref);
+              psum += a + c;
+              pb[2 * mt + kk][w] = pack_bf16x2(a, c);
+            }
+        l_part += psum;
 
-    // ---- O^T += V^T P^T ------------------------------------------------------
+        // ---- O^T += V^T P^T of tile t ---------------------------------------
+        const unsigned char *vr = v_ring + (t & 1) * kVDma * 1024 + col * kVPitch + g * 32;
+        u32x4_t va[2][4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int dim = dt * 32 + col;
-      const unsigned char *vrow = sv + dim * (kBN * 2);
+        for (int ks = 0; ks < 4; ++ks) va[0][ks] = ld16(vr + (4 * (ks >> 1) + (ks & 1)) * 16);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int chunk = 4 * (ks >> 1) + 2 * g + (ks & 1);
-        const u32x4_t a = ld16(vrow + ((chunk ^ (dim & 7)) << 4));
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                        __builtin_bit_cast(bf16x8_t, pb[ks]),
-                                                        o[dt], 0, 0, 0);
+        for (int dt = 0; dt < 8; ++dt) {
+          const int cur = dt & 1;
+          if (dt + 1 < 8) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              va[cur ^ 1][ks] =
+                  ld16(vr + (dt + 1) * 32 * kVPitch + (4 * (ks >> 1) + (ks & 1)) * 16);
+          }
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+            // k-step ks = tokens 32(ks/2)+16g+8(ks%2) .. +7 = chunk 4(ks/2)+2g+ks%2
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, va[cur][ks]),
+                __builtin_bit_cast(bf16x8_t, pb[ks]), o[dt], 0, 0, 0);
+        }
       }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) s_cur[mt] = s_nxt[mt];
     }
+    if constexpr (kMode == 1) m_ref = m_acc;
+    return over;
+  };
+
+  auto zero_acc = [&] {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+    l_part = 0.f;
+  };
+
+  zero_acc();
+  const bool over = run_pass(std::integral_constant<int, 0>{});
+  if (__syncthreads_or(over)) {
+    // Cold path: some score exceeded the first tile's max by more than
+    // 2^kHeadroom.  Redo the block exactly: a max pass, then accumulation.
+    issue_first();
+    run_pass(std::integral_constant<int, 1>{});
+    __syncthreads();
+    issue_first();
+    zero_acc();
+    run_pass(std::integral_constant<int, 2>{});
   }
 
   // ---- normalise and store: lane holds row qrow, dims dt*32 + 8j + 4g + i -------
