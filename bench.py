@@ -88,8 +88,14 @@ def prefill_flops(lengths):
 
 # ------------------------------------------------------------------ timing
 
-def time_graph(fn, steps, warmup):
-    """Capture fn in a graph, replay warmup + steps; return ms per replay."""
+STEPS_PER_GRAPH = 8
+
+
+def time_graph(fn, steps, warmup, per_graph=STEPS_PER_GRAPH):
+    """Capture `per_graph` back-to-back calls of fn in one graph (as a decode
+    step graph holds every attention layer), replay it until `steps` calls
+    have run after `warmup` untimed ones; return ms per call, wall clock
+    bracketed by device synchronisation."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -97,15 +103,17 @@ def time_graph(fn, steps, warmup):
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
-    for _ in range(warmup):
+        for _ in range(per_graph):
+            fn()
+    for _ in range(max(1, warmup // per_graph)):
         g.replay()
     torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for _ in range(reps):
         g.replay()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    return (time.perf_counter() - t0) * 1e3 / (reps * per_graph)
 
 
 def time_events(fn, iters, warmup=3):
@@ -253,7 +261,8 @@ def main():
         "config": {"workload": "config2: paged GQA decode step B=32, L~U[128,2048], "
                                "8q/2kv heads, d=256, 16-token pages",
                    "global_batch": 32, "sum_context_tokens": sum(lens),
-                   "step": "one-launch append+split+merge+gate, HIP graph replay",
+                   "step": "one-launch append+split+merge+gate; 8 steps per HIP graph, "
+                           "as a decode graph holds every attention layer",
                    "parallelism": "single GPU"},
         "roofline": {"kernel": "paged_decode_split_kernel<true> (fused step)", "bound": "hbm",
                      "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -32,7 +32,7 @@
 // so the MFMA operand reads are conflict-free.
 // Rows past a sequence's end are loaded from its last row (a safe address)
 // and masked in the scores; V^T past the end is zero from the pre-pass.
-// Query blocks are launched heaviest first (LPT): blockIdx.z counts down.
+// Query blocks are launched heaviest first (LPT), spread over the XCDs.
 #include <type_traits>
 
 #include "wy_common.h"
@@ -124,11 +124,19 @@ void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h,
     const bf16_t *__restrict__ k, int64_t ks_t, int64_t ks_h,
     const bf16_t *__restrict__ vt, int64_t t_pad, bf16_t *__restrict__ out, int64_t os_t,
-    int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2) {
+    int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
+    int n_kv_heads, int n_qblocks) {
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const int b = blockIdx.x, h = blockIdx.y;
-  const int qb = gridDim.z - 1 - blockIdx.z;
+  // 1-D launch, heaviest query blocks first (LPT).  Workgroups are dealt to
+  // the 8 XCDs round-robin by id; rotating the (sequence, head) order by one
+  // per slice spreads every sequence over all XCDs instead of pinning it to
+  // XCD (b*H_kv + h) % 8.
+  const int bh_count = n_seq * n_kv_heads;
+  const int slice = blockIdx.x / bh_count;
+  const int bh = (blockIdx.x - slice * bh_count + slice) % bh_count;
+  const int b = bh / n_kv_heads, h = bh - b * n_kv_heads;
+  const int qb = n_qblocks - 1 - slice;
   const int start = cu[b];
   const int n = cu[b + 1] - start;
   const int q0 = qb * kBQ;
@@ -431,10 +439,12 @@ extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const 
   dim3 pgrid((max_seqlen + kBN - 1) / kBN, num_kv_heads, batch);
   vt_pack_kernel<<<pgrid, 256, 0, s>>>(static_cast<const bf16_t *>(v), vs[0], vs[1], vt, t_pad,
                                       cu_seqlens);
-  dim3 grid(batch, num_kv_heads, (max_seqlen + kBQ - 1) / kBQ);
-  varlen_causal_prefill_kernel<<<grid, 256, kLdsBytes, s>>>(
+  const int n_qblocks = (max_seqlen + kBQ - 1) / kBQ;
+  const int64_t n_wg = int64_t(n_qblocks) * batch * num_kv_heads;
+  if (n_wg > INT32_MAX) return WY_E_SHAPE;
+  varlen_causal_prefill_kernel<<<dim3(unsigned(n_wg)), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
       ks[1], vt, t_pad, static_cast<bf16_t *>(out), os[0], os[1], cu_seqlens,
-      kLog2e / sqrtf(float(head_dim)));
+      kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks);
   return wyh::launch_status();
 }
