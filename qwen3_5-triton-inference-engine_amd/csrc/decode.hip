@@ -9,9 +9,9 @@
 //     reads 16 bytes at dims 32i + 8g, so each instruction reads sixteen
 //     64-byte row segments; q (4 heads, rows 4..15 zero) is the A operand and
 //     8 MFMAs give the 4 x 16 score tile in lanes 0..15.
-//   * V is read row-contiguous (lane l: token 2i + l/32, dims (l%32)*8..+8)
-//     and P.V runs on the VALU in fp32 with P rounded to bf16, the rounding
-//     the reference applies before its PV dot.
+//   * V is read one 512-byte row per instruction (lane l: dims 4l..4l+3) and
+//     P.V runs on the VALU as v_dot2_f32_bf16 over token pairs, with P rounded
+//     to bf16 (the rounding the reference applies before its PV dot).
 //   * The softmax max/sum reduce across the 16 token lanes with xor shuffles.
 // After the page loop the four wave states merge through LDS and one fp32
 // (m, l, acc) triple per query head is written for the split.
@@ -68,19 +68,25 @@ __device__ __forceinline__ float readlane0(float v) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
-// Max / sum over each row of 16 lanes (lanes 0..15 hold the scores).
+// Max / sum over each row of 16 lanes (lanes 0..15 hold the scores): DPP
+// row rotations by 8, 4, 2, 1 leave the row result in every lane of the row.
+template <int kRor>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + kRor, 0xf, 0xf,
+                                                    false));
+}
 __device__ __forceinline__ float max16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1));
-  v = fmaxf(v, __shfl_xor(v, 2));
-  v = fmaxf(v, __shfl_xor(v, 4));
-  v = fmaxf(v, __shfl_xor(v, 8));
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
   return v;
 }
 __device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
   return v;
 }
 
@@ -188,7 +194,8 @@ __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lan
 template <bool kFused>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void paged_decode_split_kernel(const DecodeArgs a) {
-  __shared__ float4 sm_p[kWaves][kPage];         // bf16-rounded P, [token][head]
+  // bf16 P in token-pair layout: sm_p[wave][j][r] = (P[r][2j], P[r][2j+1]).
+  __shared__ u32x4_t sm_p[kWaves][kPage / 2];
   __shared__ float sm_ml[kWaves][2][kG];         // per-wave m, l
   __shared__ float4 sm_acc[kWaves][kG][kD / 4];  // per-wave unnormalised acc
   __shared__ int sm_last;
@@ -298,9 +305,13 @@ void paged_decode_split_kernel(const DecodeArgs a) {
       l_run[r] = l_run[r] * alpha[r] + ps;
       m_run[r] = m_new;
     }
-    if (lane < kPage)
-      sm_p[wave][lane] = make_float4(round_bf16(pr[0]), round_bf16(pr[1]),
-                                     round_bf16(pr[2]), round_bf16(pr[3]));
+    {
+      // even token lanes pair their P with the next token's (lane swap)
+      u32x4_t w;
+#pragma unroll
+      for (int r = 0; r < kG; ++r) w[r] = pack_bf16x2(pr[r], __shfl_xor(pr[r], 1));
+      if (lane < kPage && (lane & 1) == 0) sm_p[wave][lane >> 1] = w;
+    }
     __builtin_amdgcn_wave_barrier();
 
     // Rows past the sequence end may hold anything (even NaN): zero them so
@@ -315,22 +326,32 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     for (int r = 0; r < kG; ++r)
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[r][e] *= alpha[r];
+    // Token pairs (2j, 2j+1): P pairs come from LDS, V pairs per dim are
+    // assembled with v_perm_b32, and each (head, dim, pair) is one
+    // v_dot2_f32_bf16 (bf16 products summed in fp32).
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int i = 0; i < kPage; ++i) {
-      const float4 pv = sm_p[wave][i];
-      const float pw[kG] = {pv.x, pv.y, pv.z, pv.w};
-      u32x2_t vi = vr[i];
+    for (int j = 0; j < kPage / 2; ++j) {
+      const u32x4_t pp = sm_p[wave][j];
+      u32x2_t va = vr[2 * j], vb = vr[2 * j + 1];
       if constexpr (kFused) {
-        if (new_page && i == last_slot) vi = vnew;
+        if (new_page && 2 * j == last_slot) va = vnew;
+        if (new_page && 2 * j + 1 == last_slot) vb = vnew;
       }
-      const float v0 = bf16_lo(vi[0]), v1 = bf16_hi(vi[0]);
-      const float v2 = bf16_lo(vi[1]), v3 = bf16_hi(vi[1]);
+      const uint32_t vd[4] = {__builtin_amdgcn_perm(vb[0], va[0], 0x05040100u),
+                              __builtin_amdgcn_perm(vb[0], va[0], 0x07060302u),
+                              __builtin_amdgcn_perm(vb[1], va[1], 0x05040100u),
+                              __builtin_amdgcn_perm(vb[1], va[1], 0x07060302u)};
 #pragma unroll
       for (int r = 0; r < kG; ++r) {
-        acc[r][0] = fmaf(pw[r], v0, acc[r][0]);
-        acc[r][1] = fmaf(pw[r], v1, acc[r][1]);
-        acc[r][2] = fmaf(pw[r], v2, acc[r][2]);
-        acc[r][3] = fmaf(pw[r], v3, acc[r][3]);
+        // copy the lane out first: bit-casting an ext-vector element directly
+        // is lowered as a cast of element 0
+        const uint32_t pr_pair = pp[r];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[r][e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr_pair),
+                                                      __builtin_bit_cast(bf16x2_t, vd[e]),
+                                                      acc[r][e], false);
       }
     }
     __builtin_amdgcn_wave_barrier();
