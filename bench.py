@@ -264,7 +264,7 @@ def main():
                    "step": "one-launch append+split+merge+gate; 8 steps per HIP graph, "
                            "as a decode graph holds every attention layer",
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "paged_decode_split_kernel<true> (fused step)", "bound": "hbm",
+        "roofline": {"kernel": "paged_decode_split_kernel<true, 4> (fused step)", "bound": "hbm",
                      "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": step_bytes,

@@ -1,19 +1,25 @@
 // Paged GQA decode attention, split-K over 16-token pages (gfx950).
 //
-// Partial pass: one 256-thread workgroup per (sequence b, KV head h, split s).
-// The split's pages are dealt round-robin to the four wavefronts; each wave
+// Partial pass: one 4-wavefront workgroup per (sequence b, KV head h, split
+// s).  The split's pages are dealt round-robin to the wavefronts; each wave
 // keeps its own online-softmax state for the 4 query heads of the KV group, so
 // one read of a K/V page serves all 4 heads.  Per page and wave:
 //   * K (16 tokens x 256 dims) is loaded straight into the B operand of
 //     v_mfma_f32_16x16x32_bf16 -- lane (token n = l%16, dim group g = l/16)
-//     reads 16 bytes at dims 32i + 8g, so each instruction reads sixteen
-//     64-byte row segments; q (4 heads, rows 4..15 zero) is the A operand and
-//     8 MFMAs give the 4 x 16 score tile in lanes 0..15.
+//     reads 16 bytes at dims 32i + 8g; q (4 heads, rows 4..15 zero, re-read
+//     from LDS) is the A operand and 8 MFMAs give the 4 x 16 score tile in
+//     lanes 0..15.
 //   * V is read one 512-byte row per instruction (lane l: dims 4l..4l+3) and
 //     P.V runs on the VALU as v_dot2_f32_bf16 over token pairs, with P rounded
 //     to bf16 (the rounding the reference applies before its PV dot).
-//   * The softmax max/sum reduce across the 16 token lanes with xor shuffles.
-// After the page loop the four wave states merge through LDS and one fp32
+//   * The softmax max/sum reduce across the 16 token lanes with DPP row
+//     rotations.
+//   * Loads are software-pipelined in registers: K of the next page is
+//     requested once the score MFMAs have consumed this page's K, V of the
+//     next page once P.V has consumed this page's V.  Page loads are buffer
+//     loads from a per-page resource, block-table entries scalar loads issued
+//     one page ahead.
+// After the page loop the wave states merge through LDS and one fp32
 // (m, l, acc) triple per query head is written for the split.
 //
 // Merge pass: one wavefront per (b, query head) folds the active splits with
@@ -26,6 +32,8 @@
 // With min_pps = 1 this is exactly the reference partition
 // (gqa_attention_decode_paged.py:675-682, 779-784); a larger min_pps trades
 // split count for less fp32 scratch traffic.
+#include <type_traits>
+
 #include "wy_common.h"
 
 using namespace wy;
@@ -34,7 +42,7 @@ namespace {
 
 constexpr int kD = 256;   // head_dim
 constexpr int kG = 4;     // query heads per KV head
-constexpr int kWaves = 4; // wavefronts per workgroup
+constexpr int kWaves = 4; // wavefronts per split workgroup
 
 struct DecodeArgs {
   const bf16_t *q;
@@ -49,6 +57,7 @@ struct DecodeArgs {
   float scale;
   int min_pps;
   int hkv;
+  int batch;
   // fused step only
   const bf16_t *kn, *vn;
   int64_t kn_b, kn_h, vn_b, vn_h;
@@ -88,6 +97,12 @@ __device__ __forceinline__ float sum16(float v) {
   v += row_ror<2>(v);
   v += row_ror<1>(v);
   return v;
+}
+
+// Raw buffer resource over one cache page (bounds check off: the launcher has
+// validated the strides, and every offset stays inside the page).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const bf16_t *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(base), 0, -1, 0x00020000);
 }
 
 __device__ __forceinline__ float sigmoidf(float g) { return 1.0f / (1.0f + __expf(-g)); }
@@ -157,6 +172,12 @@ __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lan
   const float *mrow = a.mp + b * a.ml_b + hq * a.ml_h;
   const float *lrow = a.lp + b * a.ml_b + hq * a.ml_h;
   const float *arow = a.ap + b * a.a_b + hq * a.a_h + lane * 4;
+  // The first 8 accumulator rows are requested together with m and l, so a
+  // merge of up to 8 splits costs one memory round trip.
+  float4 x[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (u < nact) x[u] = ld_f4<kCoherent>(arow + u * a.a_s);
   const bool has0 = lane < nact, has1 = lane + 64 < nact;
   const float m0 = has0 ? ld_f<kCoherent>(mrow + lane * a.ml_s) : -INFINITY;
   const float m1 = has1 ? ld_f<kCoherent>(mrow + (lane + 64) * a.ml_s) : -INFINITY;
@@ -168,10 +189,11 @@ __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lan
   const float L = wave_sum(w0 * l0 + w1 * l1);
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = 0; s0 < nact; s0 += 8) {
-    float4 x[8];
+    if (s0 > 0) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (s0 + u < nact) x[u] = ld_f4<kCoherent>(arow + (s0 + u) * a.a_s);
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < nact) x[u] = ld_f4<kCoherent>(arow + (s0 + u) * a.a_s);
+    }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int sp = s0 + u;
@@ -191,26 +213,39 @@ __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lan
 // from k_new/v_new and writes them into their page (the append), and (ii)
 // lets the last workgroup of each (b, h) to finish merge all splits and write
 // the (optionally gated) output, so one launch is a whole decode step.
-template <bool kFused>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
-void paged_decode_split_kernel(const DecodeArgs a) {
-  // bf16 P in token-pair layout: sm_p[wave][j][r] = (P[r][2j], P[r][2j+1]).
-  __shared__ u32x4_t sm_p[kWaves][kPage / 2];
-  __shared__ float sm_ml[kWaves][2][kG];         // per-wave m, l
-  __shared__ float4 sm_acc[kWaves][kG][kD / 4];  // per-wave unnormalised acc
-  __shared__ int sm_last;
-  __shared__ __align__(16) bf16_t sm_q[kG][kD + 8];
+template <int kW>
+struct SplitLds {
+  u32x4_t p[kW][kPage / 2];      // bf16 P, token pairs: p[wave][j][r] = (P[r][2j], P[r][2j+1])
+  float ml[kW][2][kG];           // per-wave m, l
+  float4 acc[kW][kG][kD / 4];    // per-wave unnormalised acc
+  bf16_t q[kG][kD + 8];          // the group's query rows
+  int last;
+};
 
-  const int b = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+template <bool kFused, int kW>
+__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(4)))
+void paged_decode_split_kernel(const DecodeArgs a) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  SplitLds<kW> &sm = *reinterpret_cast<SplitLds<kW> *>(lds_raw);
+  auto &sm_p = sm.p;
+  auto &sm_ml = sm.ml;
+  auto &sm_acc = sm.acc;
+  auto &sm_q = sm.q;
+
+  // 1-D grid of batch * H_kv * max_splits workgroups, sequence index fastest.
+  // Splits past a sequence's end exit at once.
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x % a.batch;
+  const int h = (blockIdx.x / a.batch) % a.hkv;
+  const int s = blockIdx.x / (a.batch * a.hkv);
   const int seq_len = int(a.pos[b]) + 1;
   const int npg = (seq_len + kPage - 1) / kPage;
   const int pps = split_pps(npg, a.min_pps);
-  const int p0 = s * pps;
-  if (p0 >= npg) return;  // inactive split: uniform over the workgroup
-  const int p1 = min(p0 + pps, npg);
   const int nact = (npg + pps - 1) / pps;
+  if (s * pps >= npg) return;  // inactive split: uniform over the workgroup
+  const int p0 = s * pps;
+  const int p1 = min(p0 + pps, npg);
 
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
 
@@ -246,51 +281,109 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   const int32_t *btrow = a.bt + b * a.bt_b;
   const int last_page = (seq_len - 1) / kPage;
   const int last_slot = (seq_len - 1) % kPage;
+  const bf16_t *knrow = nullptr, *vnrow = nullptr;
+  if constexpr (kFused) {
+    knrow = a.kn + b * a.kn_b + h * a.kn_h;
+    vnrow = a.vn + b * a.vn_b + h * a.vn_h;
+  }
 
-  for (int p = p0 + wave; p < p1; p += kWaves) {
-    const int64_t phys = btrow[p];
-    const bf16_t *kp = kh + phys * a.kc_p + n16 * a.kc_s + g4 * 8;
-    const bf16_t *vp = vh + phys * a.vc_p + lane * 4;
-    const bool new_page = kFused && p == last_page;
-    const bf16_t *knrow = nullptr, *vnrow = nullptr;
-    if constexpr (kFused) {
-      if (new_page) {
-        knrow = a.kn + b * a.kn_b + h * a.kn_h;
-        vnrow = a.vn + b * a.vn_b + h * a.vn_h;
-        if (n16 == last_slot) kp = knrow + g4 * 8;  // the new token's key row
+  // This wave's pages are p0 + wave + i*kW, i < npw.  Their block-table
+  // entries are read with scalar loads (the table is constant during the
+  // launch), one page ahead, so a page's address never waits on the vector
+  // memory counter that its K/V loads share.
+  const int npw = p0 + wave < p1 ? (p1 - p0 - wave + kW - 1) / kW : 0;
+  typedef const __attribute__((address_space(4))) int32_t *bt_const_t;
+  const bt_const_t bt_s = (bt_const_t)btrow;
+  int32_t bt_ahead = npw > 0 ? bt_s[p0 + wave] : 0;
+  // Register pipeline, no extra registers: K of page i+1 is requested as soon
+  // as the score MFMAs have consumed K of page i, and V of page i+1 as soon as
+  // P.V has consumed V of page i, so each load overlaps the other half of the
+  // page's work.
+  u32x4_t kr[8];
+  u32x2_t vr[kPage];
+  int64_t phys_next = 0;
+  // Page loads are buffer loads off a per-page resource: one lane-offset
+  // register per operand and the row/column steps in the scalar offset.
+  const uint32_t k_voff = uint32_t(n16 * a.kc_s + g4 * 8) * 2u;
+  const uint32_t v_voff = uint32_t(lane) * 8u;
+  const int v_row_bytes = int(a.vc_s) * 2;
+  auto issue_k = [&](int i) {
+    phys_next = bt_ahead;
+    if (i + 1 < npw) bt_ahead = bt_s[p0 + wave + (i + 1) * kW];
+    const __amdgpu_buffer_rsrc_t rk = page_rsrc(kh + phys_next * a.kc_p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kr[e] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_voff, 64 * e, 0);
+  };
+  auto issue_v = [&](int i) {
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(vh + phys_next * a.vc_p);
+#pragma unroll
+    for (int e = 0; e < kPage; ++e)
+      vr[e] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, v_row_bytes * e, 0);
+  };
+
+  // Fused step: the wave whose pages end with the new token's page (always
+  // its final page) takes the new token from k_new / v_new, since the cached
+  // row at that slot is stale until the append below lands.  Its score column
+  // comes from the same 8 MFMAs run on the k_new row (each output element of
+  // the MFMA depends only on its own row and column, so the value is the one
+  // the page pass would produce from the cache), and v_new replaces that row
+  // of V.  All of it is fetched before the page loop.
+  f32x4_t sc_new = {0.f, 0.f, 0.f, 0.f};
+  u32x2_t vnew = {0u, 0u};
+  bool owns_new = false;
+  if constexpr (kFused) {
+    owns_new = p0 <= last_page && last_page < p1 && (last_page - p0) % kW == wave;
+    if (owns_new) {
+      u32x4_t kn[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kn[e] = ld16(knrow + g4 * 8 + 32 * e);
+      vnew = *reinterpret_cast<const u32x2_t *>(vnrow + lane * 4);
+      // the append: one 512-byte row of K (lanes 0..31) and V (32..63)
+      const int64_t phys = btrow[last_page];
+      const int c = (lane & 31) * 8;
+      if (lane < 32)
+        st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(knrow + c));
+      else
+        st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, ld16(vnrow + c));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const u32x4_t qw = n16 < kG ? ld16(&sm_q[n16 & 3][32 * e + 8 * g4])
+                                    : u32x4_t{0u, 0u, 0u, 0u};
+        sc_new = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qw),
+                                                         __builtin_bit_cast(bf16x8_t, kn[e]),
+                                                         sc_new, 0, 0, 0);
       }
     }
-    u32x4_t kr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = ld16(kp + 32 * i);
-    u32x2_t vr[kPage];
-#pragma unroll
-    for (int i = 0; i < kPage; ++i) vr[i] = *reinterpret_cast<const u32x2_t *>(vp + i * a.vc_s);
-    // the new token's value row (the cached row at that slot is stale)
-    u32x2_t vnew = {0u, 0u};
-    if constexpr (kFused) {
-      if (new_page) vnew = *reinterpret_cast<const u32x2_t *>(vnrow + lane * 4);
-    }
-    if constexpr (kFused) {
-      if (new_page) {  // the append: one 512-byte row of K (lanes 0..31) and V (32..63)
-        const int c = (lane & 31) * 8;
-        if (lane < 32)
-          st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(knrow + c));
-        else
-          st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, ld16(vnrow + c));
-      }
-    }
+  }
+
+  if (npw > 0) {
+    issue_k(0);
+    issue_v(0);
+  }
+
+  // One page of work; kMore: the wave has a next page whose loads to issue.
+  auto page = [&](int i, auto more) {
+    constexpr bool kMore = decltype(more)::value;
+    const int p = p0 + wave + i * kW;
+    const bool new_page = kFused && !kMore && owns_new;  // then p == last_page
 
     // ---- scores: 4 heads x 16 tokens in lanes 0..15 ------------------------
     f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+    // q is re-read from LDS for every page (the opaque offset keeps the
+    // compiler from hoisting 32 loop-invariant registers out of the loop).
+    uint32_t q_off = uint32_t(((n16 & 3) * (kD + 8) + 8 * g4) * 2);
+    asm volatile("" : "+v"(q_off));
+    const char *q_lds = reinterpret_cast<const char *>(&sm_q[0][0]) + q_off;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const u32x4_t qw = n16 < kG ? ld16(&sm_q[n16 & 3][32 * i + 8 * g4])
-                                  : u32x4_t{0u, 0u, 0u, 0u};
+    for (int e = 0; e < 8; ++e) {
+      const u32x4_t qw = n16 < kG ? ld16(q_lds + 64 * e) : u32x4_t{0u, 0u, 0u, 0u};
       sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qw),
-                                                   __builtin_bit_cast(bf16x8_t, kr[i]), sc,
+                                                   __builtin_bit_cast(bf16x8_t, kr[e]), sc,
                                                    0, 0, 0);
     }
+    if constexpr (kMore) issue_k(i + 1);
+    if (new_page && n16 == last_slot) sc = sc_new;
+
     const int valid_rows = seq_len - p * kPage;  // >= 1
     const bool valid = n16 < valid_rows;
     float pr[kG], alpha[kG];
@@ -318,8 +411,8 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     // 0 * garbage cannot reach the accumulator.
     if (valid_rows < kPage) {
 #pragma unroll
-      for (int i = 0; i < kPage; ++i)
-        if (i >= valid_rows) vr[i] = u32x2_t{0u, 0u};
+      for (int e = 0; e < kPage; ++e)
+        if (e >= valid_rows) vr[e] = u32x2_t{0u, 0u};
     }
     // ---- acc = acc * alpha + P V (lane: dims 4*lane..+3, all 16 tokens) ----------
 #pragma unroll
@@ -334,7 +427,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     for (int j = 0; j < kPage / 2; ++j) {
       const u32x4_t pp = sm_p[wave][j];
       u32x2_t va = vr[2 * j], vb = vr[2 * j + 1];
-      if constexpr (kFused) {
+      if constexpr (kFused && !kMore) {
         if (new_page && 2 * j == last_slot) va = vnew;
         if (new_page && 2 * j + 1 == last_slot) vb = vnew;
       }
@@ -355,6 +448,11 @@ void paged_decode_split_kernel(const DecodeArgs a) {
       }
     }
     __builtin_amdgcn_wave_barrier();
+    if constexpr (kMore) issue_v(i + 1);
+  };
+  if (npw > 0) {
+    for (int i = 0; i + 1 < npw; ++i) page(i, std::true_type{});
+    page(npw - 1, std::false_type{});
   }
 
   // ---- merge the four wave states through LDS ---------------------------------
@@ -370,26 +468,30 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   }
   __syncthreads();
 
-  const int r = wave;  // query head within the group handled by this wave
+  // waves 0..3 finish one query head each
+  const int r = wave & (kG - 1);
+  const bool head_wave = wave < kG;
   float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_ml[w][0][r]);
+  for (int w = 0; w < kW; ++w) M = fmaxf(M, sm_ml[w][0][r]);
   float L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const float e = __expf(sm_ml[w][0][r] - M);
-    L += e * sm_ml[w][1][r];
-    const float4 x = sm_acc[w][r][lane];
-    A.x += e * x.x;
-    A.y += e * x.y;
-    A.z += e * x.z;
-    A.w += e * x.w;
+  if (head_wave) {
+#pragma unroll 4
+    for (int w = 0; w < kW; ++w) {
+      const float e = __expf(sm_ml[w][0][r] - M);
+      L += e * sm_ml[w][1][r];
+      const float4 x = sm_acc[w][r][lane];
+      A.x += e * x.x;
+      A.y += e * x.y;
+      A.z += e * x.z;
+      A.w += e * x.w;
+    }
   }
   const int hq = h * kG + r;
   if constexpr (kFused) {
     if (nact == 1) {  // the only split: finish here, no scratch round trip
-      store_out4(a, b, hq, lane * 4, A, L);
+      if (head_wave) store_out4(a, b, hq, lane * 4, A, L);
       return;
     }
   }
@@ -397,20 +499,27 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   float *mdst = a.mp + b * a.ml_b + hq * a.ml_h + s * a.ml_s;
   float *ldst = a.lp + b * a.ml_b + hq * a.ml_h + s * a.ml_s;
   if constexpr (!kFused) {
-    *reinterpret_cast<float4 *>(adst) = A;
-    if (lane == 0) {
-      *mdst = M;
-      *ldst = L;
+    if (head_wave) {
+      *reinterpret_cast<float4 *>(adst) = A;
+      if (lane == 0) {
+        *mdst = M;
+        *ldst = L;
+      }
     }
   } else {
-    // Publish this split with device-coherent stores, wait for them to
-    // complete (workgroup-scope release), then count it.  The workgroup that
-    // brings the count to nact merges, reading the partials coherently.
-    st_coherent4(adst, A);
-    if (lane == 0) {
-      st_coherent(mdst, M);
-      st_coherent(ldst, L);
+    // Publish this split with device-coherent stores, wait until they have
+    // completed, then count it.  The workgroup that brings the count to nact
+    // merges, reading the partials coherently.  (A workgroup-scope release
+    // fence alone does not wait for the stores to complete on gfx950, hence
+    // the explicit vmcnt wait before the barrier.)
+    if (head_wave) {
+      st_coherent4(adst, A);
+      if (lane == 0) {
+        st_coherent(mdst, M);
+        st_coherent(ldst, L);
+      }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -419,10 +528,10 @@ void paged_decode_split_kernel(const DecodeArgs a) {
                                               __HIP_MEMORY_SCOPE_AGENT);
       const int last = done == nact - 1;
       if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sm_last = last;
+      sm.last = last;
     }
     __syncthreads();
-    if (!sm_last) return;
+    if (!sm.last || !head_wave) return;
     merge_head<true>(a, b, hq, nact, lane);
   }
 }
@@ -459,6 +568,30 @@ bool out_layout_ok(const void *out, const int64_t *os) {
 int split_grid_z(int max_pages, int min_pps) {
   const int z = (max_pages + min_pps - 1) / min_pps;
   return z > kMaxSplits ? kMaxSplits : z;
+}
+
+template <bool kFused, int kW>
+int launch_split_w(dim3 grid, const DecodeArgs &a, hipStream_t st) {
+  const size_t lds = sizeof(SplitLds<kW>);
+  auto *fn = paged_decode_split_kernel<kFused, kW>;
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(lds));
+    if (e != hipSuccess) return int(e);
+  }
+  fn<<<grid, 64 * kW, lds, st>>>(a);
+  return wyh::launch_status();
+}
+
+template <bool kFused>
+int launch_split(const DecodeArgs &args, int batch, int num_kv_heads, int max_pages, int min_pps,
+                 void *stream) {
+  DecodeArgs a = args;
+  a.batch = batch;
+  const dim3 grid(unsigned(batch) * unsigned(num_kv_heads) *
+                  unsigned(split_grid_z(max_pages, min_pps)));
+  return launch_split_w<kFused, kWaves>(grid, a, static_cast<hipStream_t>(stream));
 }
 
 DecodeArgs base_args(const void *q, const int64_t *qs, const void *k_cache,
@@ -522,9 +655,7 @@ extern "C" int wy_paged_decode_split(const void *q, const int64_t *qs, const voi
   const DecodeArgs a = base_args(q, qs, k_cache, v_cache, kcs, vcs, block_table, bt_stride0,
                                  pos, m_partial, l_partial, acc_partial, mls, as,
                                  num_kv_heads, head_dim, min_pages_per_split);
-  dim3 grid(batch, num_kv_heads, split_grid_z(max_pages, min_pages_per_split));
-  paged_decode_split_kernel<false><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
-  return wyh::launch_status();
+  return launch_split<false>(a, batch, num_kv_heads, max_pages, min_pages_per_split, stream);
 }
 
 extern "C" int wy_paged_decode_combine(const float *m_partial, const float *l_partial,
@@ -605,7 +736,5 @@ extern "C" int wy_paged_decode_step(const void *q, const int64_t *qs, const void
   a.o_b = os[0];
   a.o_h = os[1];
   a.o_d = os[2];
-  dim3 grid(batch, num_kv_heads, split_grid_z(max_pages, min_pages_per_split));
-  paged_decode_split_kernel<true><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
-  return wyh::launch_status();
+  return launch_split<true>(a, batch, num_kv_heads, max_pages, min_pages_per_split, stream);
 }

@@ -37,7 +37,7 @@ MAX_SPLITS = 128
 # more from fewer partials to merge (16 pages = 256 tokens).  Both ops derive
 # it from the batch size alone, a static shape, so the pair stays graph-safe.
 MIN_PAGES_PER_SPLIT = 4
-MIN_PAGES_PER_SPLIT_LARGE_BATCH = 16
+MIN_PAGES_PER_SPLIT_LARGE_BATCH = 32
 LARGE_BATCH = 16
 
 

@@ -136,7 +136,7 @@ def test_decode_oracle_uniform_keys_give_mean_of_v():
 
 
 @pytest.mark.parametrize("L", [1, 7, 64, 65, 200, 511, 2100, 4097])
-@pytest.mark.parametrize("min_pps", [1, 4, 16])
+@pytest.mark.parametrize("min_pps", [1, 4, 16, 32])
 def test_split_merge_equals_one_shot(L, min_pps):
     """gqa_attention_decode.py:1083-1097: split-K merge == one-shot softmax."""
     gen = torch.Generator().manual_seed(7)
