@@ -146,22 +146,17 @@ int wy_paged_decode_step(const void *q, const int64_t *q_strides, const void *k_
  *   out[t, hq, :] = softmax_{j<=i}(q_i . k_j / sqrt(D)) V  within each sequence
  * q/out [total, H_q, D], k/v [total, H_kv, D] bf16 (innermost stride must be
  * 1, rows 16-byte aligned).  max_seqlen is the host-side longest length and
- * total_tokens = q.shape[0].  workspace (16-byte aligned, at least
- * wy_varlen_causal_prefill_workspace_size() bytes, contents irrelevant) holds
- * V transposed per sequence for the PV product.
+ * total_tokens = q.shape[0].  Allocates nothing; one kernel launch.
  * Replaces wy_lib::gqa_attention_varlen_causal
  *   (triton_kernels/gqa_attention_varlen_causal.py:214-278, kernel :101-210).
  */
-size_t wy_varlen_causal_prefill_workspace_size(int64_t total_tokens, int batch,
-                                               int num_kv_heads, int head_dim);
 int wy_varlen_causal_prefill(const void *q, const int64_t *q_strides,
                              const void *k, const int64_t *k_strides,
                              const void *v, const int64_t *v_strides, void *out,
                              const int64_t *out_strides,
                              const int32_t *cu_seqlens, int batch,
                              int num_q_heads, int num_kv_heads, int head_dim,
-                             int max_seqlen, int64_t total_tokens, void *workspace,
-                             size_t workspace_bytes, void *stream);
+                             int max_seqlen, int64_t total_tokens, void *stream);
 
 /*
  * Partial rotate-half RoPE on dims [0, rotary_dim) of x [B, H, T, D] bf16;

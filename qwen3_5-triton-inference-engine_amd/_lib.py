@@ -35,14 +35,13 @@ _SIGNATURES = {
                              _c_i64p, _vp, _i64, _vp, _vp, _vp, _vp, _c_i64p, _c_i64p, _vp,
                              _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _i, _i, _i, _vp],
     "wy_varlen_causal_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
-                                 _vp, _i, _i, _i, _i, _i, _i64, _vp, ctypes.c_size_t, _vp],
+                                 _vp, _i, _i, _i, _i, _i, _i64, _vp],
     "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,
                         _i, _vp],
     "wy_attention_gate_pack": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _i, _vp],
 }
 
-EXPORTED = ("wy_status_string", "wy_build_info", "wy_varlen_causal_prefill_workspace_size",
-            *_SIGNATURES)
+EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)
 
 _lib: ctypes.CDLL | None = None
 
@@ -64,8 +63,6 @@ def load() -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     lib.wy_status_string.argtypes = [ctypes.c_int]
     lib.wy_status_string.restype = ctypes.c_char_p
-    lib.wy_varlen_causal_prefill_workspace_size.argtypes = [_i64, _i, _i, _i]
-    lib.wy_varlen_causal_prefill_workspace_size.restype = ctypes.c_size_t
     lib.wy_build_info.argtypes = []
     lib.wy_build_info.restype = ctypes.c_char_p
     _lib = lib

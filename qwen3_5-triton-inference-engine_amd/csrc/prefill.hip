@@ -1,38 +1,34 @@
 // Packed varlen causal GQA prefill attention on bf16 MFMA (gfx950).
 //
-// Two launches:
-//   1. vt_pack: V [total, H_kv, D] -> V^T workspace [H_kv, D, T_pad], each
-//      sequence's tokens at a 64-aligned offset pstart(b) = 64*(ceil(cu[b]/64)+b)
-//      and zero-filled up to the next multiple of 64.  This moves the
-//      transposition the PV product needs out of the attention loop.
-//   2. the attention kernel: one workgroup = 4 wavefronts on (sequence b,
-//      KV head h, 32-token query block); wave w owns query head 4h + w, so
-//      the four heads of the GQA group share every K/V tile in LDS.
+// One launch; one workgroup = 4 wavefronts on (sequence b, KV head h,
+// 32-token query block); wave w owns query head 4h + w, so the four heads of
+// the GQA group share every K/V tile in LDS.
 //
 // Attention is computed transposed so that a lane owns one query row:
 //   S^T = K Q^T      v_mfma_f32_32x32x16_bf16; A = K tile (LDS), B = q row
 //                    (lane%32) kept in registers for the whole kernel.
-//   O^T += V^T P^T   A = V^T tile (LDS), B = P^T taken straight from the S^T
-//                    accumulators.
+//   O^T += V^T P^T   A = V^T, read from the row-major V tile in LDS with
+//                    ds_read_b64_tr_b16 (the gfx950 transposing LDS read), B =
+//                    P^T taken straight from the S^T accumulators.
 // The K tile's LDS rows are a permutation of the 64 tokens, chosen so that
 // the S^T accumulator registers of lane (col, g) hold tokens 32mt + 16g + r
-// (r = register index 0..15): every PV k-step then reads 8 contiguous tokens
-// of V^T, one 16-byte LDS read.  Row max / sum are lane-local plus one xor-32
-// exchange.  Softmax in base 2 with 1/sqrt(D) folded into log2(e); P is
-// rounded to bf16 for PV as in the reference kernel
+// (r = register index 0..15): every PV k-step then needs 8 consecutive tokens
+// of V, two transposing reads of 4 tokens each.  Row max / sum are lane-local
+// plus one xor-32 exchange.  Softmax in base 2 with 1/sqrt(D) folded into
+// log2(e); P is rounded to bf16 for PV as in the reference kernel
 // (gqa_attention_varlen_causal.py:146-203).  The exponentials use a per-row
 // reference fixed by the first KV tile instead of a running max, so O is
 // never rescaled inside the loop (exact after the final 1/l); a row whose
 // scores outgrow it by more than 2^64 sends the block through an exact
 // two-pass recomputation.
 //
-// K and V^T tiles travel global -> LDS with global_load_lds_dwordx4 (no
+// K and V tiles travel global -> LDS with global_load_lds_dwordx4 (no
 // registers), double-buffered: tile t+1 is in flight while tile t is
-// consumed, one barrier per tile.  LDS rows are padded by one 16-byte slot
-// so the MFMA operand reads are conflict-free.
-// Rows past a sequence's end are loaded from its last row (a safe address)
-// and masked in the scores; V^T past the end is zero from the pre-pass.
-// Query blocks are launched heaviest first (LPT), spread over the XCDs.
+// consumed, one barrier per tile.  LDS rows are padded so the MFMA operand
+// reads are conflict-free.  Rows past a sequence's end are loaded from its
+// last row (a safe address): their scores are masked to -inf, so their P is
+// exactly 0.  Query blocks are launched heaviest first (LPT), spread over the
+// XCDs.
 #include <type_traits>
 
 #include "wy_common.h"
@@ -45,19 +41,20 @@ constexpr int kD = 256;
 constexpr int kG = 4;
 constexpr int kBQ = 32;                  // query tokens per workgroup
 constexpr int kBN = 64;                  // kv tokens per tile
-// LDS rows carry one 16-byte pad slot: K rows are 32 + 1 slots (528 B), V^T
-// rows 8 + 1 slots (144 B).  Eight consecutive rows then start on eight
-// different 4-bank groups, so the MFMA operand reads are conflict-free, and
-// every k-step's operand sits at a constant offset from the lane's row.
+// LDS rows are padded.  K rows are 32 + 1 16-byte slots (528 B): eight
+// consecutive rows start on eight different 4-bank groups, so the b128 MFMA
+// operand reads are conflict-free.  V rows are 32 + 4 slots (576 B): the four
+// rows one half-wave reads per transposing load start 16 banks apart.
 constexpr int kKSlots = kD / 8 + 1;      // 33 slots per K row
-constexpr int kVSlots = kBN / 8 + 1;     // 9 slots per V^T row
+constexpr int kVSlots = kD / 8 + 4;      // 36 slots per V row
 constexpr int kKPitch = kKSlots * 16;    // 528 B
-constexpr int kVPitch = kVSlots * 16;    // 144 B
+constexpr int kVPitch = kVSlots * 16;    // 576 B
 constexpr int kTileK = kBN * kKPitch;    // 33792 B
-constexpr int kTileV = kD * kVPitch;     // 36864 B
+constexpr int kTileV = kBN * kVPitch;    // 36864 B
 constexpr int kKDma = kTileK / 1024 + (kTileK % 1024 != 0);  // 1 KiB DMA blocks: 33
 constexpr int kVDma = kTileV / 1024;                          // 36
-constexpr int kLdsBytes = 2 * (kTileK + kVDma * 1024);  // two K + two V^T slots: 138 KiB
+static_assert(kTileV % 1024 == 0, "V tile is a whole number of DMA blocks");
+constexpr int kLdsBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 KiB
 // Exponentials are taken against a per-row reference fixed by the first KV
 // tile; a later score may exceed it by up to 2^kHeadroomLog2 (P stays finite
 // in bf16 and fp32).  Beyond that the block is recomputed exactly.
@@ -65,10 +62,8 @@ constexpr float kHeadroomLog2 = 64.0f;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef const __attribute__((address_space(1))) void gbl_void_t;
-
-__device__ __forceinline__ int64_t pstart(int cu_b, int b) {
-  return 64 * (int64_t((cu_b + 63) >> 6) + b);
-}
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
 // Token held by LDS row `row` of a K tile (see the header comment).
 __device__ __forceinline__ int k_row_token(int row) {
@@ -81,49 +76,13 @@ __device__ __forceinline__ void lds_dma16(const void *src, unsigned char *lds_ds
                                    (lds_void_t *)(lds_dst), 16, 0, 0);
 }
 
-// ------------------------------------------------------------------ V^T pack
-__global__ __launch_bounds__(256) void vt_pack_kernel(const bf16_t *__restrict__ v,
-                                                      int64_t vs_t, int64_t vs_h,
-                                                      bf16_t *__restrict__ vt, int64_t t_pad,
-                                                      const int32_t *__restrict__ cu) {
-  __shared__ bf16_t tile[kBN][kD + 2];
-  const int b = blockIdx.z, h = blockIdx.y, t0 = blockIdx.x * kBN;
-  const int start = cu[b], n = cu[b + 1] - start;
-  if (t0 >= n) return;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int u = tid + 256 * j;
-    const int row = u >> 5, c = (u & 31) * 8;
-    const int t = t0 + row;
-    const int tc = t < n ? t : n - 1;
-    u32x4_t x = ld16(v + (int64_t(start) + tc) * vs_t + h * vs_h + c);
-    if (t >= n) x = u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      *reinterpret_cast<uint32_t *>(&tile[row][c + 2 * w]) = x[w];
-    }
-  }
-  __syncthreads();
-  bf16_t *dst = vt + int64_t(h) * kD * t_pad + pstart(start, b) + t0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int u = tid + 256 * j;
-    const int dim = u >> 3, tc = (u & 7) * 8;
-    u32x4_t w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      w[e] = uint32_t(tile[tc + 2 * e][dim]) | (uint32_t(tile[tc + 2 * e + 1][dim]) << 16);
-    st16(dst + int64_t(dim) * t_pad + tc, w);
-  }
-}
-
 // ------------------------------------------------------------------ attention
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h,
     const bf16_t *__restrict__ k, int64_t ks_t, int64_t ks_h,
-    const bf16_t *__restrict__ vt, int64_t t_pad, bf16_t *__restrict__ out, int64_t os_t,
+    const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t *__restrict__ out,
+    int64_t os_t,
     int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
     int n_kv_heads, int n_qblocks) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -151,11 +110,11 @@ void varlen_causal_prefill_kernel(
   const int qrow = q0 + col;
 
   const bf16_t *kseq = k + int64_t(start) * ks_t + h * ks_h;
-  const bf16_t *vtseq = vt + int64_t(h) * kD * t_pad + pstart(start, b);
+  const bf16_t *vseq = v + int64_t(start) * vs_t + h * vs_h;
   const int kv_end = min(q0 + kBQ, n);  // exclusive bound of keys any row can see
   const int n_tiles = (kv_end + kBN - 1) / kBN;
 
-  // LDS: a two-slot ring of K tiles, then a two-slot ring of V^T tiles.  K
+  // LDS: a two-slot ring of K tiles, then a two-slot ring of V tiles.  K
   // runs one tile ahead of V: iteration t computes S^T of tile t+1 (MFMA)
   // while the VALU turns S^T of tile t into P, then runs PV of tile t.
   unsigned char *const k_ring = smem;
@@ -168,7 +127,7 @@ void varlen_causal_prefill_kernel(
   constexpr int kKPerWave = (kKDma + 3) / 4;  // 9
   constexpr int kVPerWave = kVDma / 4;        // 9
   int k_tok[kKPerWave], k_cb[kKPerWave];      // token row within the tile, chunk byte offset
-  uint32_t v_off[kVPerWave];                  // byte offset of the lane's V^T chunk
+  int v_tok[kVPerWave], v_cb[kVPerWave];
 #pragma unroll
   for (int i = 0; i < kKPerWave; ++i) {
     const int sl = 64 * (wave + 4 * i) + lane;
@@ -180,11 +139,13 @@ void varlen_causal_prefill_kernel(
 #pragma unroll
   for (int i = 0; i < kVPerWave; ++i) {
     const int sl = 64 * (wave + 4 * i) + lane;
-    const int dim = sl / kVSlots;
-    const int c = sl - dim * kVSlots;
-    v_off[i] = uint32_t(dim) * uint32_t(t_pad) * 2u + uint32_t(c < kBN / 8 ? c : 0) * 16u;
+    const int row = sl / kVSlots;
+    const int c = sl - row * kVSlots;
+    v_tok[i] = row;
+    v_cb[i] = (c < kD / 8 ? c : 0) * 16;
   }
   const int64_t k_row_bytes = ks_t * 2;
+  const int64_t v_row_bytes = vs_t * 2;
   // Issue K blocks [i0, i1) of this wave for tile t into `slot`.
   auto issue_k = [&](int t, int slot, int i0, int i1) {
     const int kv0 = t * kBN;
@@ -200,10 +161,14 @@ void varlen_causal_prefill_kernel(
     }
   };
   auto issue_v = [&](int t, int slot, int i0, int i1) {
-    const unsigned char *src = reinterpret_cast<const unsigned char *>(vtseq) + t * kBN * 2;
+    const int kv0 = t * kBN;
+    const unsigned char *src = reinterpret_cast<const unsigned char *>(vseq) + kv0 * v_row_bytes;
+    const int last_rel = n - 1 - kv0;
 #pragma unroll
-    for (int i = i0; i < i1; ++i)
-      lds_dma16(src + v_off[i], v_ring + slot * kVDma * 1024 + (wave + 4 * i) * 1024);
+    for (int i = i0; i < i1; ++i) {
+      const int tr = min(v_tok[i], last_rel);
+      lds_dma16(src + tr * v_row_bytes + v_cb[i], v_ring + slot * kTileV + (wave + 4 * i) * 1024);
+    }
   };
   auto issue_first = [&] {
     issue_k(0, 0, 0, kKPerWave);
@@ -260,6 +225,9 @@ void varlen_causal_prefill_kernel(
   float l_part = 0.f;
   float m_ref = 0.f;  // per-row reference max (log2 units) of the exponentials
   const int row_lim = min(qrow, n - 1);  // last key this row may attend to
+  const int l16 = lane & 15;
+  const uint32_t v_lane_off =
+      uint32_t((16 * g + (l16 >> 2)) * kVPitch + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2);
 
   // One pass over the KV tiles.  kMode 0: m_ref = row max of the first tile
   // (it always holds the row's first token), later tiles accumulate against
@@ -281,15 +249,17 @@ void varlen_causal_prefill_kernel(
       __syncthreads();  // and every wave is done with S^T(t) and PV(t-1)
       const bool k_next = t + 2 < n_tiles, v_next = t + 1 < n_tiles;  // uniform
 
-      // S^T of tile t+1 (on the last tile this reads a stale slot; unused),
-      // with the DMA of K(t+2) and V(t+1) issued between its k-steps.
+      // S^T of tile t+1 (none after the last tile), with the DMA of K(t+2)
+      // and V(t+1) issued between its k-steps.
       f32x16_t s_nxt[2];
-      qk((t + 1) & 1, s_nxt, [&](int kb) {
-        if (kb == 0 && k_next) issue_k(t + 2, t & 1, 0, 5);
-        if (kb == 1 && k_next) issue_k(t + 2, t & 1, 5, kKPerWave);
-        if (kb == 2 && v_next) issue_v(t + 1, (t + 1) & 1, 0, 5);
-        if (kb == 3 && v_next) issue_v(t + 1, (t + 1) & 1, 5, kVPerWave);
-      });
+      if (v_next) {
+        qk((t + 1) & 1, s_nxt, [&](int kb) {
+          if (kb == 0 && k_next) issue_k(t + 2, t & 1, 0, 5);
+          if (kb == 1 && k_next) issue_k(t + 2, t & 1, 5, kKPerWave);
+          if (kb == 2) issue_v(t + 1, (t + 1) & 1, 0, 5);
+          if (kb == 3) issue_v(t + 1, (t + 1) & 1, 5, kVPerWave);
+        });
+      }
 
       // ---- P of tile t (VALU; overlaps the MFMAs above) -------------------
       float mx = -INFINITY;
@@ -327,25 +297,34 @@ void varlen_causal_prefill_kernel(
         l_part += psum;
 
         // ---- O^T += V^T P^T of tile t ---------------------------------------
-        const unsigned char *vr = v_ring + (t & 1) * kVDma * 1024 + col * kVPitch + g * 32;
-        u32x4_t va[2][4];
+        // A operand of k-step ks = (mt, kk), dim block dt: lane (m = lane%32,
+        // g) needs V[32mt + 16g + 8kk + 0..7][32dt + m].  A transposing read
+        // hands lane i of each 16-lane group element i%4 of the 8-byte chunks
+        // addressed by lanes 4j + i/4 (j = 0..3), so lane L addresses token
+        // row 16g + L%16/4 (+4 for the second half) at dims 32dt + 16(L/16%2)
+        // + 4(L%4).
+        const unsigned char *vr = v_ring + (t & 1) * kTileV + v_lane_off;
+        auto vload = [&](int dt, int ks) {
+          const unsigned char *pv = vr + (32 * (ks >> 1) + 8 * (ks & 1)) * kVPitch + dt * 64;
+          const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(pv));
+          const bf16x4_t hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(pv + 4 * kVPitch));
+          return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        };
+        bf16x8_t va[2][4];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) va[0][ks] = ld16(vr + (4 * (ks >> 1) + (ks & 1)) * 16);
+        for (int ks = 0; ks < 4; ++ks) va[0][ks] = vload(0, ks);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           const int cur = dt & 1;
           if (dt + 1 < 8) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-              va[cur ^ 1][ks] =
-                  ld16(vr + (dt + 1) * 32 * kVPitch + (4 * (ks >> 1) + (ks & 1)) * 16);
+            for (int ks = 0; ks < 4; ++ks) va[cur ^ 1][ks] = vload(dt + 1, ks);
           }
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks)
-            // k-step ks = tokens 32(ks/2)+16g+8(ks%2) .. +7 = chunk 4(ks/2)+2g+ks%2
             o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8_t, va[cur][ks]),
-                __builtin_bit_cast(bf16x8_t, pb[ks]), o[dt], 0, 0, 0);
+                va[cur][ks], __builtin_bit_cast(bf16x8_t, pb[ks]), o[dt], 0, 0, 0);
         }
       }
 #pragma unroll
@@ -392,38 +371,23 @@ void varlen_causal_prefill_kernel(
   }
 }
 
-int64_t t_pad_for(int64_t total_tokens, int batch) {
-  return 64 * ((total_tokens + 63) / 64 + batch) + 64;
-}
-
 }  // namespace
-
-extern "C" size_t wy_varlen_causal_prefill_workspace_size(int64_t total_tokens, int batch,
-                                                          int num_kv_heads, int head_dim) {
-  if (total_tokens < 0 || batch < 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
-  return size_t(num_kv_heads) * size_t(head_dim) * size_t(t_pad_for(total_tokens, batch)) * 2;
-}
 
 extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const void *k,
                                         const int64_t *ks, const void *v,
                                         const int64_t *vs, void *out, const int64_t *os,
                                         const int32_t *cu_seqlens, int batch,
                                         int num_q_heads, int num_kv_heads, int head_dim,
-                                        int max_seqlen, int64_t total_tokens, void *workspace,
-                                        size_t workspace_bytes, void *stream) {
-  if (!q || !qs || !k || !ks || !v || !vs || !out || !os || !cu_seqlens || !workspace)
-    return WY_E_NULL;
+                                        int max_seqlen, int64_t total_tokens, void *stream) {
+  if (!q || !qs || !k || !ks || !v || !vs || !out || !os || !cu_seqlens) return WY_E_NULL;
   if (batch < 0 || num_kv_heads <= 0 || max_seqlen < 0 || total_tokens < 0)
     return WY_E_SHAPE;
   if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
   if (qs[2] != 1 || ks[2] != 1 || vs[2] != 1 || os[2] != 1 || qs[0] % 8 || qs[1] % 8 ||
       ks[0] % 8 || ks[1] % 8 || vs[0] % 8 || vs[1] % 8 || os[0] % 4 || os[1] % 4 ||
       !wyh::aligned16(q) || !wyh::aligned16(k) || !wyh::aligned16(v) ||
-      !wyh::aligned16(workspace) || (reinterpret_cast<uintptr_t>(out) & 7u))
+      (reinterpret_cast<uintptr_t>(out) & 7u))
     return WY_E_LAYOUT;
-  if (workspace_bytes <
-      wy_varlen_causal_prefill_workspace_size(total_tokens, batch, num_kv_heads, head_dim))
-    return WY_E_SHAPE;
   if (batch == 0 || max_seqlen == 0) return WY_OK;
   static bool attr_set = false;
   if (!attr_set) {
@@ -434,17 +398,13 @@ extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const 
     attr_set = true;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t t_pad = t_pad_for(total_tokens, batch);
-  bf16_t *vt = static_cast<bf16_t *>(workspace);
-  dim3 pgrid((max_seqlen + kBN - 1) / kBN, num_kv_heads, batch);
-  vt_pack_kernel<<<pgrid, 256, 0, s>>>(static_cast<const bf16_t *>(v), vs[0], vs[1], vt, t_pad,
-                                      cu_seqlens);
   const int n_qblocks = (max_seqlen + kBQ - 1) / kBQ;
   const int64_t n_wg = int64_t(n_qblocks) * batch * num_kv_heads;
   if (n_wg > INT32_MAX) return WY_E_SHAPE;
   varlen_causal_prefill_kernel<<<dim3(unsigned(n_wg)), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
-      ks[1], vt, t_pad, static_cast<bf16_t *>(out), os[0], os[1], cu_seqlens,
+      ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],
+      os[1], cu_seqlens,
       kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks);
   return wyh::launch_status();
 }

@@ -39,15 +39,11 @@ def gqa_attention_varlen_causal(
     assert cu_seqlens.is_contiguous()
 
     out = torch.empty_like(q)
-    ws_bytes = _lib.load().wy_varlen_causal_prefill_workspace_size(
-        total_tokens, batch, num_kv_head, d_model)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     _lib.call(
         "wy_varlen_causal_prefill",
         _lib.ptr(q), _lib.strides(q), _lib.ptr(k), _lib.strides(k), _lib.ptr(v),
         _lib.strides(v), _lib.ptr(out), _lib.strides(out), _lib.ptr(cu_seqlens), batch,
-        num_q_head, num_kv_head, d_model, max_seqlen, total_tokens, _lib.ptr(workspace),
-        ws_bytes, _lib.stream(q.device),
+        num_q_head, num_kv_head, d_model, max_seqlen, total_tokens, _lib.stream(q.device),
     )
     return out
 
