@@ -25,10 +25,10 @@
 // K and V tiles travel global -> LDS with global_load_lds_dwordx4 (no
 // registers), double-buffered: tile t+1 is in flight while tile t is
 // consumed, one barrier per tile.  LDS rows are padded so the MFMA operand
-// reads are conflict-free.  Rows past a sequence's end are loaded from its
-// last row (a safe address): their scores are masked to -inf, so their P is
-// exactly 0.  Query blocks are launched heaviest first (LPT), spread over the
-// XCDs.
+// reads are conflict-free.  The DMAs are buffer loads whose range ends at the
+// sequence's last row, so rows past the end are never fetched; their scores
+// are masked to -inf, so their P is exactly 0.  Query blocks are launched
+// heaviest first (LPT), spread over the XCDs.
 #include <type_traits>
 
 #include "wy_common.h"
@@ -56,14 +56,45 @@ constexpr int kVDma = kTileV / 1024;                          // 36
 static_assert(kTileV % 1024 == 0, "V tile is a whole number of DMA blocks");
 constexpr int kLdsBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 KiB
 // Exponentials are taken against a per-row reference fixed by the first KV
-// tile; a later score may exceed it by up to 2^kHeadroomLog2 (P stays finite
-// in bf16 and fp32).  Beyond that the block is recomputed exactly.
-constexpr float kHeadroomLog2 = 64.0f;
+// tile; a later score may exceed it by a factor up to 2^64 (P stays finite in
+// bf16 and fp32).  Beyond that the block is recomputed exactly.
+constexpr float kHeadroomScale = 18446744073709551616.0f;  // 2^64
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void gbl_void_t;
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+__device__ __forceinline__ uint32_t lds_u32(const unsigned char *p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) unsigned char *)(p)));
+}
+
+// ds_read_b64_tr_b16 (gfx950 transposing LDS read) as inline asm.  Issued
+// through the builtin, the compiler waits for every in-flight LDS DMA before
+// the read (it cannot tell the DMA targets from the tile being read), which
+// would expose the DMA latency once per tile.  The caller waits for the data
+// with lgkm_wait<N>(), which ties the destination registers so that nothing
+// reads them earlier.  LDS reads complete in order, so lgkmcnt(N) with N the
+// number of reads issued after the awaited ones is sufficient whatever other
+// LDS or scalar-memory operations are interleaved.
+template <int kOff>
+__device__ __forceinline__ u32x2_t ds_read_tr16(uint32_t lds_addr) {
+  u32x2_t r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds_addr), "i"(kOff));
+  return r;
+}
+template <int kN>
+__device__ __forceinline__ void lgkm_wait(u32x2_t (&a)[4], u32x2_t (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]),
+                 "+v"(b[2]), "+v"(b[3])
+               : "n"(kN));
+}
 
 // Token held by LDS row `row` of a K tile (see the header comment).
 __device__ __forceinline__ int k_row_token(int row) {
@@ -71,10 +102,6 @@ __device__ __forceinline__ int k_row_token(int row) {
   return 32 * mt + 16 * ((r >> 2) & 1) + 4 * (r >> 3) + (r & 3);
 }
 
-__device__ __forceinline__ void lds_dma16(const void *src, unsigned char *lds_dst) {
-  __builtin_amdgcn_global_load_lds((gbl_void_t *)(src),
-                                   (lds_void_t *)(lds_dst), 16, 0, 0);
-}
 
 // ------------------------------------------------------------------ attention
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -122,53 +149,55 @@ void varlen_causal_prefill_kernel(
 
   // DMA one tile into a ring slot as wave-wide 1 KiB blocks (lane j fills
   // 16-byte slot 64*blk + j; pad slots get the row's first chunk, unread).
-  // Wave w issues blocks w, w+4, ...; the per-lane source offsets of those
-  // blocks are tile-invariant and computed once here.
+  // Wave w issues blocks w, w+4, ...  The DMAs are buffer loads over the
+  // sequence's rows of this KV head: the per-lane row/chunk offsets are
+  // tile-invariant registers computed once here, the tile offset is scalar,
+  // and rows past the sequence's end fall outside the buffer's range (no
+  // clamping arithmetic, nothing fetched).  Keeping the address registers
+  // invariant also keeps the compiler from waiting on in-flight DMAs before
+  // reusing them.
   constexpr int kKPerWave = (kKDma + 3) / 4;  // 9
   constexpr int kVPerWave = kVDma / 4;        // 9
-  int k_tok[kKPerWave], k_cb[kKPerWave];      // token row within the tile, chunk byte offset
-  int v_tok[kVPerWave], v_cb[kVPerWave];
+  const uint32_t k_row_bytes = uint32_t(ks_t) * 2u;
+  const uint32_t v_row_bytes = uint32_t(vs_t) * 2u;
+  uint32_t k_voff[kKPerWave], v_voff[kVPerWave];
 #pragma unroll
   for (int i = 0; i < kKPerWave; ++i) {
     const int sl = 64 * (wave + 4 * i) + lane;
     const int row = sl / kKSlots;
     const int c = sl - row * kKSlots;
-    k_tok[i] = k_row_token(row < kBN ? row : kBN - 1);
-    k_cb[i] = (c < kD / 8 ? c : 0) * 16;
+    k_voff[i] = uint32_t(k_row_token(row < kBN ? row : kBN - 1)) * k_row_bytes +
+                uint32_t(c < kD / 8 ? c : 0) * 16u;
   }
 #pragma unroll
   for (int i = 0; i < kVPerWave; ++i) {
     const int sl = 64 * (wave + 4 * i) + lane;
     const int row = sl / kVSlots;
     const int c = sl - row * kVSlots;
-    v_tok[i] = row;
-    v_cb[i] = (c < kD / 8 ? c : 0) * 16;
+    v_voff[i] = uint32_t(row) * v_row_bytes + uint32_t(c < kD / 8 ? c : 0) * 16u;
   }
-  const int64_t k_row_bytes = ks_t * 2;
-  const int64_t v_row_bytes = vs_t * 2;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(kseq), 0, int(uint32_t(n - 1) * k_row_bytes + kD * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(vseq), 0, int(uint32_t(n - 1) * v_row_bytes + kD * 2), 0x00020000);
   // Issue K blocks [i0, i1) of this wave for tile t into `slot`.
   auto issue_k = [&](int t, int slot, int i0, int i1) {
-    const int kv0 = t * kBN;
-    const unsigned char *src = reinterpret_cast<const unsigned char *>(kseq) + kv0 * k_row_bytes;
-    const int last_rel = n - 1 - kv0;  // rows past the end re-read the last row
+    const uint32_t soff = uint32_t(t * kBN) * k_row_bytes;
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
-      if (wave + 4 * i < kKDma) {
-        const int tr = min(k_tok[i], last_rel);
-        lds_dma16(src + tr * k_row_bytes + k_cb[i],
-                  k_ring + slot * kTileK + (wave + 4 * i) * 1024);
-      }
+      if (wave + 4 * i < kKDma)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            k_rsrc, (lds_void_t *)(k_ring + slot * kTileK + (wave + 4 * i) * 1024), 16,
+            k_voff[i], soff, 0, 0);
     }
   };
   auto issue_v = [&](int t, int slot, int i0, int i1) {
-    const int kv0 = t * kBN;
-    const unsigned char *src = reinterpret_cast<const unsigned char *>(vseq) + kv0 * v_row_bytes;
-    const int last_rel = n - 1 - kv0;
+    const uint32_t soff = uint32_t(t * kBN) * v_row_bytes;
 #pragma unroll
-    for (int i = i0; i < i1; ++i) {
-      const int tr = min(v_tok[i], last_rel);
-      lds_dma16(src + tr * v_row_bytes + v_cb[i], v_ring + slot * kTileV + (wave + 4 * i) * 1024);
-    }
+    for (int i = i0; i < i1; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          v_rsrc, (lds_void_t *)(v_ring + slot * kTileV + (wave + 4 * i) * 1024), 16,
+          v_voff[i], soff, 0, 0);
   };
   auto issue_first = [&] {
     issue_k(0, 0, 0, kKPerWave);
@@ -176,9 +205,19 @@ void varlen_causal_prefill_kernel(
     if (n_tiles > 1) issue_k(1, 1, 0, kKPerWave);
   };
 
+  // V rows past the sequence's end are not fetched; their P is 0, so their
+  // LDS rows only need to hold finite values: zero the V ring once when the
+  // last tile is partial.
+  if (n < n_tiles * kBN) {
+    for (int o = tid * 16; o < 2 * kTileV; o += 256 * 16)
+      st16(v_ring + o, u32x4_t{0u, 0u, 0u, 0u});
+    __syncthreads();
+  }
   issue_first();
 
-  // q row as the B operand of S^T, one 16-byte slice per 16-dim k-step.
+  // q row as the B operand of S^T, one 16-byte slice per 16-dim k-step,
+  // pre-multiplied by scale*log2(e) and rounded to bf16 as the reference does
+  // (gqa_attention_varlen_causal.py:146,158): scores come out in log2 units.
   bf16x8_t qb_op[16];
   {
     const int qc = qrow < n ? qrow : n - 1;
@@ -187,6 +226,9 @@ void varlen_causal_prefill_kernel(
     for (int kk = 0; kk < 16; ++kk) {
       u32x4_t x = ld16(qp + 16 * kk);
       if (qrow >= n) x = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        x[w] = pack_bf16x2(bf16_lo(x[w]) * qk_scale_log2, bf16_hi(x[w]) * qk_scale_log2);
       qb_op[kk] = __builtin_bit_cast(bf16x8_t, x);
     }
   }
@@ -194,11 +236,11 @@ void varlen_causal_prefill_kernel(
   // S^T of the tile in K slot `slot`: register r of slab mt = token 32mt+16g+r.
   // dma(kb) is called after k-step block kb so the next tiles' DMA issue is
   // spread between the MFMAs instead of stalling the wave in one burst.
-  auto qk = [&](int slot, f32x16_t(&sc)[2], auto &&dma) {
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sc[mt][e] = 0.f;
+  // The accumulators start at `init` (0, or -m_ref once the row reference is
+  // known, so the MFMAs deliver s - m_ref directly).
+  auto qk = [&](int slot, f32x16_t(&sc)[2], const f32x16_t &init, auto &&dma) {
+    sc[0] = init;
+    sc[1] = init;
     const unsigned char *kr = k_ring + slot * kTileK + col * kKPitch + g * 16;
     u32x4_t ka[2][8];
 #pragma unroll
@@ -220,6 +262,9 @@ void varlen_causal_prefill_kernel(
     }
   };
   auto no_dma = [](int) {};
+  f32x16_t zero16;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) zero16[e] = 0.f;
 
   f32x16_t o[8];
   float l_part = 0.f;
@@ -230,57 +275,70 @@ void varlen_causal_prefill_kernel(
       uint32_t((16 * g + (l16 >> 2)) * kVPitch + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2);
 
   // One pass over the KV tiles.  kMode 0: m_ref = row max of the first tile
-  // (it always holds the row's first token), later tiles accumulate against
-  // it and only check that no score exceeds it by more than 2^kHeadroom;
-  // returns whether one did.  kMode 1: exact row max only (no PV).  kMode 2:
-  // accumulate against the exact m_ref of a preceding kMode-1 pass.
-  // There is no rescaling of O inside the loop.
-  auto run_pass = [&](auto mode) -> bool {
+  // (it always holds the row's first token); later tiles accumulate against
+  // it.  A later score may exceed it; if one does by more than a factor 2^64,
+  // the row sum l exceeds 2^64 and the caller redoes the block.
+  // kMode 1: exact row max only (no PV).  kMode 2: accumulate against the
+  // exact m_ref of a preceding kMode-1 pass.  There is no rescaling of O
+  // inside the loop.  Once m_ref is known, S^T tiles are computed with their
+  // accumulators started at -m_ref (tile 0 and 1 of kMode 0 subtract on the
+  // VALU), and only tiles that reach the diagonal are masked.
+  auto run_pass = [&](auto mode) {
     constexpr int kMode = decltype(mode)::value;
-    bool over = false;
     float m_acc = -INFINITY;
+    f32x16_t neg_m;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) neg_m[e] = -m_ref;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     f32x16_t s_cur[2];
-    qk(0, s_cur, no_dma);
+    qk(0, s_cur, kMode == 2 ? neg_m : zero16, no_dma);
     for (int t = 0; t < n_tiles; ++t) {
       const int kv0 = t * kBN;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K(t+1), V(t) landed
       __syncthreads();  // and every wave is done with S^T(t) and PV(t-1)
       const bool k_next = t + 2 < n_tiles, v_next = t + 1 < n_tiles;  // uniform
+      // s_cur holds s - m_ref (biased) or s
+      const bool biased = kMode == 2 || (kMode == 0 && t >= 2);
 
       // S^T of tile t+1 (none after the last tile), with the DMA of K(t+2)
       // and V(t+1) issued between its k-steps.
       f32x16_t s_nxt[2];
       if (v_next) {
-        qk((t + 1) & 1, s_nxt, [&](int kb) {
-          if (kb == 0 && k_next) issue_k(t + 2, t & 1, 0, 5);
-          if (kb == 1 && k_next) issue_k(t + 2, t & 1, 5, kKPerWave);
-          if (kb == 2) issue_v(t + 1, (t + 1) & 1, 0, 5);
-          if (kb == 3) issue_v(t + 1, (t + 1) & 1, 5, kVPerWave);
-        });
+        qk((t + 1) & 1, s_nxt, (kMode == 2 || (kMode == 0 && t >= 1)) ? neg_m : zero16,
+           [&](int kb) {
+             if (kb == 0 && k_next) issue_k(t + 2, t & 1, 0, 5);
+             if (kb == 1 && k_next) issue_k(t + 2, t & 1, 5, kKPerWave);
+             if (kb == 2) issue_v(t + 1, (t + 1) & 1, 0, 5);
+             if (kb == 3) issue_v(t + 1, (t + 1) & 1, 5, kVPerWave);
+           });
       }
 
       // ---- P of tile t (VALU; overlaps the MFMAs above) -------------------
-      float mx = -INFINITY;
+      if (kv0 + kBN - 1 > q0) {  // the tile reaches the diagonal: mask
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int thr = row_lim - (kv0 + 32 * mt + 16 * g);  // keep registers e <= thr
+        for (int mt = 0; mt < 2; ++mt) {
+          const int thr = row_lim - (kv0 + 32 * mt + 16 * g);  // keep registers e <= thr
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const float x = e > thr ? -INFINITY : s_cur[mt][e] * qk_scale_log2;
-          s_cur[mt][e] = x;
-          mx = fmaxf(mx, x);
+          for (int e = 0; e < 16; ++e) s_cur[mt][e] = e > thr ? -INFINITY : s_cur[mt][e];
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if constexpr (kMode == 1) {
-        m_acc = fmaxf(m_acc, mx);
-      } else {
-        if constexpr (kMode == 0) {
-          m_ref = t == 0 ? mx : m_ref;
-          over |= mx > m_ref + kHeadroomLog2;
+      if (kMode == 1 || (kMode == 0 && t == 0)) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[mt][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if constexpr (kMode == 1) m_acc = fmaxf(m_acc, mx);
+        else {
+          m_ref = mx;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) neg_m[e] = -mx;
         }
+      }
+      if constexpr (kMode != 1) {
+        const float sub = biased ? 0.f : m_ref;
         float psum = 0.f;
         u32x4_t pb[4];  // P^T B operands: k-step 2mt+kk = tokens 32mt+16g+8kk .. +7
 #pragma unroll
@@ -289,8 +347,8 @@ void varlen_causal_prefill_kernel(
           for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-              const float a = __builtin_amdgcn_exp2f(s_cur[mt][8 * kk + 2 * w] - m_ref);
-              const float c = __builtin_amdgcn_exp2f(s_cur[mt][8 * kk + 2 * w + 1] - m_ref);
+              const float a = __builtin_amdgcn_exp2f(s_cur[mt][8 * kk + 2 * w] - sub);
+              const float c = __builtin_amdgcn_exp2f(s_cur[mt][8 * kk + 2 * w + 1] - sub);
               psum += a + c;
               pb[2 * mt + kk][w] = pack_bf16x2(a, c);
             }
@@ -303,35 +361,39 @@ void varlen_causal_prefill_kernel(
         // addressed by lanes 4j + i/4 (j = 0..3), so lane L addresses token
         // row 16g + L%16/4 (+4 for the second half) at dims 32dt + 16(L/16%2)
         // + 4(L%4).
-        const unsigned char *vr = v_ring + (t & 1) * kTileV + v_lane_off;
-        auto vload = [&](int dt, int ks) {
-          const unsigned char *pv = vr + (32 * (ks >> 1) + 8 * (ks & 1)) * kVPitch + dt * 64;
-          const bf16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(pv));
-          const bf16x4_t hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)(pv + 4 * kVPitch));
-          return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        const uint32_t vr = lds_u32(v_ring + (t & 1) * kTileV) + v_lane_off;
+        u32x2_t vlo[2][4], vhi[2][4];
+        auto vload = [&](auto dtc, auto bufc) {
+          constexpr int dt = decltype(dtc)::value, buf = decltype(bufc)::value;
+          static_for<0, 4>([&](auto ksc) {
+            constexpr int ks = decltype(ksc)::value;
+            constexpr int off = (32 * (ks >> 1) + 8 * (ks & 1)) * kVPitch + dt * 64;
+            vlo[buf][ks] = ds_read_tr16<off>(vr);
+            vhi[buf][ks] = ds_read_tr16<off + 4 * kVPitch>(vr);
+          });
         };
-        bf16x8_t va[2][4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) va[0][ks] = vload(0, ks);
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const int cur = dt & 1;
-          if (dt + 1 < 8) {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) va[cur ^ 1][ks] = vload(dt + 1, ks);
+        vload(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+        static_for<0, 8>([&](auto dtc) {
+          constexpr int dt = decltype(dtc)::value, cur = dt & 1;
+          if constexpr (dt + 1 < 8) {
+            vload(std::integral_constant<int, dt + 1>{}, std::integral_constant<int, cur ^ 1>{});
+            lgkm_wait<8>(vlo[cur], vhi[cur]);  // this block's 8 reads have landed
+          } else {
+            lgkm_wait<0>(vlo[cur], vhi[cur]);
           }
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks)
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                va[cur][ks], __builtin_bit_cast(bf16x8_t, pb[ks]), o[dt], 0, 0, 0);
-        }
+          for (int ks = 0; ks < 4; ++ks) {
+            const u32x4_t a = {vlo[cur][ks][0], vlo[cur][ks][1], vhi[cur][ks][0], vhi[cur][ks][1]};
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                            __builtin_bit_cast(bf16x8_t, pb[ks]),
+                                                            o[dt], 0, 0, 0);
+          }
+        });
       }
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) s_cur[mt] = s_nxt[mt];
     }
     if constexpr (kMode == 1) m_ref = m_acc;
-    return over;
   };
 
   auto zero_acc = [&] {
@@ -343,20 +405,24 @@ void varlen_causal_prefill_kernel(
   };
 
   zero_acc();
-  const bool over = run_pass(std::integral_constant<int, 0>{});
+  run_pass(std::integral_constant<int, 0>{});
+  float l = l_part + __shfl_xor(l_part, 32);
+  // Some score exceeded its row's first-tile maximum by a factor over 2^64
+  // (or is not finite): l is then at least 2^64.
+  const bool over = qrow < n && !(l < kHeadroomScale);
   if (__syncthreads_or(over)) {
     // Cold path: some score exceeded the first tile's max by more than
-    // 2^kHeadroom.  Redo the block exactly: a max pass, then accumulation.
+    // 2^64.  Redo the block exactly: a max pass, then accumulation.
     issue_first();
     run_pass(std::integral_constant<int, 1>{});
     __syncthreads();
     issue_first();
     zero_acc();
     run_pass(std::integral_constant<int, 2>{});
+    l = l_part + __shfl_xor(l_part, 32);
   }
 
   // ---- normalise and store: lane holds row qrow, dims dt*32 + 8j + 4g + i -------
-  const float l = l_part + __shfl_xor(l_part, 32);
   const float inv_l = 1.0f / l;
   if (qrow < n) {
     bf16_t *op = out + (int64_t(start) + qrow) * os_t + hq * os_h;
@@ -401,6 +467,9 @@ extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const 
   const int n_qblocks = (max_seqlen + kBQ - 1) / kBQ;
   const int64_t n_wg = int64_t(n_qblocks) * batch * num_kv_heads;
   if (n_wg > INT32_MAX) return WY_E_SHAPE;
+  // per-sequence DMA ranges are 32-bit byte offsets
+  if (int64_t(max_seqlen) * ks[0] * 2 >= INT32_MAX || int64_t(max_seqlen) * vs[0] * 2 >= INT32_MAX)
+    return WY_E_SHAPE;
   varlen_causal_prefill_kernel<<<dim3(unsigned(n_wg)), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
       ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],

@@ -393,6 +393,28 @@ def test_prefill_vs_oracle(pkg, dev, lengths):
     close(out, orc.varlen_causal(q, k, v, cu), what=f"prefill {lengths}")
 
 
+def test_prefill_exact_fallback(pkg, dev):
+    """Rows whose later scores exceed the first KV tile's maximum by more than
+    2^64 (log2 units > 64) take the kernel's exact two-pass path; rows before
+    the outlier key and the second sequence take the one-pass path."""
+    say("prefill exact fallback")
+    gen = torch.Generator().manual_seed(41)
+    lengths = [200, 70]
+    total = sum(lengths)
+    q, k, v = bf((total, HQ, D), gen), bf((total, HKV, D), gen), bf((total, HKV, D), gen)
+    q[:200] = 1.0
+    k[:200] = (k[:200].float() * 0.05).to(torch.bfloat16)
+    k[130, :, :] = 4.0  # q.k = 1024 -> score 64 * log2(e) = 92 above tile 0
+    cu = torch.tensor([0, 200, 270], dtype=torch.int32)
+    out = pkg.gqa_attention_varlen_causal(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), 200)
+    ref = orc.varlen_causal(q, k, v, cu)
+    close(out, ref, what="prefill fallback")
+    # rows from 130 on attend almost only to token 130
+    torch.testing.assert_close(out[140:200].float().cpu(),
+                               v[130].float().repeat_interleave(4, 0).expand(60, HQ, D),
+                               atol=2e-2, rtol=0)
+
+
 def test_prefill_strided_inputs(pkg, dev):
     """q/k/v as row-strided views (stride_t != H*D) are addressed correctly."""
     say("prefill strided")
