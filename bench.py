@@ -143,14 +143,20 @@ def time_graph_events(fn, iters):
     with torch.cuda.graph(g):
         for _ in range(iters):
             fn()
-    g.replay()
-    torch.cuda.synchronize()
+    # bring the clocks to their loaded steady state first (~0.3 s of replays)
+    t_end = time.perf_counter() + 0.3
+    while True:
+        g.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() > t_end:
+            break
     st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     st.record()
-    g.replay()
+    for _ in range(3):
+        g.replay()
     en.record()
     en.synchronize()
-    return st.elapsed_time(en) / iters
+    return st.elapsed_time(en) / (3 * iters)
 
 
 # ------------------------------------------------------------------ main
@@ -159,7 +165,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed steps first")
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
     ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill"],
