@@ -286,6 +286,25 @@ def main():
     def want(name):
         return not args.quick and (not only or name in only)
 
+    # ---- config 2 as the whole attention block: from the fused projection
+    # output (q/k RMSNorm + partial RoPE in the same launch) ----------------------
+    if want("block"):
+        gen_b = torch.Generator(device=dev).manual_seed(7)
+        fused = torch.randn(32, 5120, device=dev, generator=gen_b).to(torch.bfloat16)
+        qw = (torch.randn(D, device=dev, generator=gen_b) * 0.3).to(torch.bfloat16)
+        kw = (torch.randn(D, device=dev, generator=gen_b) * 0.3).to(torch.bfloat16)
+        inv = pkg.rope_inv_freq(64, 1e7, device=dev)
+
+        def block():
+            return pkg.decode_attention_block(fused, qw, kw, 1e-6, inv, 64, w["pos"], w["kc"],
+                                              w["vc"], w["bt"], scratch)
+
+        msb = time_graph(block, args.steps, args.warmup)
+        extra["config2_attention_block"] = {
+            "us_per_step": round(msb * 1e3, 2),
+            "what": "fused q/gate/k/v projection output -> o_proj input in one launch "
+                    "(q/k RMSNorm, partial RoPE, append, split-K, merge, gate)"}
+
     # ---- config 1: B=1, 256 tokens, contiguous table --------------------------
     if want("c1"):
         w1 = decode_workload([256], dev, seed=1, contiguous=True)

@@ -184,6 +184,50 @@ int wy_attention_gate_pack(const void *x, const int64_t *x_strides,
                            void *out, int num_heads, int num_tokens,
                            int head_dim, void *stream);
 
+/*
+ * Per-row RMSNorm with a (1 + w) weight:
+ *   out[b, m, :] = bf16(x * rsqrt(mean(x^2) + eps) * (1 + weight))  (fp32 math)
+ * x [batch, rows, d_model] bf16 with strides x_strides (innermost 1, rows
+ * 16-byte aligned); weight [d_model] bf16; out [batch, rows, d_model] with
+ * out_strides.  d_model a multiple of 256.
+ * Replaces wy_lib::qwen_rmsnorm
+ *   (triton_kernels/qwen_rmsnorm.py:92-147, kernel :28-90).
+ */
+int wy_qwen_rmsnorm(const void *x, const int64_t *x_strides, const void *weight,
+                    void *out, const int64_t *out_strides, int batch, int rows,
+                    int d_model, float eps, void *stream);
+
+/*
+ * Decode attention block in one launch: from the fused projection's raw
+ * q / gate / k / v slices to the gated, head-packed attention output.
+ *   q = rope(rmsnorm(q_raw, q_norm_weight)), k = rope(rmsnorm(k_raw, k_norm_weight))
+ *   at position pos[b] on dims [0, rotary_dim), v = v_raw; append k, v at pos;
+ *   split-K attention + merge; out = bf16(bf16(ctx) * sigmoid(gate)).
+ * q_raw, gate [B, H_q, D] and k_raw, v_raw [B, H_kv, D] bf16 with any row
+ * strides (innermost 1), e.g. views of the [B, 5120] projection output;
+ * weights [D] bf16; inv_freq [rotary_dim/2] fp32; rotary_dim <= 128, a multiple of
+ * 16.  Caches, table, scratch and counters as wy_paged_decode_step; out
+ * [B, H_q, D] (the packed [B, H_q*D] row when contiguous).  Bit-identical to
+ * wy_qwen_rmsnorm + wy_partial_rope + wy_paged_decode_step in sequence.
+ * Replaces the sequence qwen_rmsnorm(q), qwen_rmsnorm(k), partial_rope(q),
+ * partial_rope(k), call_paged_gqa_attention_decode_triton, attention_gate_pack
+ * of engine/runner.py:476-517.
+ */
+int wy_paged_decode_block(const void *q_raw, const int64_t *q_strides, const void *gate,
+                          const int64_t *gate_strides, const void *k_raw,
+                          const int64_t *k_strides, const void *v_raw,
+                          const int64_t *v_strides, const void *q_norm_weight,
+                          const void *k_norm_weight, float eps, const float *inv_freq,
+                          int rotary_dim, void *k_cache, void *v_cache,
+                          const int64_t *kc_strides, const int64_t *vc_strides,
+                          const int32_t *block_table, int64_t bt_stride0,
+                          const int64_t *pos, float *m_partial, float *l_partial,
+                          float *acc_partial, const int64_t *ml_strides,
+                          const int64_t *acc_strides, int32_t *counters, void *out,
+                          const int64_t *out_strides, int batch, int num_q_heads,
+                          int num_kv_heads, int head_dim, int max_pages,
+                          int min_pages_per_split, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,8 @@ PINNED = {
     "partial_rope": "HF transformers qwen3_5 apply_rotary_pos_emb with fp32 cos/sin; "
                     "pos 0 identity; norm preservation; tail bit-exact",
     "gate_pack": "gate=0 -> x/2 exactly; large gate -> x; layout by index identity",
+    "qwen_rmsnorm": "pure-Python brute force (math.sqrt); power-of-two scale invariance; "
+                    "constant rows -> (1+w)*sign; weight 0 -> unit RMS",
 }
 
 
@@ -189,6 +191,14 @@ def partial_rope(x, position_ids, inv_freq, rotary_dim: int) -> torch.Tensor:
     out[..., :half] = (x1 * cos - x2 * sin).to(x.dtype)
     out[..., half:rotary_dim] = (x1 * sin + x2 * cos).to(x.dtype)
     return out
+
+
+def qwen_rmsnorm(x, weight, eps: float) -> torch.Tensor:
+    """bf16 ``x * rsqrt(mean(x^2) + eps) * (1 + weight)`` over the last dim in
+    fp32 (qwen_rmsnorm.py:69-73, torch version :165-174)."""
+    xf = x.float()
+    ms = (xf * xf).mean(dim=-1, keepdim=True)
+    return (xf * torch.rsqrt(ms + eps) * (1.0 + weight.float())).to(x.dtype)
 
 
 def gate_pack(x, gate) -> torch.Tensor:

@@ -14,6 +14,7 @@ from . import _lib
 from .attention import (
     PackedBatch,
     build_packed_batch,
+    decode_attention_block,
     decode_attention_step,
     prefill_attention_packed,
 )
@@ -27,6 +28,7 @@ from .gqa_attention_decode_paged import (
     allocate_split_scratch,
     call_paged_gqa_attention_decode_triton,
     SplitScratch,
+    paged_gqa_attention_decode_block,
     paged_gqa_attention_decode_combine,
     paged_gqa_attention_decode_fused,
     paged_gqa_attention_decode_split,
@@ -38,18 +40,20 @@ from .gqa_attention_decode_paged import (
 from .gqa_attention_varlen_causal import build_cu_seqlens, gqa_attention_varlen_causal
 from .paging import PagePool, SequencePages, allocate_block_table
 from .partial_rope import partial_rope, rope_inv_freq
+from .qwen_rmsnorm import call_qwen_rmsnorm_triton, qwen_rmsnorm
 
 
 def install_as_triton_kernels() -> None:
     """Alias the reference module paths (``triton_kernels.<op>`` and
     ``engine.paging``) to this package's modules in ``sys.modules``."""
     from . import (attention_gate_pack, gqa_attention_decode_paged,
-                   gqa_attention_varlen_causal, paging, partial_rope)
+                   gqa_attention_varlen_causal, paging, partial_rope, qwen_rmsnorm)
     for name, mod in (
         ("triton_kernels.gqa_attention_decode_paged", gqa_attention_decode_paged),
         ("triton_kernels.gqa_attention_varlen_causal", gqa_attention_varlen_causal),
         ("triton_kernels.partial_rope", partial_rope),
         ("triton_kernels.attention_gate_pack", attention_gate_pack),
+        ("triton_kernels.qwen_rmsnorm", qwen_rmsnorm),
         ("engine.paging", paging),
     ):
         sys.modules[name] = mod

@@ -19,6 +19,7 @@ _c_i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
+_f = ctypes.c_float
 
 # name -> argtypes (all return int status)
 _SIGNATURES = {
@@ -39,6 +40,11 @@ _SIGNATURES = {
     "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,
                         _i, _vp],
     "wy_attention_gate_pack": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _i, _vp],
+    "wy_qwen_rmsnorm": [_vp, _c_i64p, _vp, _vp, _c_i64p, _i, _i, _i, _f, _vp],
+    "wy_paged_decode_block": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
+                              _vp, _f, _vp, _i, _vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp,
+                              _vp, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _i, _i,
+                              _i, _i, _i, _i, _vp],
 }
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)
@@ -74,6 +80,10 @@ def strides(t):
         return None
     s = t.stride()
     return (ctypes.c_int64 * len(s))(*s)
+
+
+def i64_array(values):
+    return (ctypes.c_int64 * len(values))(*values)
 
 
 def ptr(t):

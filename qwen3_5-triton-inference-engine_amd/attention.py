@@ -24,6 +24,7 @@ import torch
 from .attention_gate_pack import attention_gate_pack
 from .gqa_attention_decode_paged import (
     call_paged_gqa_attention_decode_triton,
+    paged_gqa_attention_decode_block,
     paged_gqa_attention_decode_fused,
     paged_kv_fill_varlen,
 )
@@ -159,3 +160,39 @@ def decode_attention_step(
     gate4 = gate.reshape(batch, nh, d).permute(1, 0, 2).unsqueeze(0).contiguous()
     ctx4 = ctx.permute(1, 0, 2).unsqueeze(0).contiguous()
     return attention_gate_pack(ctx4, gate4)
+
+
+def decode_attention_block(
+    fused: torch.Tensor,
+    q_norm: torch.Tensor,
+    k_norm: torch.Tensor,
+    eps: float,
+    inv_freq: torch.Tensor,
+    rotary_dim: int,
+    pos: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    scratch,
+    num_heads: int = 8,
+    num_kv_heads: int = 2,
+    head_dim: int = 256,
+) -> torch.Tensor:
+    """The decode attention of one layer from the fused q/gate/k/v projection
+    output ``fused [B, 2*Hq*D + 2*Hkv*D]`` (engine/runner.py:462-517) to the
+    ``[B, Hq*D]`` o_proj input, in one launch: the slices are passed as
+    strided views, no copies.  ``scratch`` must carry merge counters
+    (``allocate_split_scratch``)."""
+    batch = fused.shape[0]
+    qd, kd = num_heads * head_dim, num_kv_heads * head_dim
+    q_raw = fused[:, :qd].view(batch, num_heads, head_dim)
+    gate = fused[:, qd:2 * qd].view(batch, num_heads, head_dim)
+    k_raw = fused[:, 2 * qd:2 * qd + kd].view(batch, num_kv_heads, head_dim)
+    v_raw = fused[:, 2 * qd + kd:2 * qd + 2 * kd].view(batch, num_kv_heads, head_dim)
+    counters = getattr(scratch, "counters", None)
+    assert counters is not None, "the attention block needs a scratch with merge counters"
+    m, l, acc = scratch
+    out = paged_gqa_attention_decode_block(
+        q_raw, gate, k_raw, v_raw, q_norm, k_norm, eps, inv_freq, rotary_dim, k_cache,
+        v_cache, block_table, pos, m, l, acc, counters)
+    return out.view(batch, num_heads * head_dim)

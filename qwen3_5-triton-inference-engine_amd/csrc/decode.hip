@@ -66,6 +66,11 @@ struct DecodeArgs {
   int64_t g_b, g_h, g_d;
   bf16_t *out;        // [B, H_q, D]
   int64_t o_b, o_h, o_d;
+  // fused attention block only: q/k RMSNorm weights and the partial RoPE
+  const bf16_t *qw, *kw;
+  const float *inv_freq;
+  float eps;
+  int rope_dim;
 };
 
 __device__ __forceinline__ int split_pps(int npg, int min_pps) {
@@ -219,10 +224,16 @@ struct SplitLds {
   float ml[kW][2][kG];           // per-wave m, l
   float4 acc[kW][kG][kD / 4];    // per-wave unnormalised acc
   bf16_t q[kG][kD + 8];          // the group's query rows
+  bf16_t kn[kD];                 // attention block: the new token's normalised, rotated key
   int last;
 };
 
-template <bool kFused, int kW>
+// kProlog (with kFused): the decode attention block.  q and the new key
+// arrive raw from the fused projection; the kernel applies the per-head
+// RMSNorm (weight 1 + w) and the partial RoPE at position pos itself, with the
+// same device code and roundings as the standalone qwen_rmsnorm and
+// partial_rope kernels, so the block equals the op-by-op sequence bit for bit.
+template <bool kFused, int kW, bool kProlog>
 __global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(4)))
 void paged_decode_split_kernel(const DecodeArgs a) {
   extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -251,7 +262,38 @@ void paged_decode_split_kernel(const DecodeArgs a) {
 
   // The group's 4 query rows, staged once in LDS; each page rebuilds the MFMA
   // A operand from it (rows 4..15 of the operand are zero).
-  if (threadIdx.x < kG * kD / 8) {
+  if constexpr (kProlog) {
+    // The RoPE inputs are fetched with the rows: lane i later rotates pair
+    // (head i / half, j = i % half).
+    const int half = a.rope_dim / 2;
+    const float pf = float(seq_len - 1);  // = float(pos[b])
+    float sn = 0.f, cs = 1.f;
+    if (threadIdx.x < kG * half) rope_sincos(pf, a.inv_freq[threadIdx.x % half], sn, cs);
+    // RMSNorm: 32 lanes per row, 8 elements each (rms_rsigma's layout).
+    if (threadIdx.x < kG * kD / 8) {
+      const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
+      const u32x4_t xw = ld16(a.q + b * a.qs_b + (h * kG + r) * a.qs_h + c);
+      const u32x4_t ww = ld16(a.qw + c);
+      const float ss = rms_acc8(xw, 0.f);
+      const float rs = rms_rsigma(ss, kD, a.eps);
+      u32x4_t y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = pack_bf16x2(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])),
+                           rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
+      st16(&sm_q[r][c], y);
+    }
+    __syncthreads();
+    // partial RoPE on dims [0, rope_dim): one lane per (head, pair)
+    if (threadIdx.x < kG * half) {  // rope_dim <= 128: one pass covers every pair
+      const int i = threadIdx.x, r = i / half, j = i - r * half;
+      float o1, o2;
+      rope_rotate(bf16_to_f32(sm_q[r][j]), bf16_to_f32(sm_q[r][j + half]), cs, sn, o1, o2);
+      const uint32_t pk = pack_bf16x2(o1, o2);
+      sm_q[r][j] = bf16_t(pk & 0xffffu);
+      sm_q[r][j + half] = bf16_t(pk >> 16);
+    }
+  } else if (threadIdx.x < kG * kD / 8) {
     const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
     const bf16_t *qrow = a.q + b * a.qs_b + (h * kG + r) * a.qs_h;
     u32x4_t w;
@@ -334,15 +376,67 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   if constexpr (kFused) {
     owns_new = p0 <= last_page && last_page < p1 && (last_page - p0) % kW == wave;
     if (owns_new) {
+      const int c = (lane & 31) * 8;
+      const bf16_t *ksrc = knrow;  // where the new key row is read from
+      if constexpr (kProlog) {
+        // RMSNorm + partial RoPE of the raw key row; both 32-lane halves of
+        // the wave compute it, lanes 0..31 publish it in LDS.
+        const u32x4_t xw = ld16(knrow + c);
+        const u32x4_t ww = ld16(a.kw + c);
+        // chunk l (dims 8l..8l+7) pairs with chunk l +- half/8
+        const int hc = a.rope_dim / 16, l32 = lane & 31;
+        const bool first = l32 < hc, second = l32 >= hc && l32 < 2 * hc;
+        const int partner = (lane & 32) | (first ? l32 + hc : second ? l32 - hc : l32);
+        const float pf = float(seq_len - 1);  // = float(pos[b])
+        float sn8[8], cs8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          sn8[e] = 0.f;
+          cs8[e] = 1.f;
+          if (first || second) rope_sincos(pf, a.inv_freq[(first ? c : c - 8 * hc) + e], sn8[e], cs8[e]);
+        }
+        const float ss = rms_acc8(xw, 0.f);
+        const float rs = rms_rsigma(ss, kD, a.eps);
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y[2 * e] = round_bf16(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])));
+          y[2 * e + 1] = round_bf16(rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
+        }
+        u32x4_t kr16;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          float o[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const float other = __shfl(y[e + u], partner);
+            o[u] = y[e + u];
+            if (first || second) {
+              float o1, o2;
+              if (first) {
+                rope_rotate(y[e + u], other, cs8[e + u], sn8[e + u], o1, o2);
+                o[u] = o1;
+              } else {
+                rope_rotate(other, y[e + u], cs8[e + u], sn8[e + u], o1, o2);
+                o[u] = o2;
+              }
+            }
+          }
+          kr16[e / 2] = pack_bf16x2(o[0], o[1]);
+        }
+        if (lane < 32) st16(&sm.kn[c], kr16);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        ksrc = sm.kn;
+      }
       u32x4_t kn[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kn[e] = ld16(knrow + g4 * 8 + 32 * e);
+      for (int e = 0; e < 8; ++e) kn[e] = ld16(ksrc + g4 * 8 + 32 * e);
       vnew = *reinterpret_cast<const u32x2_t *>(vnrow + lane * 4);
       // the append: one 512-byte row of K (lanes 0..31) and V (32..63)
       const int64_t phys = btrow[last_page];
-      const int c = (lane & 31) * 8;
       if (lane < 32)
-        st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(knrow + c));
+        st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(ksrc + c));
       else
         st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, ld16(vnrow + c));
 #pragma unroll
@@ -570,10 +664,10 @@ int split_grid_z(int max_pages, int min_pps) {
   return z > kMaxSplits ? kMaxSplits : z;
 }
 
-template <bool kFused, int kW>
+template <bool kFused, int kW, bool kProlog = false>
 int launch_split_w(dim3 grid, const DecodeArgs &a, hipStream_t st) {
   const size_t lds = sizeof(SplitLds<kW>);
-  auto *fn = paged_decode_split_kernel<kFused, kW>;
+  auto *fn = paged_decode_split_kernel<kFused, kW, kProlog>;
   if (lds > 65536) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -584,14 +678,14 @@ int launch_split_w(dim3 grid, const DecodeArgs &a, hipStream_t st) {
   return wyh::launch_status();
 }
 
-template <bool kFused>
+template <bool kFused, bool kProlog = false>
 int launch_split(const DecodeArgs &args, int batch, int num_kv_heads, int max_pages, int min_pps,
                  void *stream) {
   DecodeArgs a = args;
   a.batch = batch;
   const dim3 grid(unsigned(batch) * unsigned(num_kv_heads) *
                   unsigned(split_grid_z(max_pages, min_pps)));
-  return launch_split_w<kFused, kWaves>(grid, a, static_cast<hipStream_t>(stream));
+  return launch_split_w<kFused, kWaves, kProlog>(grid, a, static_cast<hipStream_t>(stream));
 }
 
 DecodeArgs base_args(const void *q, const int64_t *qs, const void *k_cache,
@@ -737,4 +831,60 @@ extern "C" int wy_paged_decode_step(const void *q, const int64_t *qs, const void
   a.o_h = os[1];
   a.o_d = os[2];
   return launch_split<true>(a, batch, num_kv_heads, max_pages, min_pages_per_split, stream);
+}
+
+extern "C" int wy_paged_decode_block(const void *q_raw, const int64_t *qs, const void *gate,
+                                     const int64_t *gs, const void *k_raw, const int64_t *kns,
+                                     const void *v_raw, const int64_t *vns,
+                                     const void *q_norm_weight, const void *k_norm_weight,
+                                     float eps, const float *inv_freq, int rotary_dim,
+                                     void *k_cache, void *v_cache, const int64_t *kcs,
+                                     const int64_t *vcs, const int32_t *block_table,
+                                     int64_t bt_stride0, const int64_t *pos, float *m_partial,
+                                     float *l_partial, float *acc_partial, const int64_t *mls,
+                                     const int64_t *as, int32_t *counters, void *out,
+                                     const int64_t *os, int batch, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int max_pages,
+                                     int min_pages_per_split, void *stream) {
+  if (!q_raw || !qs || !gate || !gs || !k_raw || !kns || !v_raw || !vns || !q_norm_weight ||
+      !k_norm_weight || !inv_freq || !k_cache || !v_cache || !kcs || !vcs || !block_table ||
+      !pos || !m_partial || !l_partial || !acc_partial || !mls || !as || !counters || !out ||
+      !os)
+    return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || max_pages <= 0 || min_pages_per_split <= 0)
+    return WY_E_SHAPE;
+  if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
+  if (rotary_dim < 0 || rotary_dim > 128 || rotary_dim % 16 != 0) return WY_E_UNSUPPORTED;
+  if (!cache_layout_ok(k_cache, v_cache, kcs, vcs) || !scratch_layout_ok(acc_partial, as) ||
+      !out_layout_ok(out, os) || qs[2] != 1 || qs[0] % 8 || qs[1] % 8 || !wyh::aligned16(q_raw) ||
+      kns[2] != 1 || vns[2] != 1 || kns[0] % 8 || kns[1] % 8 || vns[0] % 8 || vns[1] % 8 ||
+      !wyh::aligned16(k_raw) || !wyh::aligned16(v_raw) || !wyh::aligned16(q_norm_weight) ||
+      !wyh::aligned16(k_norm_weight))
+    return WY_E_LAYOUT;
+  if (batch == 0) return WY_OK;
+  DecodeArgs a = base_args(q_raw, qs, k_cache, v_cache, kcs, vcs, block_table, bt_stride0, pos,
+                           m_partial, l_partial, acc_partial, mls, as, num_kv_heads, head_dim,
+                           min_pages_per_split);
+  a.kn = static_cast<const bf16_t *>(k_raw);
+  a.vn = static_cast<const bf16_t *>(v_raw);
+  a.kn_b = kns[0];
+  a.kn_h = kns[1];
+  a.vn_b = vns[0];
+  a.vn_h = vns[1];
+  a.counters = counters;
+  a.gate = static_cast<const bf16_t *>(gate);
+  a.g_b = gs[0];
+  a.g_h = gs[1];
+  a.g_d = gs[2];
+  a.out = static_cast<bf16_t *>(out);
+  a.o_b = os[0];
+  a.o_h = os[1];
+  a.o_d = os[2];
+  a.qw = static_cast<const bf16_t *>(q_norm_weight);
+  a.kw = static_cast<const bf16_t *>(k_norm_weight);
+  a.inv_freq = inv_freq;
+  a.eps = eps;
+  a.rope_dim = rotary_dim;
+  return launch_split<true, true>(a, batch, num_kv_heads, max_pages, min_pages_per_split,
+                                  stream);
 }

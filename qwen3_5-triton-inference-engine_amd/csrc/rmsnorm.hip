@@ -1,0 +1,58 @@
+// Per-row RMSNorm with a (1 + w) weight (Qwen's q/k head norm), bf16 in/out,
+// fp32 math.  A row is owned by 32 consecutive lanes; lane l holds elements
+// 8(32k + l) .. +7 of each 256-element block k.  The reduction order is the
+// one rms_rsigma() fixes, shared with the fused decode attention block.
+// Reference: qwen_rmsnorm.py:28-90 (kernel), :92-147 (op).
+#include "wy_common.h"
+
+using namespace wy;
+
+namespace {
+
+constexpr int kRowsPerBlock = 8;  // 256 threads
+
+__global__ __launch_bounds__(256) void qwen_rmsnorm_kernel(
+    const bf16_t *__restrict__ x, int64_t xs_b, int64_t xs_m, const bf16_t *__restrict__ w,
+    bf16_t *__restrict__ out, int64_t os_b, int64_t os_m, int rows, int D, float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  if (row >= rows) return;  // uniform over the row's 32 lanes
+  const int l = threadIdx.x & 31;
+  const bf16_t *xr = x + blockIdx.y * xs_b + row * xs_m;
+  bf16_t *orow = out + blockIdx.y * os_b + row * os_m;
+  const int nk = D / 256;
+  float ss = 0.f;
+  for (int k = 0; k < nk; ++k) {
+    ss = rms_acc8(ld16(xr + (32 * k + l) * 8), ss);
+  }
+  const float rs = rms_rsigma(ss, D, eps);
+  for (int k = 0; k < nk; ++k) {
+    const int c = (32 * k + l) * 8;
+    const u32x4_t xw = ld16(xr + c);
+    const u32x4_t ww = ld16(w + c);
+    u32x4_t y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      y[e] = pack_bf16x2(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])),
+                         rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
+    st16(orow + c, y);
+  }
+}
+
+}  // namespace
+
+extern "C" int wy_qwen_rmsnorm(const void *x, const int64_t *xs, const void *weight, void *out,
+                               const int64_t *os, int batch, int rows, int d_model, float eps,
+                               void *stream) {
+  if (!x || !xs || !weight || !out || !os) return WY_E_NULL;
+  if (batch < 0 || rows < 0 || d_model <= 0) return WY_E_SHAPE;
+  if (d_model % 256 != 0) return WY_E_UNSUPPORTED;
+  if (xs[2] != 1 || os[2] != 1 || xs[0] % 8 || xs[1] % 8 || os[0] % 8 || os[1] % 8 ||
+      !wyh::aligned16(x) || !wyh::aligned16(weight) || !wyh::aligned16(out))
+    return WY_E_LAYOUT;
+  if (batch == 0 || rows == 0) return WY_OK;
+  const dim3 grid(unsigned((rows + kRowsPerBlock - 1) / kRowsPerBlock), unsigned(batch));
+  qwen_rmsnorm_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(x), xs[0], xs[1], static_cast<const bf16_t *>(weight),
+      static_cast<bf16_t *>(out), os[0], os[1], rows, d_model, eps);
+  return wyh::launch_status();
+}

@@ -13,15 +13,6 @@ __device__ __forceinline__ float load_pos(const void *pos, int64_t off, bool is6
               : float(static_cast<const int32_t *>(pos)[off]);
 }
 
-// out1 = x1*cos - x2*sin, out2 = x1*sin + x2*cos, each product rounded on its
-// own (no fused multiply-add), matching the fp32 formula of
-// partial_rope.py:97-98.
-__device__ __forceinline__ void rotate(float x1, float x2, float c, float s, float &o1,
-                                       float &o2) {
-  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  o2 = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
-}
-
 // ------------------------------------------------------------ partial RoPE --
 // Fast path: lanes own 16-byte chunks of a row.  A chunk in the first rotary
 // half also produces its partner chunk R/2 further on; chunks of the second
@@ -51,10 +42,10 @@ __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       float o1l, o2l, o1h, o2h, sl, cl, sh, ch;
-      sincosf(__fmul_rn(p, inv_freq[c * 8 + 2 * w]), &sl, &cl);
-      sincosf(__fmul_rn(p, inv_freq[c * 8 + 2 * w + 1]), &sh, &ch);
-      rotate(bf16_lo(a[w]), bf16_lo(bb[w]), cl, sl, o1l, o2l);
-      rotate(bf16_hi(a[w]), bf16_hi(bb[w]), ch, sh, o1h, o2h);
+      rope_sincos(p, inv_freq[c * 8 + 2 * w], sl, cl);
+      rope_sincos(p, inv_freq[c * 8 + 2 * w + 1], sh, ch);
+      rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), cl, sl, o1l, o2l);
+      rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), ch, sh, o1h, o2h);
       oa[w] = pack_bf16x2(o1l, o1h);
       ob[w] = pack_bf16x2(o2l, o2h);
     }
@@ -89,11 +80,11 @@ __global__ __launch_bounds__(256) void partial_rope_generic_kernel(
   const int j = d < half ? d : d - half;
   const float p = load_pos(pos, b * ps_b + int64_t(t) * ps_t, pos64 != 0);
   float s, c;
-  sincosf(__fmul_rn(p, inv_freq[j]), &s, &c);
+  rope_sincos(p, inv_freq[j], s, c);
   const float x1 = bf16_to_f32(xr[j * xs_d]);
   const float x2 = bf16_to_f32(xr[(j + half) * xs_d]);
   float o1, o2;
-  rotate(x1, x2, c, s, o1, o2);
+  rope_rotate(x1, x2, c, s, o1, o2);
   *o = bf16_t(f32_to_bf16_bits(d < half ? o1 : o2));
 }
 

@@ -62,6 +62,47 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---- shared by the standalone RMSNorm / RoPE kernels and the fused decode
+// block, so that the fused path is bit-identical to the op-by-op path ------
+
+// out1 = x1*cos - x2*sin, out2 = x1*sin + x2*cos, each product rounded on its
+// own (no fused multiply-add), matching the fp32 formula of
+// partial_rope.py:97-98.
+__device__ __forceinline__ void rope_rotate(float x1, float x2, float c, float s, float &o1,
+                                            float &o2) {
+  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+  o2 = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
+}
+// angle = float(pos) * inv_freq[j] in fp32 (partial_rope.py:74-75).
+__device__ __forceinline__ void rope_sincos(float pos, float inv_freq_j, float &s, float &c) {
+  sincosf(__fmul_rn(pos, inv_freq_j), &s, &c);
+}
+
+// RMSNorm of one row held by a group of 32 consecutive lanes, lane l holding
+// 8 consecutive elements of each 256-element block k (elements 8(32k+l) ..).
+// The sum of squares runs over the lane's elements in order, then an xor
+// tree over the 32 lanes; rsigma = rsqrt(sum/D + eps).  y = x*rsigma*(1+w)
+// in fp32 (qwen_rmsnorm.py:69-73).
+// Sum of squares of 8 bf16 elements (one 16-byte chunk) into ss, in element
+// order, one fused multiply-add each.
+__device__ __forceinline__ float rms_acc8(u32x4_t xw, float ss) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    ss = __fmaf_rn(bf16_lo(xw[e]), bf16_lo(xw[e]), ss);
+    ss = __fmaf_rn(bf16_hi(xw[e]), bf16_hi(xw[e]), ss);
+  }
+  return ss;
+}
+__device__ __forceinline__ float rms_rsigma(float sumsq_lane, int d_model, float eps) {
+  float s = sumsq_lane;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  return rsqrtf(s / float(d_model) + eps);
+}
+__device__ __forceinline__ float rms_apply(float x, float rsigma, float w) {
+  return (x * rsigma) * (1.0f + w);
+}
+
 }  // namespace wy
 
 // Host-side helpers shared by the launchers.

@@ -371,6 +371,81 @@ def _paged_fused_fake(q, k_new, v_new, k_cache, v_cache, block_table, pos, m_par
     return torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
 
 
+@torch.library.custom_op(
+    "wy_lib::paged_gqa_attention_decode_block",
+    mutates_args=("k_cache", "v_cache", "m_partial", "l_partial", "acc_partial", "counters"),
+    device_types="cuda",
+)
+def paged_gqa_attention_decode_block(
+    q_raw: torch.Tensor,
+    gate: torch.Tensor,
+    k_raw: torch.Tensor,
+    v_raw: torch.Tensor,
+    q_norm: torch.Tensor,
+    k_norm: torch.Tensor,
+    eps: float,
+    inv_freq: torch.Tensor,
+    rotary_dim: int,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    pos: torch.Tensor,
+    m_partial: torch.Tensor,
+    l_partial: torch.Tensor,
+    acc_partial: torch.Tensor,
+    counters: torch.Tensor,
+) -> torch.Tensor:
+    """The decode attention block of one layer in one launch (the sequence of
+    engine/runner.py:476-517 from the projection slices to the o_proj input):
+    q/k RMSNorm (weight ``1 + w``), partial RoPE at ``pos``, K/V append,
+    split-K attention + merge, sigmoid gate.  q_raw / gate ``[B, H_q, D]``,
+    k_raw / v_raw ``[B, H_kv, D]``, any row strides.  Returns ``[B, H_q, D]``
+    bf16, bit-identical to qwen_rmsnorm -> partial_rope ->
+    paged_gqa_attention_decode_fused."""
+    batch, num_q_heads, head_dim = q_raw.shape
+    num_pages, num_kv_heads, page, cache_dim = k_cache.shape
+    assert page == PAGE_SIZE and cache_dim == head_dim
+    assert v_cache.shape == k_cache.shape
+    assert gate.shape == q_raw.shape
+    assert k_raw.shape == v_raw.shape == (batch, num_kv_heads, head_dim)
+    for t in (q_raw, gate, k_raw, v_raw, q_norm, k_norm, k_cache, v_cache):
+        assert t.dtype == torch.bfloat16
+    assert q_raw.stride(-1) == 1 and k_raw.stride(-1) == 1 and v_raw.stride(-1) == 1
+    assert q_norm.shape == k_norm.shape == (head_dim,)
+    assert q_norm.is_contiguous() and k_norm.is_contiguous()
+    assert inv_freq.dtype == torch.float32 and inv_freq.is_contiguous()
+    assert inv_freq.numel() == rotary_dim // 2
+    assert block_table.dtype == torch.int32 and block_table.shape[0] == batch
+    assert block_table.stride(1) == 1
+    assert pos.dtype == torch.int64 and pos.shape == (batch,) and pos.is_contiguous()
+    assert m_partial.shape == (batch, num_q_heads, MAX_SPLITS)
+    assert l_partial.shape == m_partial.shape and l_partial.stride() == m_partial.stride()
+    assert acc_partial.shape == (batch, num_q_heads, MAX_SPLITS, head_dim)
+    assert counters.dtype == torch.int32 and counters.is_contiguous()
+    assert counters.numel() >= batch * num_kv_heads
+    out = torch.empty((batch, num_q_heads, head_dim), dtype=torch.bfloat16, device=q_raw.device)
+    _lib.call(
+        "wy_paged_decode_block",
+        _lib.ptr(q_raw), _lib.strides(q_raw), _lib.ptr(gate), _lib.strides(gate),
+        _lib.ptr(k_raw), _lib.strides(k_raw), _lib.ptr(v_raw), _lib.strides(v_raw),
+        _lib.ptr(q_norm), _lib.ptr(k_norm), float(eps), _lib.ptr(inv_freq), rotary_dim,
+        _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.strides(k_cache), _lib.strides(v_cache),
+        _lib.ptr(block_table), block_table.stride(0), _lib.ptr(pos),
+        _lib.ptr(m_partial), _lib.ptr(l_partial), _lib.ptr(acc_partial),
+        _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(counters),
+        _lib.ptr(out), _lib.strides(out), batch, num_q_heads, num_kv_heads, head_dim,
+        block_table.shape[1], min_pages_per_split(batch), _lib.stream(q_raw.device),
+    )
+    return out
+
+
+@paged_gqa_attention_decode_block.register_fake
+def _paged_block_fake(q_raw, gate, k_raw, v_raw, q_norm, k_norm, eps, inv_freq, rotary_dim,
+                      k_cache, v_cache, block_table, pos, m_partial, l_partial, acc_partial,
+                      counters) -> torch.Tensor:
+    return torch.empty(q_raw.shape, dtype=torch.bfloat16, device=q_raw.device)
+
+
 def _seq_bucket(seq_len: int) -> int:
     """Kept for interface parity with the reference (:950); the HIP kernels
     have fixed launch configurations, so the bucket selects nothing."""

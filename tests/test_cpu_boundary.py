@@ -75,6 +75,7 @@ def test_op_schemas_match_reference():
         "gqa_attention_varlen_causal": "(Tensor q, Tensor k, Tensor v, Tensor cu_seqlens, "
                                        "SymInt max_seqlen) -> Tensor",
         "attention_gate_pack": "(Tensor x, Tensor gate) -> Tensor",
+        "qwen_rmsnorm": "(Tensor x, Tensor weight, float eps=9.9999999999999995e-07) -> Tensor",
     }
     for name, sig in schemas.items():
         op = getattr(torch.ops.wy_lib, name).default

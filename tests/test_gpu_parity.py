@@ -528,3 +528,125 @@ def test_decode_attention_step_with_gate(pkg, dev):
     ref = orc.gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), gate4)
     assert out.shape == (B, 2048)
     close(out, ref, what="gated step")
+
+
+# ------------------------------------------------------------------ q/k norm + attention block
+
+@pytest.mark.parametrize("shape,strided", [((5, 8, 256), True), ((3, 2, 256), True),
+                                           ((40, 1024), False), ((7, 3, 256), False)])
+def test_qwen_rmsnorm_vs_oracle(pkg, dev, shape, strided):
+    say(f"qwen_rmsnorm {shape} strided={strided}")
+    gen = torch.Generator().manual_seed(sum(shape))
+    d = shape[-1]
+    w = bf((d,), gen, 0.3)
+    if strided:  # a [B, H, D] view of a wider row, as the fused projection gives
+        B, H, _ = shape
+        wide = bf((B, 5120), gen, 2.0)
+        x = wide[:, 256:256 + H * d].view(B, H, d)
+        out = pkg.qwen_rmsnorm(wide.to(dev)[:, 256:256 + H * d].view(B, H, d), w.to(dev), 1e-6)
+    else:
+        x = bf(shape, gen, 2.0)
+        out = pkg.qwen_rmsnorm(x.to(dev), w.to(dev), 1e-6)
+    ref = orc.qwen_rmsnorm(x, w, 1e-6)
+    assert out.shape == ref.shape and out.is_contiguous()
+    # fp32 math rounded to bf16 once: at most one bf16 ulp apart
+    torch.testing.assert_close(out.cpu().float(), ref.float(), atol=1e-6, rtol=2 ** -7)
+
+
+def _block_case(gen, lens):
+    B = len(lens)
+    # the table must cover every sequence's pages: pos is not range-checked on
+    # the device (the host allocates pages before the step, engine/paging.py)
+    max_pages = -(-max(lens) // 16) + 1
+    num_pages = B * max_pages
+    return dict(
+        B=B, bt=rand_table(B, max_pages, num_pages, gen),
+        kc=bf((num_pages, HKV, 16, D), gen), vc=bf((num_pages, HKV, 16, D), gen),
+        fused=bf((B, 5120), gen, 1.5), qw=bf((D,), gen, 0.3), kw=bf((D,), gen, 0.3),
+        pos=torch.tensor([n - 1 for n in lens]))
+
+
+def test_decode_block_equals_op_sequence(pkg, dev):
+    """One-launch attention block == qwen_rmsnorm -> partial_rope -> fused
+    step with gate, bit for bit (output and both caches)."""
+    say("decode attention block == op sequence")
+    gen = torch.Generator().manual_seed(51)
+    c = _block_case(gen, [33, 1000, 129, 2, 16, 17, 512, 1111])
+    B = c["B"]
+    inv = C.inv_freq().to(dev)
+    fg, bt, pos = c["fused"].to(dev), c["bt"].to(dev), c["pos"].to(dev)
+    qw, kw = c["qw"].to(dev), c["kw"].to(dev)
+    kc1, vc1 = c["kc"].to(dev), c["vc"].to(dev)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    sc1 = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    sc2 = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    out1 = pkg.decode_attention_block(fg, qw, kw, 1e-6, inv, 64, pos, kc1, vc1, bt, sc1)
+    q = pkg.qwen_rmsnorm(fg[:, :2048].view(B, HQ, D), qw, 1e-6)
+    k = pkg.qwen_rmsnorm(fg[:, 4096:4608].view(B, HKV, D), kw, 1e-6)
+    out2 = pkg.decode_attention_step(q, k, fg[:, 4608:], fg[:, 2048:4096], inv, 64, pos,
+                                     kc2, vc2, bt, sc2)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(out1, out2)
+    assert int(sc1.counters.abs().sum()) == 0
+
+
+def test_decode_block_vs_oracle(pkg, dev):
+    """The block against the reference op sequence computed by the oracle."""
+    say("decode attention block vs oracle")
+    gen = torch.Generator().manual_seed(52)
+    c = _block_case(gen, [300, 1, 64, 2000])
+    B = c["B"]
+    inv = C.inv_freq()
+    kg, vg = c["kc"].to(dev), c["vc"].to(dev)
+    sc = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    out = pkg.decode_attention_block(c["fused"].to(dev), c["qw"].to(dev), c["kw"].to(dev), 1e-6,
+                                     inv.to(dev), 64, c["pos"].to(dev), kg, vg, c["bt"].to(dev), sc)
+    fused, pos = c["fused"], c["pos"]
+    q = orc.qwen_rmsnorm(fused[:, :2048].view(B, HQ, D), c["qw"], 1e-6)
+    k = orc.qwen_rmsnorm(fused[:, 4096:4608].view(B, HKV, D), c["kw"], 1e-6)
+    q = orc.partial_rope(q.unsqueeze(2), pos.view(B, 1), inv, 64)[:, :, 0]
+    k = orc.partial_rope(k.unsqueeze(2), pos.view(B, 1), inv, 64)[:, :, 0]
+    v = fused[:, 4608:].reshape(B, HKV, D)
+    kc, vc = c["kc"].clone(), c["vc"].clone()
+    orc.paged_kv_append(kc, vc, k, v, c["bt"], pos)
+    assert torch.equal(kg.cpu(), kc) and torch.equal(vg.cpu(), vc)
+    ctx = orc.paged_decode(q, kc, vc, c["bt"], pos + 1).to(torch.bfloat16)
+    gate4 = fused[:, 2048:4096].reshape(B, HQ, D).permute(1, 0, 2).unsqueeze(0)
+    ref = orc.gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), gate4)
+    close(out, ref, what="attention block")
+
+
+def test_decode_block_graph_replays(pkg, dev):
+    """The block captured with an in-graph pos += 1, replayed 4 times with
+    eager work in between; every replay equals the eager block."""
+    say("decode attention block graph replays")
+    gen = torch.Generator().manual_seed(53)
+    c = _block_case(gen, [100, 15, 700])
+    B = c["B"]
+    inv = C.inv_freq().to(dev)
+    fg, bt = c["fused"].to(dev), c["bt"].to(dev)
+    qw, kw = c["qw"].to(dev), c["kw"].to(dev)
+    kc_g, vc_g = c["kc"].to(dev), c["vc"].to(dev)
+    kc_e, vc_e = kc_g.clone(), vc_g.clone()
+    pos_g, pos_e = c["pos"].to(dev), c["pos"].to(dev)
+    sc_g = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    sc_e = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up outside the graph on a throwaway copy
+        pkg.decode_attention_block(fg, qw, kw, 1e-6, inv, 64, pos_g.clone(), kc_g.clone(),
+                                   vc_g.clone(), bt, pkg.allocate_split_scratch(HQ, D, batch=B,
+                                                                                device=dev))
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out_g = pkg.decode_attention_block(fg, qw, kw, 1e-6, inv, 64, pos_g, kc_g, vc_g, bt, sc_g)
+        pos_g.add_(1)
+    for rep in range(4):
+        g.replay()
+        out_e = pkg.decode_attention_block(fg, qw, kw, 1e-6, inv, 64, pos_e, kc_e, vc_e, bt, sc_e)
+        pos_e.add_(1)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), rep
+        assert torch.equal(kc_g, kc_e) and torch.equal(vc_g, vc_e), rep

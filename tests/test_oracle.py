@@ -249,3 +249,37 @@ def test_gate_pack_oracle_special_cases():
     for t in (0, 7, 12):
         for h in (0, 5):
             assert torch.equal(out[t, h * 256:(h + 1) * 256], x[0, h, t])
+
+
+# ------------------------------------------------------------------ qwen_rmsnorm
+
+def test_rmsnorm_oracle_brute_force():
+    """Pure-Python restatement with math.sqrt on a few small rows."""
+    gen = torch.Generator().manual_seed(5)
+    x = (torch.randn(3, 256, generator=gen) * 3).to(torch.bfloat16)
+    w = (torch.randn(256, generator=gen) * 0.2).to(torch.bfloat16)
+    got = orc.qwen_rmsnorm(x, w, 1e-6).float()
+    for r in range(3):
+        xs = [float(v) for v in x[r]]
+        inv = 1.0 / math.sqrt(sum(v * v for v in xs) / 256 + 1e-6)
+        for d in range(256):
+            want = xs[d] * inv * (1.0 + float(w[d]))
+            assert abs(got[r, d].item() - want) <= 2 ** -7 * abs(want) + 1e-6
+
+
+def test_rmsnorm_oracle_special_cases():
+    gen = torch.Generator().manual_seed(6)
+    w = (torch.randn(256, generator=gen) * 0.2).to(torch.bfloat16)
+    # constant rows: x / rms(x) = sign(c), so y = sign(c) * (1 + w) up to bf16
+    for c in (0.5, -3.0, 40.0):
+        x = torch.full((2, 256), c, dtype=torch.bfloat16)
+        want = (math.copysign(1.0, c) * (1.0 + w.float())).to(torch.bfloat16)
+        torch.testing.assert_close(orc.qwen_rmsnorm(x, w, 1e-6), want.expand(2, 256),
+                                   atol=0, rtol=2 ** -7)
+    # weight 0: every output row has unit RMS
+    x = (torch.randn(16, 1024, generator=gen) * 7).to(torch.bfloat16)
+    y = orc.qwen_rmsnorm(x, torch.zeros(1024, dtype=torch.bfloat16), 1e-6).float()
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(16), atol=1e-2)
+    # power-of-two scaling of the input leaves the output unchanged
+    x = torch.randn(4, 256, generator=gen).to(torch.bfloat16)
+    assert torch.equal(orc.qwen_rmsnorm(x, w, 1e-12), orc.qwen_rmsnorm(x * 8, w, 1e-12))
