@@ -16,8 +16,10 @@ Split partition.  The reference splits every sequence into
 ``ceil(npg / ceil(npg/128))`` page-aligned chunks.  The HIP pair here uses
 ``pps = max(ceil(npg/128), min_pages_per_split(B))`` pages per split in both the
 split and the combine op, so short contexts do not write one 4 KiB fp32
-partial per 16-token page.  The scratch tensors keep the reference shapes;
-their contents are a private contract between the two ops.
+partial per 16-token page.  The one-launch step and attention block (which
+merge their own splits) also raise the floor to 128 pages for tables of
+>= 1024 pages.  The scratch tensors keep the reference shapes; their contents
+are a private contract between the ops.
 """
 
 from __future__ import annotations
@@ -34,7 +36,7 @@ MAX_SPLITS = 128
 # Lower bound on pages per split shared by split and combine (see module doc).
 # Small batches keep 4 pages (64 tokens) per split so a lone sequence still
 # spreads over many workgroups; large batches already fill the GPU and gain
-# more from fewer partials to merge (16 pages = 256 tokens).  Both ops derive
+# more from fewer partials to merge (32 pages = 512 tokens).  Both ops derive
 # it from the batch size alone, a static shape, so the pair stays graph-safe.
 MIN_PAGES_PER_SPLIT = 4
 MIN_PAGES_PER_SPLIT_LARGE_BATCH = 32
@@ -43,6 +45,20 @@ LARGE_BATCH = 16
 
 def min_pages_per_split(batch: int) -> int:
     return MIN_PAGES_PER_SPLIT_LARGE_BATCH if batch >= LARGE_BATCH else MIN_PAGES_PER_SPLIT
+
+
+# The one-launch step and block merge their own splits (no combine op has to
+# agree on the partition), so they may also use the table width: with long
+# contexts (>= 1024 pages = 16k tokens) 128-page splits stream each split's
+# pages longer and cut the merge work (config 5: 818 -> 767 us per step).
+LONG_CONTEXT_PAGES = 1024
+MIN_PAGES_PER_SPLIT_LONG = 128
+
+
+def min_pages_per_split_fused(batch: int, max_pages: int) -> int:
+    if max_pages >= LONG_CONTEXT_PAGES:
+        return MIN_PAGES_PER_SPLIT_LONG
+    return min_pages_per_split(batch)
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -360,7 +376,7 @@ def paged_gqa_attention_decode_fused(
         _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(counters),
         _lib.ptr(gate), _lib.strides(gate), _lib.ptr(out), _lib.strides(out),
         batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
-        min_pages_per_split(batch), _lib.stream(q.device),
+        min_pages_per_split_fused(batch, block_table.shape[1]), _lib.stream(q.device),
     )
     return out
 
@@ -434,7 +450,8 @@ def paged_gqa_attention_decode_block(
         _lib.ptr(m_partial), _lib.ptr(l_partial), _lib.ptr(acc_partial),
         _lib.strides(m_partial), _lib.strides(acc_partial), _lib.ptr(counters),
         _lib.ptr(out), _lib.strides(out), batch, num_q_heads, num_kv_heads, head_dim,
-        block_table.shape[1], min_pages_per_split(batch), _lib.stream(q_raw.device),
+        block_table.shape[1], min_pages_per_split_fused(batch, block_table.shape[1]),
+        _lib.stream(q_raw.device),
     )
     return out
 
