@@ -50,8 +50,23 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
                                    dummy, dummy, s3, s4, 1, 8, 2, 128, 4, 4, None)
     assert rc == -4
     rc = lib.wy_varlen_causal_prefill(dummy, s3, dummy, s3, dummy, s3, dummy, s3, dummy,
-                                      1, 8, 2, 64, 16, 16, dummy, 1 << 20, None)
+                                      1, 8, 2, 64, 16, 16, None)
     assert rc == -4
+    # qwen_rmsnorm: NULL weight; d_model 384 is not a multiple of 256
+    assert lib.wy_qwen_rmsnorm(dummy, s3, None, dummy, s3, 1, 1, 256, 1e-6, None) == -1
+    assert lib.wy_qwen_rmsnorm(dummy, s3, dummy, dummy, s3, 1, 1, 384, 1e-6, None) == -4
+    # decode block: rotary_dim above 128 or not a multiple of 16 is unsupported
+    for rd, want in ((256, -4), (72, -4)):
+        rc = lib.wy_paged_decode_block(dummy, s3, dummy, s3, dummy, s3, dummy, s3, dummy, dummy,
+                                       1e-6, dummy, rd, dummy, dummy, s4, s4, dummy, 1, dummy,
+                                       dummy, dummy, dummy, s3, s4, dummy, dummy, s3, 1, 8, 2,
+                                       256, 4, 4, None)
+        assert rc == want, (rd, rc)
+    rc = lib.wy_paged_decode_block(dummy, s3, None, s3, dummy, s3, dummy, s3, dummy, dummy,
+                                   1e-6, dummy, 64, dummy, dummy, s4, s4, dummy, 1, dummy,
+                                   dummy, dummy, dummy, s3, s4, dummy, dummy, s3, 1, 8, 2,
+                                   256, 4, 4, None)
+    assert rc == -1  # the gate is required
     rc = lib.wy_partial_rope(dummy, s4, dummy, s4, dummy, (ctypes.c_int64 * 2)(1, 1), 0,
                              dummy, 1, 1, 1, 256, 65, None)
     assert rc == -2  # odd rotary_dim
@@ -173,3 +188,21 @@ def test_oracle_reproduces_golden():
     kc, vc = f["kc"].clone(), f["vc"].clone()
     orc.paged_kv_fill_varlen(kc, vc, f["k"], f["v"], f["bt"], f["cu"])
     assert str(g["fill_pool_after_sha"]) == C.digest(kc, vc)
+
+
+def test_ctypes_signatures_match_header():
+    """Every ctypes binding has as many arguments as its header declaration."""
+    import re
+
+    from importlib import import_module
+
+    import __graft_entry__
+
+    __graft_entry__.load_package()
+    lib = import_module("qwen35_amd._lib")
+    text = (ROOT / "include" / "wy_attn.h").read_text()
+    decls = dict(re.findall(r"^(?:int|size_t|const char \*)\s*(wy_\w+)\(([^;]*)\);", text, re.M | re.S))
+    for name, argtypes in lib._SIGNATURES.items():
+        assert name in decls, name
+        params = [p for p in decls[name].split(",") if p.strip()]
+        assert len(params) == len(argtypes), (name, len(params), len(argtypes))
