@@ -224,7 +224,8 @@ struct SplitLds {
   float ml[kW][2][kG];           // per-wave m, l
   float4 acc[kW][kG][kD / 4];    // per-wave unnormalised acc
   bf16_t q[kG][kD + 8];          // the group's query rows
-  bf16_t kn[kD];                 // attention block: the new token's normalised, rotated key
+  bf16_t kn[kD];                 // fused: the new token's key (normalised, rotated in the block)
+  bf16_t vn[kD];                 // fused: the new token's value
   int last;
 };
 
@@ -259,55 +260,6 @@ void paged_decode_split_kernel(const DecodeArgs a) {
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
-
-  // The group's 4 query rows, staged once in LDS; each page rebuilds the MFMA
-  // A operand from it (rows 4..15 of the operand are zero).
-  if constexpr (kProlog) {
-    // The RoPE inputs are fetched with the rows: lane i later rotates pair
-    // (head i / half, j = i % half).
-    const int half = a.rope_dim / 2;
-    const float pf = float(seq_len - 1);  // = float(pos[b])
-    float sn = 0.f, cs = 1.f;
-    if (threadIdx.x < kG * half) rope_sincos(pf, a.inv_freq[threadIdx.x % half], sn, cs);
-    // RMSNorm: 32 lanes per row, 8 elements each (rms_rsigma's layout).
-    if (threadIdx.x < kG * kD / 8) {
-      const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
-      const u32x4_t xw = ld16(a.q + b * a.qs_b + (h * kG + r) * a.qs_h + c);
-      const u32x4_t ww = ld16(a.qw + c);
-      const float ss = rms_acc8(xw, 0.f);
-      const float rs = rms_rsigma(ss, kD, a.eps);
-      u32x4_t y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        y[e] = pack_bf16x2(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])),
-                           rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
-      st16(&sm_q[r][c], y);
-    }
-    __syncthreads();
-    // partial RoPE on dims [0, rope_dim): one lane per (head, pair)
-    if (threadIdx.x < kG * half) {  // rope_dim <= 128: one pass covers every pair
-      const int i = threadIdx.x, r = i / half, j = i - r * half;
-      float o1, o2;
-      rope_rotate(bf16_to_f32(sm_q[r][j]), bf16_to_f32(sm_q[r][j + half]), cs, sn, o1, o2);
-      const uint32_t pk = pack_bf16x2(o1, o2);
-      sm_q[r][j] = bf16_t(pk & 0xffffu);
-      sm_q[r][j + half] = bf16_t(pk >> 16);
-    }
-  } else if (threadIdx.x < kG * kD / 8) {
-    const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
-    const bf16_t *qrow = a.q + b * a.qs_b + (h * kG + r) * a.qs_h;
-    u32x4_t w;
-    if (a.qs_d == 1) {
-      w = ld16(qrow + c);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = uint32_t(qrow[(c + 2 * e) * a.qs_d]) |
-               (uint32_t(qrow[(c + 2 * e + 1) * a.qs_d]) << 16);
-    }
-    st16(&sm_q[r][c], w);
-  }
-  __syncthreads();
 
   float m_run[kG], l_run[kG], acc[kG][4];
 #pragma unroll
@@ -363,82 +315,146 @@ void paged_decode_split_kernel(const DecodeArgs a) {
       vr[e] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, v_row_bytes * e, 0);
   };
 
-  // Fused step: the wave whose pages end with the new token's page (always
-  // its final page) takes the new token from k_new / v_new, since the cached
-  // row at that slot is stale until the append below lands.  Its score column
-  // comes from the same 8 MFMAs run on the k_new row (each output element of
-  // the MFMA depends only on its own row and column, so the value is the one
-  // the page pass would produce from the cache), and v_new replaces that row
-  // of V.  All of it is fetched before the page loop.
+  // Fused step: the new token's K and V rows come from k_new / v_new (the
+  // cached row at that slot is stale until the append lands).  The wave that
+  // owns the new token's page (always its final page) scores the new key with
+  // the same 8 MFMAs as a page (each MFMA output element depends only on its
+  // own row and column, so the value is the one the page pass would produce
+  // from the cache) and substitutes v_new for that V row; it also writes the
+  // append.  In the attention block the key first needs its RMSNorm and RoPE:
+  // there the workgroup's last wave, idle while the q rows are staged,
+  // prepares both rows in LDS and writes the append.
+  const bool has_new = kFused && p0 <= last_page && last_page < p1;  // uniform
+  auto stage_new = [&] {
+    const int c = (lane & 31) * 8;
+    u32x4_t krow = {0u, 0u, 0u, 0u};
+    if constexpr (kProlog) {
+      // RMSNorm + partial RoPE of the raw key row (both 32-lane halves compute it)
+      const u32x4_t xw = ld16(knrow + c);
+      const u32x4_t ww = ld16(a.kw + c);
+      // chunk l (dims 8l..8l+7) pairs with chunk l +- half/8
+      const int hc = a.rope_dim / 16, l32 = lane & 31;
+      const bool first = l32 < hc, second = l32 >= hc && l32 < 2 * hc;
+      const int partner = (lane & 32) | (first ? l32 + hc : second ? l32 - hc : l32);
+      const float pf = float(seq_len - 1);  // = float(pos[b])
+      float sn8[8], cs8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sn8[e] = 0.f;
+        cs8[e] = 1.f;
+        if (first || second)
+          rope_sincos(pf, a.inv_freq[(first ? c : c - 8 * hc) + e], sn8[e], cs8[e]);
+      }
+      const float rs = rms_rsigma(rms_acc8(xw, 0.f), kD, a.eps);
+      float y[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[2 * e] = round_bf16(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])));
+        y[2 * e + 1] = round_bf16(rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float o[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const float other = __shfl(y[e + u], partner);
+          o[u] = y[e + u];
+          if (first || second) {
+            float o1, o2;
+            if (first) {
+              rope_rotate(y[e + u], other, cs8[e + u], sn8[e + u], o1, o2);
+              o[u] = o1;
+            } else {
+              rope_rotate(other, y[e + u], cs8[e + u], sn8[e + u], o1, o2);
+              o[u] = o2;
+            }
+          }
+        }
+        krow[e / 2] = pack_bf16x2(o[0], o[1]);
+      }
+    }
+    const int64_t phys = btrow[last_page];
+    if (lane < 32) {
+      st16(&sm.kn[c], krow);
+      st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, krow);
+    } else {
+      const u32x4_t vrow = ld16(vnrow + c);
+      st16(&sm.vn[c], vrow);
+      st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, vrow);
+    }
+  };
+
+  // The group's 4 query rows, staged once in LDS; each page rebuilds the MFMA
+  // A operand from it (rows 4..15 of the operand are zero).
+  if constexpr (kProlog) {
+    if (has_new && wave == kW - 1) stage_new();
+    // The RoPE inputs are fetched with the rows: lane i later rotates pair
+    // (head i / half, j = i % half).
+    const int half = a.rope_dim / 2;
+    const float pf = float(seq_len - 1);  // = float(pos[b])
+    float sn = 0.f, cs = 1.f;
+    if (threadIdx.x < kG * half) rope_sincos(pf, a.inv_freq[threadIdx.x % half], sn, cs);
+    // RMSNorm: 32 lanes per row, 8 elements each (rms_rsigma's layout).
+    if (threadIdx.x < kG * kD / 8) {
+      const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
+      const u32x4_t xw = ld16(a.q + b * a.qs_b + (h * kG + r) * a.qs_h + c);
+      const u32x4_t ww = ld16(a.qw + c);
+      const float ss = rms_acc8(xw, 0.f);
+      const float rs = rms_rsigma(ss, kD, a.eps);
+      u32x4_t y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = pack_bf16x2(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])),
+                           rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
+      st16(&sm_q[r][c], y);
+    }
+    __syncthreads();
+    // partial RoPE on dims [0, rope_dim): one lane per (head, pair)
+    if (threadIdx.x < kG * half) {  // rope_dim <= 128: one pass covers every pair
+      const int i = threadIdx.x, r = i / half, j = i - r * half;
+      float o1, o2;
+      rope_rotate(bf16_to_f32(sm_q[r][j]), bf16_to_f32(sm_q[r][j + half]), cs, sn, o1, o2);
+      const uint32_t pk = pack_bf16x2(o1, o2);
+      sm_q[r][j] = bf16_t(pk & 0xffffu);
+      sm_q[r][j + half] = bf16_t(pk >> 16);
+    }
+  } else if (threadIdx.x < kG * kD / 8) {
+    const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
+    const bf16_t *qrow = a.q + b * a.qs_b + (h * kG + r) * a.qs_h;
+    u32x4_t w;
+    if (a.qs_d == 1) {
+      w = ld16(qrow + c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = uint32_t(qrow[(c + 2 * e) * a.qs_d]) |
+               (uint32_t(qrow[(c + 2 * e + 1) * a.qs_d]) << 16);
+    }
+    st16(&sm_q[r][c], w);
+  }
+  __syncthreads();
+
   f32x4_t sc_new = {0.f, 0.f, 0.f, 0.f};
   u32x2_t vnew = {0u, 0u};
   bool owns_new = false;
   if constexpr (kFused) {
-    owns_new = p0 <= last_page && last_page < p1 && (last_page - p0) % kW == wave;
+    owns_new = has_new && (last_page - p0) % kW == wave;
     if (owns_new) {
-      const int c = (lane & 31) * 8;
-      const bf16_t *ksrc = knrow;  // where the new key row is read from
-      if constexpr (kProlog) {
-        // RMSNorm + partial RoPE of the raw key row; both 32-lane halves of
-        // the wave compute it, lanes 0..31 publish it in LDS.
-        const u32x4_t xw = ld16(knrow + c);
-        const u32x4_t ww = ld16(a.kw + c);
-        // chunk l (dims 8l..8l+7) pairs with chunk l +- half/8
-        const int hc = a.rope_dim / 16, l32 = lane & 31;
-        const bool first = l32 < hc, second = l32 >= hc && l32 < 2 * hc;
-        const int partner = (lane & 32) | (first ? l32 + hc : second ? l32 - hc : l32);
-        const float pf = float(seq_len - 1);  // = float(pos[b])
-        float sn8[8], cs8[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          sn8[e] = 0.f;
-          cs8[e] = 1.f;
-          if (first || second) rope_sincos(pf, a.inv_freq[(first ? c : c - 8 * hc) + e], sn8[e], cs8[e]);
-        }
-        const float ss = rms_acc8(xw, 0.f);
-        const float rs = rms_rsigma(ss, kD, a.eps);
-        float y[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          y[2 * e] = round_bf16(rms_apply(bf16_lo(xw[e]), rs, bf16_lo(ww[e])));
-          y[2 * e + 1] = round_bf16(rms_apply(bf16_hi(xw[e]), rs, bf16_hi(ww[e])));
-        }
-        u32x4_t kr16;
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          float o[2];
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const float other = __shfl(y[e + u], partner);
-            o[u] = y[e + u];
-            if (first || second) {
-              float o1, o2;
-              if (first) {
-                rope_rotate(y[e + u], other, cs8[e + u], sn8[e + u], o1, o2);
-                o[u] = o1;
-              } else {
-                rope_rotate(other, y[e + u], cs8[e + u], sn8[e + u], o1, o2);
-                o[u] = o2;
-              }
-            }
-          }
-          kr16[e / 2] = pack_bf16x2(o[0], o[1]);
-        }
-        if (lane < 32) st16(&sm.kn[c], kr16);
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        ksrc = sm.kn;
-      }
+      // the attention block staged both rows in LDS; the plain step reads
+      // k_new / v_new here and writes the append itself
+      const bf16_t *ksrc = kProlog ? sm.kn : knrow;
       u32x4_t kn[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) kn[e] = ld16(ksrc + g4 * 8 + 32 * e);
-      vnew = *reinterpret_cast<const u32x2_t *>(vnrow + lane * 4);
-      // the append: one 512-byte row of K (lanes 0..31) and V (32..63)
-      const int64_t phys = btrow[last_page];
-      if (lane < 32)
-        st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(ksrc + c));
-      else
-        st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, ld16(vnrow + c));
+      vnew = *reinterpret_cast<const u32x2_t *>((kProlog ? sm.vn : vnrow) + lane * 4);
+      if constexpr (!kProlog) {
+        const int64_t phys = btrow[last_page];
+        const int c = (lane & 31) * 8;
+        if (lane < 32)
+          st16(a.kc + phys * a.kc_p + h * a.kc_h + last_slot * a.kc_s + c, ld16(knrow + c));
+        else
+          st16(a.vc + phys * a.vc_p + h * a.vc_h + last_slot * a.vc_s + c, ld16(vnrow + c));
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const u32x4_t qw = n16 < kG ? ld16(&sm_q[n16 & 3][32 * e + 8 * g4])
