@@ -228,6 +228,18 @@ int wy_paged_decode_block(const void *q_raw, const int64_t *q_strides, const voi
                           int num_kv_heads, int head_dim, int max_pages,
                           int min_pages_per_split, void *stream);
 
+/*
+ * Projection GEMM:  y[m, n] = bf16(sum_k x[m, k] * w[n, k])  (fp32 accumulation)
+ * x [M, K], w [N, K], y [M, N] bf16, row strides x_strides[0] / w_strides[0] /
+ * y_strides[0] (elements; x and w rows 16-byte aligned), inner strides 1;
+ * K a multiple of 128.  M <= 64 runs a weight-streaming kernel, larger M a
+ * 128 x 128-tile MFMA kernel.
+ * Replaces wy_lib::gemm_2d (triton_kernels/gemm_2d.py:197-230, kernel :157-195).
+ */
+int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w,
+               const int64_t *w_strides, void *y, const int64_t *y_strides, int M, int N,
+               int K, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,8 @@ PINNED = {
     "gate_pack": "gate=0 -> x/2 exactly; large gate -> x; layout by index identity",
     "qwen_rmsnorm": "pure-Python brute force (math.sqrt); power-of-two scale invariance; "
                     "constant rows -> (1+w)*sign; weight 0 -> unit RMS",
+    "gemm_2d": "pure-Python triple loop; identity weight returns x; one-hot weight rows "
+               "select columns; linearity in x",
 }
 
 
@@ -207,3 +209,10 @@ def gate_pack(x, gate) -> torch.Tensor:
     B, H, T, D = x.shape
     out = x.float() * torch.sigmoid(gate.float())
     return out.permute(0, 2, 1, 3).reshape(B * T, H * D).to(x.dtype)
+
+
+def gemm_2d(x, weight) -> torch.Tensor:
+    """fp64 ``x @ weight.T`` of bf16 inputs (the reference's own check,
+    ``torch.nn.functional.linear``, gemm_2d.py:240-250); the kernel rounds its
+    fp32 sum to bf16 once."""
+    return x.double() @ weight.double().T

@@ -20,6 +20,7 @@ from .attention import (
 )
 from .attention_gate_pack import attention_gate_pack
 from .cache import AttnCaches, allocate_attn_caches
+from .gemm_2d import call_gemm_2d_triton, gemm_2d
 from .gqa_attention_decode_paged import (
     MAX_SPLITS,
     MIN_PAGES_PER_SPLIT,
@@ -46,17 +47,18 @@ from .qwen_rmsnorm import call_qwen_rmsnorm_triton, qwen_rmsnorm
 def install_as_triton_kernels() -> None:
     """Alias the reference module paths (``triton_kernels.<op>`` and
     ``engine.paging``) to this package's modules in ``sys.modules``."""
-    from . import (attention_gate_pack, gqa_attention_decode_paged,
-                   gqa_attention_varlen_causal, paging, partial_rope, qwen_rmsnorm)
-    for name, mod in (
-        ("triton_kernels.gqa_attention_decode_paged", gqa_attention_decode_paged),
-        ("triton_kernels.gqa_attention_varlen_causal", gqa_attention_varlen_causal),
-        ("triton_kernels.partial_rope", partial_rope),
-        ("triton_kernels.attention_gate_pack", attention_gate_pack),
-        ("triton_kernels.qwen_rmsnorm", qwen_rmsnorm),
-        ("engine.paging", paging),
+    import importlib
+    for name, sub in (
+        ("triton_kernels.gqa_attention_decode_paged", "gqa_attention_decode_paged"),
+        ("triton_kernels.gqa_attention_varlen_causal", "gqa_attention_varlen_causal"),
+        ("triton_kernels.partial_rope", "partial_rope"),
+        ("triton_kernels.attention_gate_pack", "attention_gate_pack"),
+        ("triton_kernels.qwen_rmsnorm", "qwen_rmsnorm"),
+        ("triton_kernels.gemm_2d", "gemm_2d"),
+        ("engine.paging", "paging"),
     ):
-        sys.modules[name] = mod
+        # the submodule itself: several share their name with the op they define
+        sys.modules[name] = importlib.import_module(f"{__name__}.{sub}")
 
 
 def library_loaded() -> bool:

@@ -1,0 +1,266 @@
+// y = x @ W^T in bf16 with fp32 accumulation on MFMA (gfx950): the projection
+// GEMM of the attention block (triton_kernels/gemm_2d.py:157-240).
+//   x [M, K], W [N, K], y [M, N]; K contiguous in x and W, N contiguous in y,
+//   K % 128 == 0 (the reference's own precondition).
+//
+// Two kernels, chosen by M:
+//   * M <= 64 (decode: M is the batch): weight streaming.  A workgroup owns 16
+//     output columns (16 rows of W); its waves split K.  W rows are loaded
+//     straight into the B operand of v_mfma_f32_16x16x32_bf16 (lane: column
+//     l%16, 8 consecutive k at 8(l/16)), x rows into the A operand, one MFMA
+//     per 16 rows of M, so every W byte is read once.  The waves' partial
+//     16-column tiles are summed through LDS.
+//   * M > 64 (prefill: M is the token count): 128 x 128 output tiles, 4 waves
+//     of 64 x 64 on v_mfma_f32_32x32x16_bf16, K in 64-wide steps.  x and W
+//     tiles move global -> LDS with buffer loads carrying the LDS-DMA bit
+//     (no registers), two stages; rows past M / N lie outside the buffer
+//     range and read as zero.
+#include "wy_common.h"
+
+using namespace wy;
+
+namespace {
+
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// ------------------------------------------------------------ skinny (M <= 64)
+constexpr int kSkinnyMaxM = 64;
+
+template <int kNW>
+__global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
+    const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
+    bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K) {
+  __shared__ f32x4v_t red[kNW][kSkinnyMaxM / 16][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = blockIdx.x * 16;
+  const int kc = K / kNW;  // a multiple of 32 (host)
+  const int kb = wave * kc;
+  const int g = lane >> 4;
+  const int nrow = min(n0 + (lane & 15), N - 1);
+  const bf16_t *wp = w + int64_t(nrow) * ws0 + kb + 8 * g;
+  const int mtn = (M + 15) >> 4;
+
+  f32x4v_t acc[kSkinnyMaxM / 16];
+#pragma unroll
+  for (int mt = 0; mt < kSkinnyMaxM / 16; ++mt) acc[mt] = f32x4v_t{0.f, 0.f, 0.f, 0.f};
+  const bf16_t *xp[kSkinnyMaxM / 16];
+  bool xok[kSkinnyMaxM / 16];
+#pragma unroll
+  for (int mt = 0; mt < kSkinnyMaxM / 16; ++mt) {
+    const int row = mt * 16 + (lane & 15);
+    xok[mt] = row < M;
+    xp[mt] = x + int64_t(xok[mt] ? row : 0) * xs0 + kb + 8 * g;
+  }
+
+#pragma unroll 4
+  for (int k = 0; k < kc; k += 32) {
+    const u32x4_t wv = ld16(wp + k);
+#pragma unroll
+    for (int mt = 0; mt < kSkinnyMaxM / 16; ++mt) {
+      if (mt < mtn) {
+        u32x4_t xv = ld16(xp[mt] + k);
+        if (!xok[mt]) xv = u32x4_t{0u, 0u, 0u, 0u};
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv),
+                                                          __builtin_bit_cast(bf16x8_t, wv),
+                                                          acc[mt], 0, 0, 0);
+      }
+    }
+  }
+
+  // lane l of tile mt holds rows mt*16 + 4(l/16) + i (i = 0..3) of column l%16
+#pragma unroll
+  for (int mt = 0; mt < kSkinnyMaxM / 16; ++mt)
+    if (mt < mtn) red[wave][mt][lane] = acc[mt];
+  __syncthreads();
+  for (int e = threadIdx.x; e < M * 16; e += 64 * kNW) {
+    const int row = e >> 4, col = e & 15;
+    const int mt = row >> 4, src = col + 16 * ((row & 15) >> 2), i = row & 3;
+    float s = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kNW; ++wv) s += red[wv][mt][src][i];
+    if (n0 + col < N) y[int64_t(row) * ys0 + n0 + col] = bf16_t(f32_to_bf16_bits(s));
+  }
+}
+
+// ------------------------------------------------------------ tiled (M > 64)
+// Output tile kTile x kTile, 4 waves in a 2 x 2 grid, each (kTile/2)^2 as
+// (kTile/64)^2 MFMA tiles of 32 x 32; K in 64-wide steps, two LDS stages.
+// kTile = 128: 72 KiB of LDS, two workgroups per CU.  (A 256-wide tile with
+// one workgroup per CU measured slower: 284 vs 256 us at 16384 x 6144 x 1024.)
+constexpr int kTK = 64;
+constexpr int kTSlots = kTK / 8 + 1;   // 16-byte slots per LDS row (one pad)
+constexpr int kTPitch = kTSlots * 16;  // 144 B: 16 consecutive rows hit disjoint banks
+
+// One 1 KiB global -> LDS block (16 bytes per lane).  A plain device function:
+// inside a kernel template the host-side pass cannot instantiate the builtin.
+__device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rsrc, unsigned char *lds,
+                                          uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 16, voff, soff, 0, 0);
+}
+
+template <int kTile>
+struct TileCfg {
+  static constexpr int kOpTile = kTile * kTPitch;       // one operand's LDS tile
+  static constexpr int kStage = 2 * kOpTile;            // x tile + W tile
+  static constexpr int kOpDma = kOpTile / 1024;         // DMA blocks per operand tile
+  static constexpr int kPerWave = 2 * kOpDma / 4;       // DMA blocks per wave per stage
+  static constexpr int kLds = 2 * kStage;
+  static constexpr int kFrag = kTile / 64;              // MFMA tiles per wave per dim
+  static_assert(kOpTile % 1024 == 0 && (2 * kOpDma) % 4 == 0, "whole DMA blocks per wave");
+};
+
+template <int kTile>
+__global__ __launch_bounds__(256) void gemm_tiled_kernel(
+    const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
+    bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K) {
+  using C = TileCfg<kTile>;
+  constexpr int kF = C::kFrag;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g = lane >> 5, r32 = lane & 31;
+  const int m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+
+  // DMA block b (= wave + 4i) of a stage: b < kOpDma fills the x tile, the
+  // rest the W tile; lane j of a block fills 16-byte slot 64 (b mod kOpDma) + j;
+  // slot c of row r holds k-chunk c (the pad slot repeats chunk 0, never read).
+  // Lane offsets are tile-invariant, the k offset is scalar, and the buffer
+  // ranges end at the last valid row, so rows past M / N read zero.
+  const int a_rows = min(kTile, M - m0), b_rows = min(kTile, N - n0);
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(x + int64_t(m0) * xs0), 0,
+      int(uint32_t(a_rows - 1) * uint32_t(xs0) * 2u + uint32_t(K) * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(w + int64_t(n0) * ws0), 0,
+      int(uint32_t(b_rows - 1) * uint32_t(ws0) * 2u + uint32_t(K) * 2u), 0x00020000);
+  uint32_t voff[C::kPerWave];
+#pragma unroll
+  for (int i = 0; i < C::kPerWave; ++i) {
+    const int blk = wave + 4 * i;
+    const int sl = 64 * (blk % C::kOpDma) + lane;
+    const int row = sl / kTSlots, c = sl - (sl / kTSlots) * kTSlots;
+    const uint32_t cb = uint32_t(c < kTK / 8 ? c : 0) * 16u;
+    voff[i] = uint32_t(row) * uint32_t(blk < C::kOpDma ? xs0 : ws0) * 2u + cb;
+  }
+  auto issue = [&](int kt) {
+    unsigned char *st = smem + (kt & 1) * C::kStage;
+    const uint32_t soff = uint32_t(kt * kTK) * 2u;
+#pragma unroll
+    for (int i = 0; i < C::kPerWave; ++i) {
+      const int blk = wave + 4 * i;  // wave-uniform
+      if (blk < C::kOpDma) dma_block(a_rsrc, st + blk * 1024, voff[i], soff);
+      else dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
+    }
+  };
+
+  f32x16_t acc[kF][kF];
+#pragma unroll
+  for (int i = 0; i < kF; ++i)
+#pragma unroll
+    for (int j = 0; j < kF; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int kt_n = K / kTK;
+  issue(0);
+  const uint32_t a_lane = uint32_t((kTile / 2 * wm + r32) * kTPitch + 16 * g);
+  const uint32_t b_lane = uint32_t(C::kOpTile + (kTile / 2 * wn + r32) * kTPitch + 16 * g);
+  for (int kt = 0; kt < kt_n; ++kt) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this stage has landed
+    __syncthreads();                                   // and every wave is done with the other
+    if (kt + 1 < kt_n) issue(kt + 1);
+    const unsigned char *st = smem + (kt & 1) * C::kStage;
+#pragma unroll
+    for (int ks = 0; ks < kTK / 16; ++ks) {
+      u32x4_t av[kF], bv[kF];
+#pragma unroll
+      for (int t = 0; t < kF; ++t) {
+        av[t] = ld16(st + a_lane + t * 32 * kTPitch + ks * 32);
+        bv[t] = ld16(st + b_lane + t * 32 * kTPitch + ks * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < kF; ++i)
+#pragma unroll
+        for (int j = 0; j < kF; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8_t, av[i]), __builtin_bit_cast(bf16x8_t, bv[j]),
+              acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // acc[i][j] register r of lane l: row (r&3) + 8(r>>2) + 4(l/32) of m-tile i,
+  // column l%32 of n-tile j.
+#pragma unroll
+  for (int i = 0; i < kF; ++i)
+#pragma unroll
+    for (int j = 0; j < kF; ++j) {
+      const int col = n0 + kTile / 2 * wn + 32 * j + r32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + kTile / 2 * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
+        if (row < M && col < N)
+          y[int64_t(row) * ys0 + col] = bf16_t(f32_to_bf16_bits(acc[i][j][r]));
+      }
+    }
+}
+
+template <int kTile>
+int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
+                 int64_t ys0, int M, int N, int K, hipStream_t st) {
+  auto *fn = gemm_tiled_kernel<kTile>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(fn),
+        hipFuncAttributeMaxDynamicSharedMemorySize, TileCfg<kTile>::kLds);
+    if (e != hipSuccess) return int(e);
+    attr_set = true;
+  }
+  const dim3 grid(unsigned((N + kTile - 1) / kTile), unsigned((M + kTile - 1) / kTile));
+  fn<<<grid, 256, TileCfg<kTile>::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K);
+  return wyh::launch_status();
+}
+
+template <int kNW>
+void launch_skinny(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
+                   int64_t ys0, int M, int N, int K, hipStream_t st) {
+  gemm_skinny_kernel<kNW><<<dim3(unsigned((N + 15) / 16)), 64 * kNW, 0, st>>>(
+      x, xs0, w, ws0, y, ys0, M, N, K);
+}
+
+}  // namespace
+
+extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w,
+                          const int64_t *w_strides, void *y, const int64_t *y_strides, int M,
+                          int N, int K, void *stream) {
+  if (!x || !x_strides || !w || !w_strides || !y || !y_strides) return WY_E_NULL;
+  if (M < 0 || N < 0 || K <= 0 || K % 128) return WY_E_SHAPE;
+  if (x_strides[1] != 1 || w_strides[1] != 1 || y_strides[1] != 1 || x_strides[0] % 8 ||
+      w_strides[0] % 8 || x_strides[0] < K || w_strides[0] < K || y_strides[0] < N ||
+      !wyh::aligned16(x) || !wyh::aligned16(w) || (reinterpret_cast<uintptr_t>(y) & 1u))
+    return WY_E_LAYOUT;
+  if (M == 0 || N == 0) return WY_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bf16_t *xb = static_cast<const bf16_t *>(x);
+  const bf16_t *wb = static_cast<const bf16_t *>(w);
+  bf16_t *yb = static_cast<bf16_t *>(y);
+  if (M <= kSkinnyMaxM) {
+    // waves per workgroup: enough workgroups x waves to keep the CUs streaming,
+    // each wave at least two 32-wide k-steps
+    const int blocks = (N + 15) / 16;
+    int nw = 4;
+    while (nw < 16 && blocks * nw < 2048 && K / (2 * nw) >= 64) nw *= 2;
+    const int64_t xs = x_strides[0], wsd = w_strides[0], ys = y_strides[0];
+    if (nw == 4) launch_skinny<4>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    else if (nw == 8) launch_skinny<8>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    else launch_skinny<16>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    return wyh::launch_status();
+  }
+  // 32-bit buffer offsets within one 128-row band
+  if (int64_t(128) * x_strides[0] * 2 >= INT32_MAX || int64_t(128) * w_strides[0] * 2 >= INT32_MAX)
+    return WY_E_SHAPE;
+  return launch_tiled<128>(xb, x_strides[0], wb, w_strides[0], yb, y_strides[0], M, N, K, st);
+}

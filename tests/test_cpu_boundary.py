@@ -70,6 +70,13 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
     rc = lib.wy_partial_rope(dummy, s4, dummy, s4, dummy, (ctypes.c_int64 * 2)(1, 1), 0,
                              dummy, 1, 1, 1, 256, 65, None)
     assert rc == -2  # odd rotary_dim
+    # gemm_2d: K not a multiple of 128; a transposed (non K-contiguous) weight
+    s2 = (ctypes.c_int64 * 2)(256, 1)
+    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 4, 8, 200, None) == -2
+    assert lib.wy_gemm_2d(dummy, s2, None, s2, dummy, s2, 4, 8, 256, None) == -1
+    assert lib.wy_gemm_2d(dummy, s2, dummy, (ctypes.c_int64 * 2)(1, 256), dummy, s2, 4, 8, 256,
+                          None) == -3
+    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 0, 8, 256, None) == 0  # empty
 
 
 def test_ops_refuse_cpu_tensors(pkg):
@@ -91,6 +98,7 @@ def test_op_schemas_match_reference():
                                        "SymInt max_seqlen) -> Tensor",
         "attention_gate_pack": "(Tensor x, Tensor gate) -> Tensor",
         "qwen_rmsnorm": "(Tensor x, Tensor weight, float eps=9.9999999999999995e-07) -> Tensor",
+        "gemm_2d": "(Tensor x, Tensor weight) -> Tensor",
     }
     for name, sig in schemas.items():
         op = getattr(torch.ops.wy_lib, name).default
@@ -114,6 +122,37 @@ def test_fake_impls_give_reference_shapes(pkg):
         pos = torch.empty(3, dtype=torch.int64, device="cuda")
         out = torch.ops.wy_lib.paged_gqa_attention_decode_combine(m, m, acc, pos)
         assert out.shape == (3, 8, 256) and out.dtype == torch.bfloat16
+        xg = torch.empty(7, 1024, dtype=torch.bfloat16, device="cuda")
+        wg = torch.empty(5120, 1024, dtype=torch.bfloat16, device="cuda")
+        assert torch.ops.wy_lib.gemm_2d(xg, wg).shape == (7, 5120)
+
+
+def test_gemm_2d_asserts_reference_preconditions(pkg):
+    # the op body's assertions (gemm_2d.py:201-203) run before any launch
+    body = pkg.gemm_2d._init_fn
+    x = torch.zeros(2, 200, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):  # K % 128
+        body(x, torch.zeros(4, 200, dtype=torch.bfloat16))
+    with pytest.raises(AssertionError):  # dtype
+        body(torch.zeros(2, 256), torch.zeros(4, 256))
+    with pytest.raises(AssertionError):  # K mismatch
+        body(torch.zeros(2, 256, dtype=torch.bfloat16), torch.zeros(4, 128, dtype=torch.bfloat16))
+    with pytest.raises(Exception):  # CUDA-only op
+        pkg.gemm_2d(torch.zeros(2, 256, dtype=torch.bfloat16),
+                    torch.zeros(4, 256, dtype=torch.bfloat16))
+
+
+def test_install_as_triton_kernels_maps_modules(pkg):
+    import sys
+    import types
+
+    pkg.install_as_triton_kernels()
+    for name in ("gemm_2d", "qwen_rmsnorm", "partial_rope", "attention_gate_pack",
+                 "gqa_attention_decode_paged", "gqa_attention_varlen_causal"):
+        mod = sys.modules[f"triton_kernels.{name}"]
+        assert isinstance(mod, types.ModuleType), name
+    assert hasattr(sys.modules["triton_kernels.gemm_2d"], "call_gemm_2d_triton")
+    assert hasattr(sys.modules["engine.paging"], "PagePool")
 
 
 # ------------------------------------------------------------------ host paging

@@ -1,0 +1,86 @@
+"""GPU parity of wy_lib::gemm_2d (the attention projections) against the fp64
+oracle.  The kernel sums in fp32 and rounds to bf16 once, so each output is
+within one bf16 rounding of the exact product (relative 2^-8) plus the fp32
+summation-order error; the bound below is written for that.  Every test prints
+its case before touching the GPU."""
+
+import sys
+
+import pytest
+import torch
+
+from oracle import attention_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def check(y, x, w):
+    ref = orc.gemm_2d(x.cpu(), w.cpu())
+    got = y.float().cpu().double()
+    assert y.dtype == torch.bfloat16 and y.shape == ref.shape and y.is_contiguous()
+    assert torch.isfinite(got).all()
+    # one bf16 rounding (2^-8 relative) + fp32 accumulation of K terms
+    tol = 2.0 ** -8 * ref.abs() + 1e-6 * x.shape[1] * 4 + 1e-3
+    bad = (got - ref).abs() > tol
+    assert not bad.any(), f"{int(bad.sum())} elements off, max err {(got - ref).abs().max():.3e}"
+
+
+SHAPES = [
+    # decode (M = batch) on the block's projections, engine/runner.py:464, :518
+    (1, 5120, 1024), (5, 5120, 1024), (16, 5120, 1024), (32, 5120, 1024), (64, 1024, 2048),
+    (33, 16, 1024), (7, 100, 128),
+    # prefill (M = tokens), engine/runner.py:329-332, :365; ragged M and N tails
+    (65, 2048, 1024), (300, 512, 1024), (1000, 1024, 2048), (129, 100, 256), (4096, 2048, 1024),
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemm_2d_vs_oracle(pkg, dev, M, N, K):
+    say(f"gemm_2d M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    y = pkg.gemm_2d(x.to(dev), w.to(dev))
+    check(y, x, w)
+
+
+def test_gemm_2d_identity_is_exact(pkg, dev):
+    say("gemm_2d identity weight, M=100 and M=3")
+    g = torch.Generator().manual_seed(5)
+    eye = torch.eye(256).bfloat16().to(dev)
+    for M in (3, 100):
+        x = torch.randn(M, 256, generator=g).bfloat16()
+        assert torch.equal(pkg.gemm_2d(x.to(dev), eye).cpu(), x)
+
+
+def test_gemm_2d_strided_inputs(pkg, dev):
+    say("gemm_2d row-strided x (slice of a wider row) and transposed weight, M=40 and M=300")
+    g = torch.Generator().manual_seed(6)
+    wt = (torch.randn(1024, 512, generator=g) * 0.05).bfloat16()   # weight^T storage
+    for M in (40, 300):
+        wide = torch.randn(M, 1536, generator=g).bfloat16()
+        x = wide[:, 256:1280]                  # row stride 1536, K contiguous
+        y = pkg.gemm_2d(wide.to(dev)[:, 256:1280], wt.to(dev).t())  # weight K-strided
+        check(y, x, wt.t())
+
+
+def test_gemm_2d_graph_replays(pkg, dev):
+    say("gemm_2d captured in a graph, replayed 4x with eager work between")
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(32, 1024, generator=g).bfloat16().to(dev)
+    xl = torch.randn(256, 1024, generator=g).bfloat16().to(dev)
+    w = (torch.randn(5120, 1024, generator=g) * 0.05).bfloat16().to(dev)
+    ref_s, ref_l = pkg.gemm_2d(x, w), pkg.gemm_2d(xl, w)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ys, yl = pkg.gemm_2d(x, w), pkg.gemm_2d(xl, w)
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys, ref_s) and torch.equal(yl, ref_l)
+        _ = (xl * 2).sum().item()

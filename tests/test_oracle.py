@@ -283,3 +283,31 @@ def test_rmsnorm_oracle_special_cases():
     # power-of-two scaling of the input leaves the output unchanged
     x = torch.randn(4, 256, generator=gen).to(torch.bfloat16)
     assert torch.equal(orc.qwen_rmsnorm(x, w, 1e-12), orc.qwen_rmsnorm(x * 8, w, 1e-12))
+
+
+def test_gemm_oracle_brute_force():
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(3, 5, generator=g).bfloat16()
+    w = torch.randn(4, 5, generator=g).bfloat16()
+    ref = orc.gemm_2d(x, w)
+    for m in range(3):
+        for n in range(4):
+            acc = 0.0
+            for k in range(5):
+                acc += float(x[m, k]) * float(w[n, k])
+            assert abs(acc - float(ref[m, n])) < 1e-12
+
+
+def test_gemm_oracle_special_cases():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(6, 128, generator=g).bfloat16()
+    eye = torch.eye(128).bfloat16()
+    assert torch.equal(orc.gemm_2d(x, eye).bfloat16(), x)  # identity weight
+    sel = torch.zeros(3, 128).bfloat16()
+    for n, c in enumerate((7, 0, 127)):
+        sel[n, c] = 1.0
+    assert torch.equal(orc.gemm_2d(x, sel).bfloat16(), x[:, [7, 0, 127]])  # one-hot rows
+    w = torch.randn(9, 128, generator=g).bfloat16()
+    x2 = torch.randn(6, 128, generator=g).bfloat16()
+    lhs = orc.gemm_2d(x.double() + x2.double(), w)
+    assert torch.allclose(lhs, orc.gemm_2d(x, w) + orc.gemm_2d(x2, w), atol=1e-9)
