@@ -361,6 +361,10 @@ def main():
         del w5, sc5
         torch.cuda.empty_cache()
 
+    # ---- projection GEMMs around the attention path (wy_lib::gemm_2d) -----------
+    if want("gemm"):
+        extra["gemm_2d"] = gemm_bench(pkg, dev)
+
     if extra:
         result["extra"] = extra
 
@@ -398,6 +402,39 @@ def prefill_bench(pkg, dev, lengths, seed):
             "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "attainable_TFLOP/s": round(attain, 1), "frac_of_attainable": round(tf / attain, 4),
             "total_tokens": total, "lengths": lengths if len(lengths) <= 32 else None}
+
+
+def gemm_bench(pkg, dev):
+    """wy_lib::gemm_2d on the attention block's projection shapes, graph-timed,
+    next to torch.nn.functional.linear (hipBLASLt) on the same tensors.  Decode
+    shapes are HBM-bound (bytes = weight + x + y), prefill shapes MFMA-bound."""
+    gen = torch.Generator(device=dev).manual_seed(7)
+    shapes = [("decode B=32 q/gate/k/v fused [5120,1024]", 32, 5120, 1024),
+              ("decode B=32 o_proj [1024,2048]", 32, 1024, 2048),
+              ("decode B=1 q/gate/k/v fused [5120,1024]", 1, 5120, 1024),
+              ("prefill T=4096 q_proj [2048,1024]", 4096, 2048, 1024),
+              ("prefill T=4096 k_proj [512,1024]", 4096, 512, 1024),
+              ("prefill T=4096 o_proj [1024,2048]", 4096, 1024, 2048),
+              ("prefill T=16384 [6144,1024]", 16384, 6144, 1024)]
+    out = {}
+    for name, M, N, K in shapes:
+        x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+        wt = torch.randn(N, K, device=dev, generator=gen).to(torch.bfloat16)
+        ms = time_graph_events(lambda: pkg.gemm_2d(x, wt), 20)
+        ms_ref = time_graph_events(lambda: torch.nn.functional.linear(x, wt), 20)
+        fl, by = 2 * M * N * K, 2 * (M * K + N * K + M * N)
+        rec = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+               "hipblaslt_us": round(ms_ref * 1e3, 2)}
+        if M <= 64:
+            rec["GB/s"] = round(by / ms / 1e6, 1)
+            rec["frac_of_hbm_peak"] = round(by / ms / 1e6 / HBM_PEAK_GBS, 4)
+        else:
+            rec["TFLOP/s"] = round(fl / ms / 1e9, 1)
+            rec["frac_of_mfma_peak"] = round(fl / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)
+        out[name] = rec
+        log(f"gemm {name}: {rec}")
+        del x, wt
+    return out
 
 
 def cpu_baseline(w, lens):
