@@ -169,7 +169,7 @@ def main():
                     help="untimed steps first")
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
-    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill"],
+    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-gemm"],
                     help="pmc-*: eager launches only, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -227,6 +227,19 @@ def main():
             pkg.gqa_attention_varlen_causal(qp, kp, vp, cu4, max(lens4))
         torch.cuda.synchronize()
         print(json.dumps({"mode": "pmc-prefill", "flops": prefill_flops(lens4)}))
+        return
+    if args.mode == "pmc-gemm":
+        # gemm_2d on the decode (B=32) and prefill (T=4096) projection shapes,
+        # 5 eager calls each, for a per-kernel trace
+        gg = torch.Generator(device=dev).manual_seed(7)
+        for M, N, K in ((32, 5120, 1024), (32, 1024, 2048), (4096, 2048, 1024),
+                        (4096, 1024, 2048)):
+            x = torch.randn(M, K, device=dev, generator=gg).to(torch.bfloat16)
+            wt = torch.randn(N, K, device=dev, generator=gg).to(torch.bfloat16)
+            for _ in range(5):
+                pkg.gemm_2d(x, wt)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "pmc-gemm"}))
         return
     if args.mode == "pmc-copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
