@@ -22,7 +22,7 @@
 // scores outgrow it by more than 2^64 sends the block through an exact
 // two-pass recomputation.
 //
-// K and V tiles travel global -> LDS with global_load_lds_dwordx4 (no
+// K and V tiles travel global -> LDS as buffer loads with the LDS-DMA bit (no
 // registers), double-buffered: tile t+1 is in flight while tile t is
 // consumed, one barrier per tile.  LDS rows are padded so the MFMA operand
 // reads are conflict-free.  The DMAs are buffer loads whose range ends at the
@@ -213,18 +213,22 @@ void varlen_causal_prefill_kernel(
       st16(v_ring + o, u32x4_t{0u, 0u, 0u, 0u});
     __syncthreads();
   }
-  issue_first();
-
   // q row as the B operand of S^T, one 16-byte slice per 16-dim k-step,
   // pre-multiplied by scale*log2(e) and rounded to bf16 as the reference does
   // (gqa_attention_varlen_causal.py:146,158): scores come out in log2 units.
+  // The q loads are issued before the first tiles' DMA, so they do not queue
+  // behind it; the conversion waits for q only.
   bf16x8_t qb_op[16];
   {
     const int qc = qrow < n ? qrow : n - 1;
     const bf16_t *qp = q + (int64_t(start) + qc) * qs_t + hq * qs_h + g * 8;
+    u32x4_t xr[16];
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) xr[kk] = ld16(qp + 16 * kk);
+    issue_first();
 #pragma unroll
     for (int kk = 0; kk < 16; ++kk) {
-      u32x4_t x = ld16(qp + 16 * kk);
+      u32x4_t x = xr[kk];
       if (qrow >= n) x = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int w = 0; w < 4; ++w)
