@@ -318,6 +318,26 @@ def main():
             "what": "fused q/gate/k/v projection output -> o_proj input in one launch "
                     "(q/k RMSNorm, partial RoPE, append, split-K, merge, gate)"}
 
+        # the whole attention layer of a decode step (engine/runner.py:444-518):
+        # h [32, 1024] -> fused projection GEMM -> block -> o_proj GEMM
+        h = torch.randn(32, 1024, device=dev, generator=gen_b).to(torch.bfloat16)
+        w_qkvg = (torch.randn(5120, 1024, device=dev, generator=gen_b) * 0.03).to(torch.bfloat16)
+        w_o = (torch.randn(1024, 2048, device=dev, generator=gen_b) * 0.03).to(torch.bfloat16)
+
+        def layer(gemm):
+            f = gemm(h, w_qkvg)
+            packed = pkg.decode_attention_block(f, qw, kw, 1e-6, inv, 64, w["pos"], w["kc"],
+                                                w["vc"], w["bt"], scratch)
+            return gemm(packed, w_o)
+
+        msl = time_graph(lambda: layer(pkg.gemm_2d), args.steps, args.warmup)
+        msl_ref = time_graph(lambda: layer(torch.nn.functional.linear), args.steps, args.warmup)
+        extra["config2_attention_layer"] = {
+            "us_per_step": round(msl * 1e3, 2),
+            "us_per_step_with_hipblaslt_gemms": round(msl_ref * 1e3, 2),
+            "what": "h [32,1024] -> gemm_2d [5120,1024] -> attention block -> gemm_2d o_proj "
+                    "[1024,2048], one graph (3 launches)"}
+
     # ---- config 1: B=1, 256 tokens, contiguous table --------------------------
     if want("c1"):
         w1 = decode_workload([256], dev, seed=1, contiguous=True)
