@@ -27,22 +27,25 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // ------------------------------------------------------------ skinny (M <= 64)
 constexpr int kSkinnyMaxM = 64;
 
-template <int kNW, int kMT>
+template <int kNW, int kMT, int kNT>
 __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K) {
-  // kMT = ceil(M / 16) tiles of 16 rows; every load of a 4-step batch is
+  // kMT = ceil(M / 16) tiles of 16 rows, kNT tiles of 16 columns per
+  // workgroup (each x load feeds kNT MFMAs); every load of a 4-step batch is
   // issued before the first MFMA consumes one, so a wave waits for memory once
   // per 128 columns of K rather than once per load.
-  __shared__ f32x4v_t red[kNW][kMT][64];
+  __shared__ f32x4v_t red[kNW][kMT * kNT][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * kNT;
   const int kc = K / kNW;  // a multiple of 32 (host)
   const int kb = wave * kc;
   const int g = lane >> 4;
-  const int nrow = min(n0 + (lane & 15), N - 1);
-  const bf16_t *wp = w + int64_t(nrow) * ws0 + kb + 8 * g;
+  const bf16_t *wp[kNT];
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt)
+    wp[nt] = w + int64_t(min(n0 + 16 * nt + (lane & 15), N - 1)) * ws0 + kb + 8 * g;
   const bf16_t *xp[kMT];
   bool xok[kMT];
 #pragma unroll
@@ -51,20 +54,26 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     xok[mt] = row < M;
     xp[mt] = x + int64_t(xok[mt] ? row : 0) * xs0 + kb + 8 * g;
   }
-  f32x4v_t acc[kMT];
+  f32x4v_t acc[kMT][kNT];
 #pragma unroll
-  for (int mt = 0; mt < kMT; ++mt) acc[mt] = f32x4v_t{0.f, 0.f, 0.f, 0.f};
-  auto step = [&](const u32x4_t &wv, u32x4_t xv, int mt) {
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) acc[mt][nt] = f32x4v_t{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](const u32x4_t (&wv)[kNT], u32x4_t xv, int mt) {
     if (!xok[mt]) xv = u32x4_t{0u, 0u, 0u, 0u};
-    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv),
-                                                      __builtin_bit_cast(bf16x8_t, wv), acc[mt],
-                                                      0, 0, 0);
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          __builtin_bit_cast(bf16x8_t, xv), __builtin_bit_cast(bf16x8_t, wv[nt]), acc[mt][nt], 0,
+          0, 0);
   };
   int k = 0;
   for (; k + 128 <= kc; k += 128) {
-    u32x4_t wv[4], xv[kMT][4];
+    u32x4_t wv[4][kNT], xv[kMT][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wv[j] = ld16(wp + k + 32 * j);
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) wv[j][nt] = ld16(wp[nt] + k + 32 * j);
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
@@ -75,22 +84,28 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
       for (int mt = 0; mt < kMT; ++mt) step(wv[j], xv[mt][j], mt);
   }
   for (; k < kc; k += 32) {
-    const u32x4_t wv = ld16(wp + k);
+    u32x4_t wv[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) wv[nt] = ld16(wp[nt] + k);
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt) step(wv, ld16(xp[mt] + k), mt);
   }
 
-  // lane l of tile mt holds rows mt*16 + 4(l/16) + i (i = 0..3) of column l%16
+  // lane l of tile (mt, nt) holds rows mt*16 + 4(l/16) + i (i = 0..3) of
+  // column 16 nt + l%16
 #pragma unroll
-  for (int mt = 0; mt < kMT; ++mt) red[wave][mt][lane] = acc[mt];
+  for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) red[wave][mt * kNT + nt][lane] = acc[mt][nt];
   __syncthreads();
-  for (int e = threadIdx.x; e < M * 16; e += 64 * kNW) {
-    const int row = e >> 4, col = e & 15;
+  for (int e = threadIdx.x; e < M * 16 * kNT; e += 64 * kNW) {
+    const int row = e / (16 * kNT), cc = e - row * (16 * kNT);
+    const int nt = cc >> 4, col = cc & 15;
     const int mt = row >> 4, src = col + 16 * ((row & 15) >> 2), i = row & 3;
     float s = 0.f;
 #pragma unroll
-    for (int wv = 0; wv < kNW; ++wv) s += red[wv][mt][src][i];
-    if (n0 + col < N) y[int64_t(row) * ys0 + n0 + col] = bf16_t(f32_to_bf16_bits(s));
+    for (int wv = 0; wv < kNW; ++wv) s += red[wv][mt * kNT + nt][src][i];
+    if (n0 + cc < N) y[int64_t(row) * ys0 + n0 + cc] = bf16_t(f32_to_bf16_bits(s));
   }
 }
 
@@ -234,21 +249,21 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
   return wyh::launch_status();
 }
 
-template <int kNW, int kMT>
+template <int kNW, int kMT, int kNT>
 void launch_skinny(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                    int64_t ys0, int M, int N, int K, hipStream_t st) {
-  gemm_skinny_kernel<kNW, kMT><<<dim3(unsigned((N + 15) / 16)), 64 * kNW, 0, st>>>(
-      x, xs0, w, ws0, y, ys0, M, N, K);
+  gemm_skinny_kernel<kNW, kMT, kNT><<<dim3(unsigned((N + 16 * kNT - 1) / (16 * kNT))), 64 * kNW,
+                                      0, st>>>(x, xs0, w, ws0, y, ys0, M, N, K);
 }
 
-template <int kNW>
+template <int kNW, int kNT>
 void launch_skinny_m(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                      int64_t ys0, int M, int N, int K, hipStream_t st) {
   switch ((M + 15) / 16) {
-    case 1: launch_skinny<kNW, 1>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
-    case 2: launch_skinny<kNW, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
-    case 3: launch_skinny<kNW, 3>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
-    default: launch_skinny<kNW, 4>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
+    case 1: launch_skinny<kNW, 1, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
+    case 2: launch_skinny<kNW, 2, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
+    case 3: launch_skinny<kNW, 3, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
+    default: launch_skinny<kNW, 4, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
   }
 }
 
@@ -269,15 +284,24 @@ extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w
   const bf16_t *wb = static_cast<const bf16_t *>(w);
   bf16_t *yb = static_cast<bf16_t *>(y);
   if (M <= kSkinnyMaxM) {
-    // waves per workgroup: enough workgroups x waves to keep the CUs streaming,
-    // each wave at least one 128-wide batch of k
-    const int blocks = (N + 15) / 16;
+    // Columns per workgroup: 32 when that still leaves >= 128 workgroups (each
+    // x load then feeds two column tiles, halving the x bytes per column),
+    // else 16.  Waves per workgroup: enough workgroups x waves to keep the CUs
+    // streaming, each wave at least one 128-wide batch of k.
+    const int nt = N >= 4096 ? 2 : 1;
+    const int blocks = (N + 16 * nt - 1) / (16 * nt);
     int nw = 4;
     while (nw < 16 && blocks * nw < 2048 && K / (2 * nw) >= 128) nw *= 2;
     const int64_t xs = x_strides[0], wsd = w_strides[0], ys = y_strides[0];
-    if (nw == 4) launch_skinny_m<4>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
-    else if (nw == 8) launch_skinny_m<8>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
-    else launch_skinny_m<16>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    if (nt == 1) {
+      if (nw == 4) launch_skinny_m<4, 1>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+      else if (nw == 8) launch_skinny_m<8, 1>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+      else launch_skinny_m<16, 1>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    } else {
+      if (nw == 4) launch_skinny_m<4, 2>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+      else if (nw == 8) launch_skinny_m<8, 2>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+      else launch_skinny_m<16, 2>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    }
     return wyh::launch_status();
   }
   // 32-bit buffer offsets within one 128-row band
