@@ -394,6 +394,10 @@ def main():
         del w5, sc5
         torch.cuda.empty_cache()
 
+    # ---- config 3's HBM-bound companions: RoPE, page scatter, gate pack --------
+    if want("c3ew"):
+        extra["config3_elementwise"] = elementwise_bench(pkg, dev)
+
     # ---- projection GEMMs around the attention path (wy_lib::gemm_2d) -----------
     if want("gemm"):
         extra["gemm_2d"] = gemm_bench(pkg, dev)
@@ -435,6 +439,51 @@ def prefill_bench(pkg, dev, lengths, seed):
             "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "attainable_TFLOP/s": round(attain, 1), "frac_of_attainable": round(tf / attain, 4),
             "total_tokens": total, "lengths": lengths if len(lengths) <= 32 else None}
+
+
+def elementwise_bench(pkg, dev):
+    """Config 3 (32 x 128 tokens): partial RoPE of q and k, the K/V page scatter
+    and the sigmoid gate pack, graph-timed, as algorithmic HBM GB/s (every byte
+    the op must read and write once)."""
+    gen = torch.Generator(device=dev).manual_seed(3)
+    T, nseq = 4096, 32
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, generator=gen).to(torch.bfloat16)
+
+    q, k, v = rnd(T, HQ, D), rnd(T, HKV, D), rnd(T, HKV, D)
+    pos_ids = torch.arange(128, device=dev).repeat(nseq).view(1, T)
+    inv = pkg.rope_inv_freq(64, 1e7, device=dev)
+    cu = torch.arange(0, T + 1, 128, dtype=torch.int32, device=dev)
+    pages_per_seq = 128 // PAGE + 1
+    num_pages = nseq * pages_per_seq
+    bt = torch.randperm(num_pages, device=dev, generator=gen).view(nseq, pages_per_seq)
+    bt = bt.to(torch.int32).contiguous()
+    kc = torch.zeros(num_pages, HKV, PAGE, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    x4, g4 = rnd(1, HQ, T, D), rnd(1, HQ, T, D)
+    cases = {
+        "partial_rope q [1,8,4096,256] (permuted view)":
+            (lambda: pkg.partial_rope(q.permute(1, 0, 2).unsqueeze(0), pos_ids, inv, 64),
+             2 * T * HQ * D * 2),
+        "partial_rope k [1,2,4096,256] (permuted view)":
+            (lambda: pkg.partial_rope(k.permute(1, 0, 2).unsqueeze(0), pos_ids, inv, 64),
+             2 * T * HKV * D * 2),
+        "paged_kv_fill_varlen 32 x 128 tokens":
+            (lambda: pkg.paged_kv_fill_varlen(kc, vc, k.permute(1, 0, 2), v.permute(1, 0, 2),
+                                              bt, cu, 128),
+             4 * T * HKV * D * 2),
+        "attention_gate_pack [1,8,4096,256]":
+            (lambda: pkg.attention_gate_pack(x4, g4), 3 * T * HQ * D * 2),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        ms = time_graph_events(fn, 20)
+        out[name] = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / ms / 1e6, 1),
+                     "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "bytes": nbytes}
+        log(f"elementwise {name}: {out[name]}")
+    return out
 
 
 def gemm_bench(pkg, dev):

@@ -14,46 +14,85 @@ __device__ __forceinline__ float load_pos(const void *pos, int64_t off, bool is6
 }
 
 // ------------------------------------------------------------ partial RoPE --
-// Fast path: lanes own 16-byte chunks of a row.  A chunk in the first rotary
-// half also produces its partner chunk R/2 further on; chunks of the second
-// half idle; tail chunks are copied verbatim.  Reference: partial_rope.py:34-132.
+// Fast path.  The grid's first part rotates: a lane owns chunk c (8 dims) of
+// the first rotary half of one (b, t) row for two heads, so its 8 sin/cos
+// pairs (which depend on (b, t, j) only) serve both; each head's chunk c and
+// partner chunk c + R/16 are rotated together.
+// The second part copies the tail chunks [R/8, D/8) of every (b, t, h) row.
+// The two kinds of work sit in different wavefronts, so neither waits on the
+// other's branch.  Reference: partial_rope.py:34-132.
+constexpr int kRopeHeads = 2;  // heads per rotating lane
+
 __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
     const bf16_t *__restrict__ x, int64_t xs_b, int64_t xs_h, int64_t xs_t,
     bf16_t *__restrict__ out, int64_t os_b, int64_t os_h, int64_t os_t,
     const void *__restrict__ pos, int64_t ps_b, int64_t ps_t, int pos64,
-    const float *__restrict__ inv_freq, int H, int T, int D, int R, int64_t rows) {
-  const int cpr = D / 8;
-  const int64_t gid = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t row = gid / cpr;
-  if (row >= rows) return;
-  const int c = int(gid - row * cpr);
-  const int t = int(row % T);
-  const int64_t bh = row / T;
-  const int h = int(bh % H);
-  const int b = int(bh / H);
-  const bf16_t *xr = x + b * xs_b + h * xs_h + t * xs_t;
-  bf16_t *orow = out + b * os_b + h * os_h + t * os_t;
-  const int half_chunks = R / 16;
-  if (c < half_chunks) {
+    const float *__restrict__ inv_freq, int H, int T, int D, int R, uint32_t bt_rows) {
+  // index math in 32 bits: the host launches this kernel only when the grid
+  // and row counts fit
+  const uint32_t half_chunks = uint32_t(R) / 16u;
+  const uint32_t hgroups = uint32_t(H + kRopeHeads - 1) / kRopeHeads;
+  const uint32_t n_rot = bt_rows * half_chunks * hgroups;
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  if (gid < n_rot) {
+    // lane -> (b, t, head group, chunk), chunk fastest
+    const uint32_t q1 = gid / half_chunks;
+    const int c = int(gid - q1 * half_chunks);
+    const uint32_t bt = q1 / hgroups;
+    const int h0 = int(q1 - bt * hgroups) * kRopeHeads;
+    const int t = int(bt % uint32_t(T)), b = int(bt / uint32_t(T));
+    const bf16_t *xr = x + b * xs_b + t * xs_t;
+    bf16_t *orow = out + b * os_b + t * os_t;
     const float p = load_pos(pos, b * ps_b + int64_t(t) * ps_t, pos64 != 0);
-    const u32x4_t a = ld16(xr + c * 8);
-    const u32x4_t bb = ld16(xr + R / 2 + c * 8);
-    u32x4_t oa, ob;
+    u32x4_t a[kRopeHeads], bb[kRopeHeads];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      float o1l, o2l, o1h, o2h, sl, cl, sh, ch;
-      rope_sincos(p, inv_freq[c * 8 + 2 * w], sl, cl);
-      rope_sincos(p, inv_freq[c * 8 + 2 * w + 1], sh, ch);
-      rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), cl, sl, o1l, o2l);
-      rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), ch, sh, o1h, o2h);
-      oa[w] = pack_bf16x2(o1l, o1h);
-      ob[w] = pack_bf16x2(o2l, o2h);
+    for (int i = 0; i < kRopeHeads; ++i) {
+      const int h = min(h0 + i, H - 1);
+      a[i] = ld16(xr + h * xs_h + c * 8);
+      bb[i] = ld16(xr + h * xs_h + R / 2 + c * 8);
     }
-    st16(orow + c * 8, oa);
-    st16(orow + R / 2 + c * 8, ob);
-  } else if (c >= 2 * half_chunks) {
-    st16(orow + c * 8, ld16(xr + c * 8));
+    float sn[8], cs[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) rope_sincos(p, inv_freq[c * 8 + e], sn[e], cs[e]);
+#pragma unroll
+    for (int i = 0; i < kRopeHeads; ++i) {
+      if (h0 + i >= H) break;
+      u32x4_t oa, ob;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float o1l, o2l, o1h, o2h;
+        rope_rotate(bf16_lo(a[i][w]), bf16_lo(bb[i][w]), cs[2 * w], sn[2 * w], o1l, o2l);
+        rope_rotate(bf16_hi(a[i][w]), bf16_hi(bb[i][w]), cs[2 * w + 1], sn[2 * w + 1], o1h,
+                    o2h);
+        oa[w] = pack_bf16x2(o1l, o1h);
+        ob[w] = pack_bf16x2(o2l, o2h);
+      }
+      st16(orow + (h0 + i) * os_h + c * 8, oa);
+      st16(orow + (h0 + i) * os_h + R / 2 + c * 8, ob);
+    }
+    return;
   }
+  // rows in memory order: heads fastest when x's head stride is the smaller
+  // one (the [T, H, D] buffer the prefill passes as a permuted view), tokens
+  // fastest otherwise
+  const uint32_t tail = uint32_t(D - R) / 8u;
+  const uint32_t k = gid - n_rot;
+  const uint32_t row = k / tail;
+  if (row >= bt_rows * uint32_t(H)) return;
+  const int c = R / 8 + int(k - row * tail);
+  int t, h, b;
+  if (xs_h < xs_t) {
+    h = int(row % uint32_t(H));
+    const uint32_t bt = row / uint32_t(H);
+    t = int(bt % uint32_t(T));
+    b = int(bt / uint32_t(T));
+  } else {
+    t = int(row % uint32_t(T));
+    const uint32_t bh = row / uint32_t(T);
+    h = int(bh % uint32_t(H));
+    b = int(bh / uint32_t(H));
+  }
+  st16(out + b * os_b + h * os_h + t * os_t + c * 8, ld16(x + b * xs_b + h * xs_h + t * xs_t + c * 8));
 }
 
 // Generic path: one lane per output element, any strides, any even R <= D.
@@ -145,15 +184,19 @@ extern "C" int wy_partial_rope(const void *x, const int64_t *xs, void *out,
   if (rows == 0) return WY_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool vec = head_dim % 8 == 0 && rotary_dim % 16 == 0 && xs[3] == 1 &&
+                   rows * (head_dim / 8) + 256 < int64_t(INT32_MAX) &&
                    os[3] == 1 && xs[0] % 8 == 0 && xs[1] % 8 == 0 && xs[2] % 8 == 0 &&
                    os[0] % 8 == 0 && os[1] % 8 == 0 && os[2] % 8 == 0 &&
                    wyh::aligned16(x) && wyh::aligned16(out);
   if (vec) {
-    const int64_t n = rows * (head_dim / 8);
+    const int64_t bt_rows = int64_t(batch) * num_tokens;
+    // rotating lanes walk the heads; tail lanes copy one chunk each
+    const int64_t n = bt_rows * (rotary_dim / 16) * ((num_heads + 1) / 2) +
+                      bt_rows * num_heads * (head_dim / 8 - rotary_dim / 8);
     partial_rope_vec_kernel<<<blocks_for(n), 256, 0, s>>>(
         static_cast<const bf16_t *>(x), xs[0], xs[1], xs[2], static_cast<bf16_t *>(out),
         os[0], os[1], os[2], position_ids, ps[0], ps[1], pos_is_int64, inv_freq,
-        num_heads, num_tokens, head_dim, rotary_dim, rows);
+        num_heads, num_tokens, head_dim, rotary_dim, uint32_t(bt_rows));
   } else {
     const int64_t n = rows * head_dim;
     partial_rope_generic_kernel<<<blocks_for(n), 256, 0, s>>>(
