@@ -147,6 +147,14 @@ int wy_paged_decode_step(const void *q, const int64_t *q_strides, const void *k_
  * q/out [total, H_q, D], k/v [total, H_kv, D] bf16 (innermost stride must be
  * 1, rows 16-byte aligned).  max_seqlen is the host-side longest length and
  * total_tokens = q.shape[0].  Allocates nothing; one kernel launch.
+ * workspace: NULL / 0 bytes, or at least
+ * wy_varlen_causal_prefill_workspace_bytes(batch, num_kv_heads, max_seqlen)
+ * bytes of 4-byte aligned device memory holding two int32 counters that are
+ * zero before the first call (each call leaves them zero).  With it a
+ * persistent grid of one workgroup per CU draws the active query blocks,
+ * heaviest first, from a shared ticket counter; without it there is one
+ * workgroup per query block.  Results are identical.  Calls that may run
+ * concurrently need distinct workspaces.
  * Replaces wy_lib::gqa_attention_varlen_causal
  *   (triton_kernels/gqa_attention_varlen_causal.py:214-278, kernel :101-210).
  */
@@ -156,7 +164,18 @@ int wy_varlen_causal_prefill(const void *q, const int64_t *q_strides,
                              const int64_t *out_strides,
                              const int32_t *cu_seqlens, int batch,
                              int num_q_heads, int num_kv_heads, int head_dim,
-                             int max_seqlen, int64_t total_tokens, void *stream);
+                             int max_seqlen, int64_t total_tokens, void *workspace,
+                             int64_t workspace_bytes, void *stream);
+
+/*
+ * Workspace bytes wy_varlen_causal_prefill uses for its queue launch on the
+ * current device: 8 (two int32 counters), or 0 when the grid of
+ * ceil(max_seqlen / 32) * batch * num_kv_heads query blocks fits the device's
+ * CUs in one round or batch + ceil(max_seqlen / 32) + 1 exceeds 4096 (then the
+ * one-workgroup-per-block launch is used).  No counterpart in the reference
+ * (its launch takes no workspace).
+ */
+int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_kv_heads, int max_seqlen);
 
 /*
  * Partial rotate-half RoPE on dims [0, rotary_dim) of x [B, H, T, D] bf16;

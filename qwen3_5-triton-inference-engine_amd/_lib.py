@@ -36,7 +36,7 @@ _SIGNATURES = {
                              _c_i64p, _vp, _i64, _vp, _vp, _vp, _vp, _c_i64p, _c_i64p, _vp,
                              _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _i, _i, _i, _vp],
     "wy_varlen_causal_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
-                                 _vp, _i, _i, _i, _i, _i, _i64, _vp],
+                                 _vp, _i, _i, _i, _i, _i, _i64, _vp, _i64, _vp],
     "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,
                         _i, _vp],
     "wy_attention_gate_pack": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _i, _vp],
@@ -72,6 +72,8 @@ def load() -> ctypes.CDLL:
     lib.wy_status_string.restype = ctypes.c_char_p
     lib.wy_build_info.argtypes = []
     lib.wy_build_info.restype = ctypes.c_char_p
+    lib.wy_varlen_causal_prefill_workspace_bytes.argtypes = [_i, _i, _i]
+    lib.wy_varlen_causal_prefill_workspace_bytes.restype = ctypes.c_int64
     _lib = lib
     return lib
 

@@ -58,6 +58,7 @@ struct DecodeArgs {
   int min_pps;
   int hkv;
   int batch;
+  int bt_cols;  // entries per block-table row (max_pages)
   // fused step only
   const bf16_t *kn, *vn;
   int64_t kn_b, kn_h, vn_b, vn_h;
@@ -250,7 +251,30 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   const int b = blockIdx.x % a.batch;
   const int h = (blockIdx.x / a.batch) % a.hkv;
   const int s = blockIdx.x / (a.batch * a.hkv);
-  const int seq_len = int(a.pos[b]) + 1;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  typedef const __attribute__((address_space(4))) int32_t *bt_const_t;
+  const int32_t *btrow = a.bt + b * a.bt_b;
+  const bt_const_t bt_s = (bt_const_t)btrow;
+  // The block-table entry of this wave's first page is requested together
+  // with pos, for the usual partition (pps == min_pps), instead of after it:
+  // the first page's address then costs one memory round trip, not two.
+  // The q rows are requested at the same time.  (pos < 2^31: its low word.)
+  const int first_guess = s * a.min_pps + wave;
+  const int32_t *bt_first = btrow + (first_guess < a.bt_cols ? first_guess : a.bt_cols - 1);
+  const int r_q = threadIdx.x >> 5, c_q = (threadIdx.x & 31) * 8;
+  const bf16_t *q_src = a.q + b * a.qs_b + (h * kG + r_q) * a.qs_h + c_q;
+  const bool q_fast = threadIdx.x < kG * kD / 8 && (kProlog || a.qs_d == 1);
+  u32x4_t q_pre = {0u, 0u, 0u, 0u};
+  if (q_fast) q_pre = ld16(q_src);
+  int32_t bt_guess, pos_lo;
+  asm volatile(
+      "s_load_dword %0, %2, 0x0\n\t"
+      "s_load_dword %1, %3, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=s"(pos_lo), "=s"(bt_guess)
+      : "s"(a.pos + b), "s"(bt_first)
+      : "memory");
+  const int seq_len = pos_lo + 1;
   const int npg = (seq_len + kPage - 1) / kPage;
   const int pps = split_pps(npg, a.min_pps);
   const int nact = (npg + pps - 1) / pps;
@@ -258,7 +282,6 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   const int p0 = s * pps;
   const int p1 = min(p0 + pps, npg);
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, g4 = lane >> 4;
 
   float m_run[kG], l_run[kG], acc[kG][4];
@@ -272,7 +295,6 @@ void paged_decode_split_kernel(const DecodeArgs a) {
 
   const bf16_t *kh = a.kc + h * a.kc_h;
   const bf16_t *vh = a.vc + h * a.vc_h;
-  const int32_t *btrow = a.bt + b * a.bt_b;
   const int last_page = (seq_len - 1) / kPage;
   const int last_slot = (seq_len - 1) % kPage;
   const bf16_t *knrow = nullptr, *vnrow = nullptr;
@@ -286,9 +308,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   // launch), one page ahead, so a page's address never waits on the vector
   // memory counter that its K/V loads share.
   const int npw = p0 + wave < p1 ? (p1 - p0 - wave + kW - 1) / kW : 0;
-  typedef const __attribute__((address_space(4))) int32_t *bt_const_t;
-  const bt_const_t bt_s = (bt_const_t)btrow;
-  int32_t bt_ahead = npw > 0 ? bt_s[p0 + wave] : 0;
+  int32_t bt_ahead = npw > 0 ? (pps == a.min_pps ? bt_guess : bt_s[p0 + wave]) : 0;
   // Register pipeline, no extra registers: K of page i+1 is requested as soon
   // as the score MFMAs have consumed K of page i, and V of page i+1 as soon as
   // P.V has consumed V of page i, so each load overlaps the other half of the
@@ -397,7 +417,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     // RMSNorm: 32 lanes per row, 8 elements each (rms_rsigma's layout).
     if (threadIdx.x < kG * kD / 8) {
       const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
-      const u32x4_t xw = ld16(a.q + b * a.qs_b + (h * kG + r) * a.qs_h + c);
+      const u32x4_t xw = q_pre;  // q row r, dims c..c+7 (r == r_q, c == c_q)
       const u32x4_t ww = ld16(a.qw + c);
       const float ss = rms_acc8(xw, 0.f);
       const float rs = rms_rsigma(ss, kD, a.eps);
@@ -422,8 +442,8 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     const int r = threadIdx.x >> 5, c = (threadIdx.x & 31) * 8;
     const bf16_t *qrow = a.q + b * a.qs_b + (h * kG + r) * a.qs_h;
     u32x4_t w;
-    if (a.qs_d == 1) {
-      w = ld16(qrow + c);
+    if (q_fast) {
+      w = q_pre;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -699,6 +719,7 @@ int launch_split(const DecodeArgs &args, int batch, int num_kv_heads, int max_pa
                  void *stream) {
   DecodeArgs a = args;
   a.batch = batch;
+  a.bt_cols = max_pages;
   const dim3 grid(unsigned(batch) * unsigned(num_kv_heads) *
                   unsigned(split_grid_z(max_pages, min_pps)));
   return launch_split_w<kFused, kWaves, kProlog>(grid, a, static_cast<hipStream_t>(stream));

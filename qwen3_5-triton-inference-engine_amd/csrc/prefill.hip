@@ -27,8 +27,10 @@
 // consumed, one barrier per tile.  LDS rows are padded so the MFMA operand
 // reads are conflict-free.  The DMAs are buffer loads whose range ends at the
 // sequence's last row, so rows past the end are never fetched; their scores
-// are masked to -inf, so their P is exactly 0.  Query blocks are launched
-// heaviest first (LPT), spread over the XCDs.
+// are masked to -inf, so their P is exactly 0.  Query blocks run heaviest
+// first (LPT): as a grid of one workgroup per block when that grid fits the
+// chip, otherwise as a persistent grid of one workgroup per CU drawing blocks
+// from a shared ticket counter.
 #include <type_traits>
 
 #include "wy_common.h"
@@ -58,6 +60,8 @@ constexpr int kLdsBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 Ki
 // Exponentials are taken against a per-row reference fixed by the first KV
 // tile; a later score may exceed it by a factor up to 2^64 (P stays finite in
 // bf16 and fp32).  Beyond that the block is recomputed exactly.
+// LDS of the queue launch's ticket -> block map: n_seq + n_qblocks + 1 ints.
+constexpr int kPlanLds = 4096;
 constexpr float kHeadroomScale = 18446744073709551616.0f;  // 2^64
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -104,6 +108,7 @@ __device__ __forceinline__ int k_row_token(int row) {
 
 
 // ------------------------------------------------------------------ attention
+template <bool kList>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h,
@@ -111,28 +116,131 @@ void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t *__restrict__ out,
     int64_t os_t,
     int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
-    int n_kv_heads, int n_qblocks) {
+    int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters) {
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_next_item;
+  __shared__ int s_scan[256];
+  __shared__ int plan_lds[kPlanLds];
 
-  // 1-D launch, heaviest query blocks first (LPT).  Workgroups are dealt to
-  // the 8 XCDs round-robin by id; rotating the (sequence, head) order by one
-  // per slice spreads every sequence over all XCDs instead of pinning it to
-  // XCD (b*H_kv + h) % 8.
   const int bh_count = n_seq * n_kv_heads;
-  const int slice = blockIdx.x / bh_count;
-  const int bh = (blockIdx.x - slice * bh_count + slice) % bh_count;
-  const int b = bh / n_kv_heads, h = bh - b * n_kv_heads;
-  const int qb = n_qblocks - 1 - slice;
-  const int start = cu[b];
-  const int n = cu[b + 1] - start;
-  const int q0 = qb * kBQ;
-  if (q0 >= n) return;
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;     // k-group / row-quad selector of the MFMA layouts
   const int col = lane & 31;   // query row within the block
+
+  // LDS: a two-slot ring of K tiles, then a two-slot ring of V tiles.  K
+  // runs one tile ahead of V: iteration t computes S^T of tile t+1 (MFMA)
+  // while the VALU turns S^T of tile t into P, then runs PV of tile t.
+  unsigned char *const k_ring = smem;
+  unsigned char *const v_ring = smem + 2 * kTileK;
+
+  // Work distribution.  Direct launch (grid = every query block): one block
+  // per workgroup, heaviest first (LPT); workgroups are dealt to the 8 XCDs
+  // round-robin by id, and rotating the (sequence, head) order by one per
+  // slice spreads every sequence over all XCDs.  Queue launch (a persistent
+  // grid of one workgroup per CU): the active query blocks, heaviest first,
+  // are numbered by tickets drawn from a counter shared by all workgroups, so
+  // a CU that finishes early takes the next block at once instead of waiting
+  // for the in-order dispatcher, and inactive blocks cost nothing.  Each
+  // workgroup derives the ticket -> block map itself (sequence lengths and
+  // per-slice prefix counts in LDS); the next ticket is requested at the
+  // start of each block, so its latency hides behind the block.
+  int item = int(blockIdx.x);
+  int n_items = 0;
+  int *const lens = plan_lds;               // [n_seq] sequence lengths
+  int *const pre = plan_lds + n_seq;        // [n_qblocks + 1] tickets before slice s
+  if constexpr (kList) {
+    if (tid == 0) s_next_item = atomicAdd(&counters[0], 1);
+    for (int i = tid; i < n_seq; i += 256) lens[i] = cu[i + 1] - cu[i];
+    __syncthreads();
+    // pre[s + 1] = H_kv * #{b : len_b > 32 * qb(s)}, qb(s) = n_qblocks - 1 - s;
+    // then an exclusive scan: each thread sums a contiguous run of slices,
+    // the run totals are scanned, and the runs are rewritten as prefixes.
+    const int per = (n_qblocks + 255) / 256;
+    const int s_lo = min(tid * per, n_qblocks), s_hi = min(s_lo + per, n_qblocks);
+    int run = 0;
+    for (int sl = s_lo; sl < s_hi; ++sl) {
+      const int thr = (n_qblocks - 1 - sl) * kBQ;
+      int c = 0;
+      for (int bb = 0; bb < n_seq; ++bb) c += lens[bb] > thr;
+      pre[sl + 1] = c * n_kv_heads;
+      run += c * n_kv_heads;
+    }
+    s_scan[tid] = run;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const int x = tid >= o ? s_scan[tid - o] : 0;
+      __syncthreads();
+      s_scan[tid] += x;
+      __syncthreads();
+    }
+    int acc = s_scan[tid] - run;
+    for (int sl = s_lo; sl < s_hi; ++sl) {
+      acc += pre[sl + 1];
+      pre[sl + 1] = acc;
+    }
+    if (tid == 0) pre[0] = 0;
+    __syncthreads();
+    n_items = pre[n_qblocks];
+    item = s_next_item;
+  }
+  for (;;) {
+  int b, h, qb;
+  if constexpr (kList) {
+    if (item >= n_items) {  // uniform: the queue is drained
+      // The last workgroup to get here leaves both counters at zero for the
+      // next launch (every workgroup has drawn its final ticket by then).
+      if (tid == 0 && atomicAdd(&counters[1], 1) == int(gridDim.x) - 1) {
+        __hip_atomic_store(&counters[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&counters[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
+    // slice: the last s with pre[s] <= item (64-ary search, one probe per lane)
+    int lo = 0, hi = n_qblocks;
+    while (hi - lo > 1) {
+      const int step = (hi - lo + 63) / 64;
+      const int probe = lo + lane * step;
+      const bool le = probe < hi && pre[probe] <= item;
+      const int k = 63 - __builtin_clzll(__ballot(le));  // lane 0 always qualifies
+      lo += k * step;
+      hi = min(lo + step, hi);
+    }
+    qb = n_qblocks - 1 - lo;
+    const int j = item - pre[lo];
+    const int pair = j / n_kv_heads;
+    h = j - pair * n_kv_heads;
+    // b: the pair-th sequence (ascending) longer than 32 * qb
+    const int thr = qb * kBQ;
+    int seen = 0;
+    b = 0;
+    for (int b0 = 0; b0 < n_seq; b0 += 64) {
+      const uint64_t m = __ballot(b0 + lane < n_seq && lens[b0 + lane] > thr);
+      const int c = __popcll(m);
+      if (pair < seen + c) {
+        // position of the (pair - seen)-th set bit of m
+        const bool mine = ((m >> lane) & 1) &&
+                          __popcll(m & ((uint64_t(1) << lane) - 1)) == pair - seen;
+        b = b0 + (__builtin_ctzll(__ballot(mine)));
+        break;
+      }
+      seen += c;
+    }
+  } else {
+    const int slice = item / bh_count;
+    const int bh = (item - slice * bh_count + slice) % bh_count;
+    b = bh / n_kv_heads;
+    h = bh - b * n_kv_heads;
+    qb = n_qblocks - 1 - slice;
+  }
+  int next_ticket = 0;
+  if (kList && tid == 0) next_ticket = atomicAdd(&counters[0], 1);
+  const int start = cu[b];
+  const int n = cu[b + 1] - start;
+  const int q0 = qb * kBQ;
+  if (q0 >= n) return;  // direct launch only (the queue holds active blocks only)
+
   const int hq = h * kG + wave;
   const int qrow = q0 + col;
 
@@ -140,12 +248,6 @@ void varlen_causal_prefill_kernel(
   const bf16_t *vseq = v + int64_t(start) * vs_t + h * vs_h;
   const int kv_end = min(q0 + kBQ, n);  // exclusive bound of keys any row can see
   const int n_tiles = (kv_end + kBN - 1) / kBN;
-
-  // LDS: a two-slot ring of K tiles, then a two-slot ring of V tiles.  K
-  // runs one tile ahead of V: iteration t computes S^T of tile t+1 (MFMA)
-  // while the VALU turns S^T of tile t into P, then runs PV of tile t.
-  unsigned char *const k_ring = smem;
-  unsigned char *const v_ring = smem + 2 * kTileK;
 
   // DMA one tile into a ring slot as wave-wide 1 KiB blocks (lane j fills
   // 16-byte slot 64*blk + j; pad slots get the row's first chunk, unread).
@@ -439,16 +541,60 @@ void varlen_causal_prefill_kernel(
         *reinterpret_cast<u32x2_t *>(op + dt * 32 + 8 * j + 4 * g) = w;
       }
   }
+  if constexpr (!kList) return;
+  // Every wave is past its last LDS read of this block before the next
+  // block's DMA refills the rings; s_next_item was last read before the
+  // barriers of this block's pass.
+  if (tid == 0) s_next_item = next_ticket;
+  __syncthreads();
+  item = s_next_item;
+  }
 }
 
 }  // namespace
+
+namespace {
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Query blocks of the launch grid: n_qblocks * batch * H_kv.
+int64_t prefill_blocks(int batch, int num_kv_heads, int max_seqlen) {
+  return int64_t((max_seqlen + kBQ - 1) / kBQ) * batch * num_kv_heads;
+}
+
+}  // namespace
+
+extern "C" int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_kv_heads,
+                                                            int max_seqlen) {
+  if (batch <= 0 || num_kv_heads <= 0 || max_seqlen <= 0) return 0;
+  const int64_t n_wg = prefill_blocks(batch, num_kv_heads, max_seqlen);
+  const int64_t n_qblocks = (max_seqlen + kBQ - 1) / kBQ;
+  const int cus = device_cus();
+  // A grid that fits the chip in one round gains nothing from the queue; the
+  // ticket -> block map must fit its LDS.
+  if (cus <= 0 || n_wg <= cus || n_wg > INT32_MAX || batch + n_qblocks + 1 > kPlanLds) return 0;
+  return 2 * int64_t(sizeof(int32_t));
+}
 
 extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const void *k,
                                         const int64_t *ks, const void *v,
                                         const int64_t *vs, void *out, const int64_t *os,
                                         const int32_t *cu_seqlens, int batch,
                                         int num_q_heads, int num_kv_heads, int head_dim,
-                                        int max_seqlen, int64_t total_tokens, void *stream) {
+                                        int max_seqlen, int64_t total_tokens, void *workspace,
+                                        int64_t workspace_bytes, void *stream) {
   if (!q || !qs || !k || !ks || !v || !vs || !out || !os || !cu_seqlens) return WY_E_NULL;
   if (batch < 0 || num_kv_heads <= 0 || max_seqlen < 0 || total_tokens < 0)
     return WY_E_SHAPE;
@@ -458,26 +604,43 @@ extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const 
       !wyh::aligned16(q) || !wyh::aligned16(k) || !wyh::aligned16(v) ||
       (reinterpret_cast<uintptr_t>(out) & 7u))
     return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return WY_E_LAYOUT;
   if (batch == 0 || max_seqlen == 0) return WY_OK;
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&varlen_causal_prefill_kernel),
+        reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<false>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return int(e);
     attr_set = true;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_qblocks = (max_seqlen + kBQ - 1) / kBQ;
-  const int64_t n_wg = int64_t(n_qblocks) * batch * num_kv_heads;
+  const int64_t n_wg = prefill_blocks(batch, num_kv_heads, max_seqlen);
   if (n_wg > INT32_MAX) return WY_E_SHAPE;
   // per-sequence DMA ranges are 32-bit byte offsets
   if (int64_t(max_seqlen) * ks[0] * 2 >= INT32_MAX || int64_t(max_seqlen) * vs[0] * 2 >= INT32_MAX)
     return WY_E_SHAPE;
-  varlen_causal_prefill_kernel<<<dim3(unsigned(n_wg)), 256, kLdsBytes, s>>>(
+  // Queue launch when the caller provides the two counters that
+  // wy_varlen_causal_prefill_workspace_bytes asks for; otherwise one
+  // workgroup per query block.
+  const int64_t need = wy_varlen_causal_prefill_workspace_bytes(batch, num_kv_heads, max_seqlen);
+  int32_t *counters = nullptr;
+  unsigned grid = unsigned(n_wg);
+  if (need > 0 && workspace_bytes >= need) {
+    counters = static_cast<int32_t *>(workspace);
+    grid = unsigned(device_cus());
+  }
+  auto *kern = counters ? varlen_causal_prefill_kernel<true> : varlen_causal_prefill_kernel<false>;
+  kern<<<dim3(grid), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
       ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],
       os[1], cu_seqlens,
-      kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks);
+      kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks, counters);
   return wyh::launch_status();
 }

@@ -50,8 +50,18 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
                                    dummy, dummy, s3, s4, 1, 8, 2, 128, 4, 4, None)
     assert rc == -4
     rc = lib.wy_varlen_causal_prefill(dummy, s3, dummy, s3, dummy, s3, dummy, s3, dummy,
-                                      1, 8, 2, 64, 16, 16, None)
+                                      1, 8, 2, 64, 16, 16, None, 0, None)
     assert rc == -4
+    # prefill: a workspace size without a workspace, or a misaligned one
+    s3p = (ctypes.c_int64 * 3)(2048, 256, 1)
+    s3k = (ctypes.c_int64 * 3)(512, 256, 1)
+    for ws, nbytes in ((None, 64), (ctypes.c_void_p(18), 64), (dummy, -1)):
+        rc = lib.wy_varlen_causal_prefill(dummy, s3p, dummy, s3k, dummy, s3k, dummy, s3p, dummy,
+                                          1, 8, 2, 256, 16, 16, ws, nbytes, None)
+        assert rc == -3
+    # no work list for an empty launch
+    assert lib.wy_varlen_causal_prefill_workspace_bytes(0, 2, 4096) == 0
+    assert lib.wy_varlen_causal_prefill_workspace_bytes(4, 2, 0) == 0
     # qwen_rmsnorm: NULL weight; d_model 384 is not a multiple of 256
     assert lib.wy_qwen_rmsnorm(dummy, s3, None, dummy, s3, 1, 1, 256, 1e-6, None) == -1
     assert lib.wy_qwen_rmsnorm(dummy, s3, dummy, dummy, s3, 1, 1, 384, 1e-6, None) == -4
