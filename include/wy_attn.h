@@ -252,12 +252,26 @@ int wy_paged_decode_block(const void *q_raw, const int64_t *q_strides, const voi
  * x [M, K], w [N, K], y [M, N] bf16, row strides x_strides[0] / w_strides[0] /
  * y_strides[0] (elements; x and w rows 16-byte aligned), inner strides 1;
  * K a multiple of 128.  M <= 64 runs a weight-streaming kernel, larger M a
- * 128 x 128-tile MFMA kernel.
+ * 128 x 128-tile MFMA kernel.  Allocates nothing; one kernel launch.
+ * workspace: NULL / 0 bytes, or at least wy_gemm_2d_workspace_bytes(M, N, K)
+ * bytes of 4-byte aligned device memory whose first 16 KiB are zero before
+ * the first call (each call leaves them zero).  With it, weight-streaming
+ * shapes with few column blocks split K across workgroups (fp32 partials
+ * summed in split order by the last workgroup of each column block);
+ * without it each column block is one workgroup.  Calls that may run
+ * concurrently need distinct workspaces.
  * Replaces wy_lib::gemm_2d (triton_kernels/gemm_2d.py:197-230, kernel :157-195).
  */
 int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w,
                const int64_t *w_strides, void *y, const int64_t *y_strides, int M, int N,
-               int K, void *stream);
+               int K, void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * Workspace bytes wy_gemm_2d uses to split K for this shape: 16 KiB of
+ * counters + split * M * N * 4 bytes of partials, or 0 when it does not
+ * split.  No counterpart in the reference (its launch takes no workspace).
+ */
+int64_t wy_gemm_2d_workspace_bytes(int M, int N, int K);
 
 #ifdef __cplusplus
 }

@@ -41,7 +41,7 @@ _SIGNATURES = {
                         _i, _vp],
     "wy_attention_gate_pack": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _i, _vp],
     "wy_qwen_rmsnorm": [_vp, _c_i64p, _vp, _vp, _c_i64p, _i, _i, _i, _f, _vp],
-    "wy_gemm_2d": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _vp],
+    "wy_gemm_2d": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _vp, _i64, _vp],
     "wy_paged_decode_block": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
                               _vp, _f, _vp, _i, _vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp,
                               _vp, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _i, _i,
@@ -72,8 +72,9 @@ def load() -> ctypes.CDLL:
     lib.wy_status_string.restype = ctypes.c_char_p
     lib.wy_build_info.argtypes = []
     lib.wy_build_info.restype = ctypes.c_char_p
-    lib.wy_varlen_causal_prefill_workspace_bytes.argtypes = [_i, _i, _i]
-    lib.wy_varlen_causal_prefill_workspace_bytes.restype = ctypes.c_int64
+    for fn in (lib.wy_varlen_causal_prefill_workspace_bytes, lib.wy_gemm_2d_workspace_bytes):
+        fn.argtypes = [_i, _i, _i]
+        fn.restype = ctypes.c_int64
     _lib = lib
     return lib
 
@@ -103,3 +104,22 @@ def call(name: str, *args) -> None:
     if rc != 0:
         msg = lib.wy_status_string(rc).decode()
         raise RuntimeError(f"{name} failed with code {rc}: {msg}")
+
+
+# Device workspaces that must start zeroed and that the kernels leave zeroed
+# (ticket / split counters), one per (device, stream, use).  Launches on one
+# stream run in order, so they can share one.  A larger request allocates a
+# new buffer; the old ones stay referenced, since a captured graph may still
+# hold their addresses.
+_WORKSPACES: dict = {}
+
+
+def stream_workspace(device, tag: str, nbytes: int) -> torch.Tensor:
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, stream(dev), tag)
+    bufs = _WORKSPACES.setdefault(key, [])
+    if not bufs or bufs[-1].numel() < nbytes:
+        size = max(nbytes, 2 * bufs[-1].numel()) if bufs else nbytes
+        bufs.append(torch.zeros(size, dtype=torch.uint8, device=dev))
+    return bufs[-1]

@@ -26,21 +26,31 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // ------------------------------------------------------------ skinny (M <= 64)
 constexpr int kSkinnyMaxM = 64;
+constexpr int kMaxSplit = 4;  // K splits across workgroups (skinny kernel)
 
 template <int kNW, int kMT, int kNT>
 __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
-    bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K) {
+    bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, float *__restrict__ part,
+    int32_t *__restrict__ cnt) {
   // kMT = ceil(M / 16) tiles of 16 rows, kNT tiles of 16 columns per
   // workgroup (each x load feeds kNT MFMAs); every load of a 4-step batch is
   // issued before the first MFMA consumes one, so a wave waits for memory once
   // per 128 columns of K rather than once per load.
+  // Split K (gridDim.y > 1): workgroup (x, y) sums K range y of gridDim.y,
+  // publishes its fp32 tile to part[y] and counts itself on cnt[x]; the
+  // workgroup that completes the count adds the tiles in split order (so the
+  // result does not depend on which one arrives last), stores bf16 and
+  // resets the counter.
   __shared__ f32x4v_t red[kNW][kMT * kNT][64];
+  __shared__ int last_ws;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n0 = blockIdx.x * 16 * kNT;
-  const int kc = K / kNW;  // a multiple of 32 (host)
-  const int kb = wave * kc;
+  const int n_split = int(gridDim.y);
+  const int ks = K / n_split;  // a multiple of 32 * kNW (host)
+  const int kc = ks / kNW;
+  const int kb = int(blockIdx.y) * ks + wave * kc;
   const int g = lane >> 4;
   const bf16_t *wp[kNT];
 #pragma unroll
@@ -98,6 +108,7 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) red[wave][mt * kNT + nt][lane] = acc[mt][nt];
   __syncthreads();
+  const int64_t part_stride = int64_t(M) * N;
   for (int e = threadIdx.x; e < M * 16 * kNT; e += 64 * kNW) {
     const int row = e / (16 * kNT), cc = e - row * (16 * kNT);
     const int nt = cc >> 4, col = cc & 15;
@@ -105,7 +116,53 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     float s = 0.f;
 #pragma unroll
     for (int wv = 0; wv < kNW; ++wv) s += red[wv][mt * kNT + nt][src][i];
-    if (n0 + cc < N) y[int64_t(row) * ys0 + n0 + cc] = bf16_t(f32_to_bf16_bits(s));
+    if (n0 + cc < N) {
+      if (n_split == 1)
+        y[int64_t(row) * ys0 + n0 + cc] = bf16_t(f32_to_bf16_bits(s));
+      else  // device-coherent: another workgroup (maybe on another XCD) reads it
+        __hip_atomic_store(part + blockIdx.y * part_stride + int64_t(row) * N + n0 + cc, s,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (n_split == 1) return;
+  // The partial stores have completed before the count (a workgroup-scope
+  // fence alone does not wait for them).
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int done = __hip_atomic_fetch_add(cnt + blockIdx.x, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    const int last = done == n_split - 1;
+    if (last) __hip_atomic_store(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_ws = last;
+  }
+  __syncthreads();
+  if (!last_ws) return;
+  // Every partial of every element this thread sums is requested before the
+  // first is added (one memory round trip); splits past n_split read split 0
+  // and weigh 0.
+  constexpr int kPer = (kSkinnyMaxM * 16 * kNT + 64 * kNW - 1) / (64 * kNW);
+  float v[kPer][kMaxSplit];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int e = threadIdx.x + u * 64 * kNW;
+    const int row = e / (16 * kNT), cc = e - row * (16 * kNT);
+    const bool ok = e < M * 16 * kNT && n0 + cc < N;
+    const float *pp = part + (ok ? int64_t(row) * N + n0 + cc : 0);
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp)
+      v[u][sp] = __hip_atomic_load(const_cast<float *>(pp + (sp < n_split ? sp : 0) * part_stride),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int e = threadIdx.x + u * 64 * kNW;
+    const int row = e / (16 * kNT), cc = e - row * (16 * kNT);
+    if (e >= M * 16 * kNT || n0 + cc >= N) continue;
+    float s = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp) s += sp < n_split ? v[u][sp] : 0.f;
+    y[int64_t(row) * ys0 + n0 + cc] = bf16_t(f32_to_bf16_bits(s));
   }
 }
 
@@ -249,34 +306,95 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
   return wyh::launch_status();
 }
 
+struct SkinnyArgs {
+  const bf16_t *x;
+  int64_t xs0;
+  const bf16_t *w;
+  int64_t ws0;
+  bf16_t *y;
+  int64_t ys0;
+  int M, N, K, split;
+  float *part;
+  int32_t *cnt;
+};
+
 template <int kNW, int kMT, int kNT>
-void launch_skinny(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
-                   int64_t ys0, int M, int N, int K, hipStream_t st) {
-  gemm_skinny_kernel<kNW, kMT, kNT><<<dim3(unsigned((N + 16 * kNT - 1) / (16 * kNT))), 64 * kNW,
-                                      0, st>>>(x, xs0, w, ws0, y, ys0, M, N, K);
+void launch_skinny(const SkinnyArgs &a, hipStream_t st) {
+  const dim3 grid(unsigned((a.N + 16 * kNT - 1) / (16 * kNT)), unsigned(a.split));
+  gemm_skinny_kernel<kNW, kMT, kNT><<<grid, 64 * kNW, 0, st>>>(
+      a.x, a.xs0, a.w, a.ws0, a.y, a.ys0, a.M, a.N, a.K, a.part, a.cnt);
 }
 
 template <int kNW, int kNT>
-void launch_skinny_m(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
-                     int64_t ys0, int M, int N, int K, hipStream_t st) {
-  switch ((M + 15) / 16) {
-    case 1: launch_skinny<kNW, 1, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
-    case 2: launch_skinny<kNW, 2, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
-    case 3: launch_skinny<kNW, 3, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
-    default: launch_skinny<kNW, 4, kNT>(x, xs0, w, ws0, y, ys0, M, N, K, st); break;
+void launch_skinny_m(const SkinnyArgs &a, hipStream_t st) {
+  switch ((a.M + 15) / 16) {
+    case 1: launch_skinny<kNW, 1, kNT>(a, st); break;
+    case 2: launch_skinny<kNW, 2, kNT>(a, st); break;
+    case 3: launch_skinny<kNW, 3, kNT>(a, st); break;
+    default: launch_skinny<kNW, 4, kNT>(a, st); break;
   }
+}
+
+#ifndef WY_GEMM_SPLIT_MAX_BLOCKS
+#define WY_GEMM_SPLIT_MAX_BLOCKS 128
+#endif
+#ifndef WY_GEMM_SPLIT_MIN_K
+#define WY_GEMM_SPLIT_MIN_K 512
+#endif
+
+// Launch shape of the skinny kernel: columns per workgroup (16 * nt), K
+// splits across workgroups, waves per workgroup.
+struct SkinnyPlan {
+  int nt, blocks, split, nw;
+};
+SkinnyPlan skinny_plan(int N, int K) {
+  SkinnyPlan p;
+  // 32 columns per workgroup when N is large (each x load then feeds two
+  // column tiles, halving the x bytes per column), else 16.
+  p.nt = N >= 4096 ? 2 : 1;
+  p.blocks = (N + 16 * p.nt - 1) / (16 * p.nt);
+  // Split K across workgroups until the grid covers the CUs once, keeping
+  // at least WY_GEMM_SPLIT_MIN_K of K per workgroup.
+  p.split = 1;
+  while (p.blocks < WY_GEMM_SPLIT_MAX_BLOCKS && p.blocks * p.split < 256 &&
+         K / (2 * p.split) >= WY_GEMM_SPLIT_MIN_K && (K / (2 * p.split)) % 128 == 0 &&
+         p.split < kMaxSplit)
+    p.split *= 2;
+  // Waves: enough workgroups x waves to keep the CUs streaming, each wave at
+  // least one 128-wide batch of k.
+  const int ks = K / p.split;
+  p.nw = 4;
+  while (p.nw < 16 && p.blocks * p.split * p.nw < 2048 && ks / (2 * p.nw) >= 128) p.nw *= 2;
+  return p;
 }
 
 }  // namespace
 
+// Split-K workspace: kSplitCounters int32 counters (one per column block;
+// zero before the first call, left zero by every call), then the fp32
+// partial tiles [split][M][N] (contents irrelevant).
+constexpr int kSplitCounters = 4096;
+constexpr int64_t kSplitPartOffset = kSplitCounters * 4;
+
+extern "C" int64_t wy_gemm_2d_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128 || M > kSkinnyMaxM) return 0;
+  const SkinnyPlan p = skinny_plan(N, K);
+  if (p.split == 1 || p.blocks > kSplitCounters) return 0;
+  return kSplitPartOffset + int64_t(p.split) * M * N * 4;
+}
+
 extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w,
                           const int64_t *w_strides, void *y, const int64_t *y_strides, int M,
-                          int N, int K, void *stream) {
+                          int N, int K, void *workspace, int64_t workspace_bytes,
+                          void *stream) {
   if (!x || !x_strides || !w || !w_strides || !y || !y_strides) return WY_E_NULL;
   if (M < 0 || N < 0 || K <= 0 || K % 128) return WY_E_SHAPE;
   if (x_strides[1] != 1 || w_strides[1] != 1 || y_strides[1] != 1 || x_strides[0] % 8 ||
       w_strides[0] % 8 || x_strides[0] < K || w_strides[0] < K || y_strides[0] < N ||
       !wyh::aligned16(x) || !wyh::aligned16(w) || (reinterpret_cast<uintptr_t>(y) & 1u))
+    return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
     return WY_E_LAYOUT;
   if (M == 0 || N == 0) return WY_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -284,23 +402,27 @@ extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w
   const bf16_t *wb = static_cast<const bf16_t *>(w);
   bf16_t *yb = static_cast<bf16_t *>(y);
   if (M <= kSkinnyMaxM) {
-    // Columns per workgroup: 32 when that still leaves >= 128 workgroups (each
-    // x load then feeds two column tiles, halving the x bytes per column),
-    // else 16.  Waves per workgroup: enough workgroups x waves to keep the CUs
-    // streaming, each wave at least one 128-wide batch of k.
-    const int nt = N >= 4096 ? 2 : 1;
-    const int blocks = (N + 16 * nt - 1) / (16 * nt);
-    int nw = 4;
-    while (nw < 16 && blocks * nw < 2048 && K / (2 * nw) >= 128) nw *= 2;
-    const int64_t xs = x_strides[0], wsd = w_strides[0], ys = y_strides[0];
-    if (nt == 1) {
-      if (nw == 4) launch_skinny_m<4, 1>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
-      else if (nw == 8) launch_skinny_m<8, 1>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
-      else launch_skinny_m<16, 1>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+    SkinnyPlan p = skinny_plan(N, K);
+    SkinnyArgs a{xb, x_strides[0], wb, w_strides[0], yb, y_strides[0], M, N, K, 1, nullptr,
+                 nullptr};
+    const int64_t need = wy_gemm_2d_workspace_bytes(M, N, K);
+    if (p.split > 1 && need > 0 && workspace_bytes >= need) {
+      a.split = p.split;
+      a.cnt = static_cast<int32_t *>(workspace);
+      a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + kSplitPartOffset);
+    } else if (p.split > 1) {  // no workspace: one workgroup per column block
+      p.split = 1;
+      p.nw = 4;
+      while (p.nw < 16 && p.blocks * p.nw < 2048 && K / (2 * p.nw) >= 128) p.nw *= 2;
+    }
+    if (p.nt == 1) {
+      if (p.nw == 4) launch_skinny_m<4, 1>(a, st);
+      else if (p.nw == 8) launch_skinny_m<8, 1>(a, st);
+      else launch_skinny_m<16, 1>(a, st);
     } else {
-      if (nw == 4) launch_skinny_m<4, 2>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
-      else if (nw == 8) launch_skinny_m<8, 2>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
-      else launch_skinny_m<16, 2>(xb, xs, wb, wsd, yb, ys, M, N, K, st);
+      if (p.nw == 4) launch_skinny_m<4, 2>(a, st);
+      else if (p.nw == 8) launch_skinny_m<8, 2>(a, st);
+      else launch_skinny_m<16, 2>(a, st);
     }
     return wyh::launch_status();
   }

@@ -30,10 +30,14 @@ def gemm_2d(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     if weight.stride(1) != 1 or weight.stride(0) % 8 or weight.data_ptr() % 16:
         weight = weight.contiguous()
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    # Decode shapes with few column blocks split K across workgroups; the
+    # split counters and fp32 partials live in a per-stream workspace.
+    ws_bytes = _lib.load().wy_gemm_2d_workspace_bytes(M, N, K)
+    ws = _lib.stream_workspace(x.device, "gemm_split", ws_bytes) if ws_bytes > 0 else None
     _lib.call(
         "wy_gemm_2d", _lib.ptr(x), _lib.i64_array(x.stride()), _lib.ptr(weight),
         _lib.i64_array(weight.stride()), _lib.ptr(out), _lib.i64_array(out.stride()),
-        M, N, K, _lib.stream(x.device),
+        M, N, K, _lib.ptr(ws), ws.numel() if ws is not None else 0, _lib.stream(x.device),
     )
     return out
 

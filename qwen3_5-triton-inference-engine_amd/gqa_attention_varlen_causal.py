@@ -45,8 +45,8 @@ def gqa_attention_varlen_causal(
     ws_bytes = _lib.load().wy_varlen_causal_prefill_workspace_bytes(
         batch, num_kv_head, max_seqlen
     )
-    ws = _queue_counters(q.device) if ws_bytes > 0 else None
-    ws_bytes = ws.numel() * 4 if ws is not None else 0
+    ws = _lib.stream_workspace(q.device, "prefill_queue", ws_bytes) if ws_bytes > 0 else None
+    ws_bytes = ws.numel() if ws is not None else 0
     _lib.call(
         "wy_varlen_causal_prefill",
         _lib.ptr(q), _lib.strides(q), _lib.ptr(k), _lib.strides(k), _lib.ptr(v),
@@ -55,22 +55,6 @@ def gqa_attention_varlen_causal(
         ws_bytes, _lib.stream(q.device),
     )
     return out
-
-
-_COUNTERS: dict[tuple[int, int], torch.Tensor] = {}
-
-
-def _queue_counters(device: torch.device) -> torch.Tensor:
-    """Zeroed int32 counters of the queue launch, one pair per (device,
-    stream): launches on one stream run in order, so they can share them."""
-    dev = torch.device(device)
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
-           _lib.stream(dev))
-    t = _COUNTERS.get(key)
-    if t is None:
-        t = torch.zeros(2, dtype=torch.int32, device=dev)
-        _COUNTERS[key] = t
-    return t
 
 
 @gqa_attention_varlen_causal.register_fake

@@ -82,11 +82,25 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
     assert rc == -2  # odd rotary_dim
     # gemm_2d: K not a multiple of 128; a transposed (non K-contiguous) weight
     s2 = (ctypes.c_int64 * 2)(256, 1)
-    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 4, 8, 200, None) == -2
-    assert lib.wy_gemm_2d(dummy, s2, None, s2, dummy, s2, 4, 8, 256, None) == -1
+    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 4, 8, 200, None, 0, None) == -2
+    assert lib.wy_gemm_2d(dummy, s2, None, s2, dummy, s2, 4, 8, 256, None, 0, None) == -1
     assert lib.wy_gemm_2d(dummy, s2, dummy, (ctypes.c_int64 * 2)(1, 256), dummy, s2, 4, 8, 256,
+                          None, 0, None) == -3
+    # a workspace size without a workspace; a misaligned workspace
+    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 4, 8, 256, None, 64, None) == -3
+    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 4, 8, 256, ctypes.c_void_p(18), 64,
                           None) == -3
-    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 0, 8, 256, None) == 0  # empty
+    assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 0, 8, 256, None, 0, None) == 0  # empty
+
+
+def test_gemm_split_workspace_sizes(pkg):
+    """Decode o_proj [1024, 2048] at B=32 splits K 4 ways: 16 KiB of counters
+    plus 4 * 32 * 1024 fp32 partials; prefill shapes and wide N do not split."""
+    lib = pkg._lib.load()
+    assert lib.wy_gemm_2d_workspace_bytes(32, 1024, 2048) == 16384 + 4 * 32 * 1024 * 4
+    assert lib.wy_gemm_2d_workspace_bytes(4096, 1024, 2048) == 0
+    assert lib.wy_gemm_2d_workspace_bytes(32, 65536, 1024) == 0
+    assert lib.wy_gemm_2d_workspace_bytes(32, 1024, 200) == 0
 
 
 def test_ops_refuse_cpu_tensors(pkg):

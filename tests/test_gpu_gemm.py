@@ -84,3 +84,45 @@ def test_gemm_2d_graph_replays(pkg, dev):
         torch.cuda.synchronize()
         assert torch.equal(ys, ref_s) and torch.equal(yl, ref_l)
         _ = (xl * 2).sum().item()
+
+
+def _gemm_no_workspace(pkg, x, w):
+    """gemm_2d through the C ABI without a workspace: no K split."""
+    lib = pkg._lib
+    y = torch.empty((x.shape[0], w.shape[0]), dtype=torch.bfloat16, device=x.device)
+    lib.call("wy_gemm_2d", lib.ptr(x), lib.i64_array(x.stride()), lib.ptr(w),
+             lib.i64_array(w.stride()), lib.ptr(y), lib.i64_array(y.stride()), x.shape[0],
+             w.shape[0], x.shape[1], None, 0, lib.stream(x.device))
+    return y
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 1024, 2048), (64, 1024, 2048), (1, 1024, 2048), (33, 16, 1024)])
+def test_gemm_2d_split_k(pkg, dev, M, N, K):
+    """Shapes that split K across workgroups: the split result and the
+    unsplit one both meet the oracle bound, repeated calls are bit-identical
+    (partials are added in split order whichever workgroup finishes last),
+    and the split counters are left at zero, also inside a graph."""
+    say(f"gemm_2d split-K M={M} N={N} K={K}")
+    lib = pkg._lib.load()
+    nbytes = lib.wy_gemm_2d_workspace_bytes(M, N, K)
+    assert nbytes > 16384, "shape must take the split path"
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    xd, wd = x.to(dev), w.to(dev)
+    y = pkg.gemm_2d(xd, wd)
+    check(y, x, w)
+    check(_gemm_no_workspace(pkg, xd, wd), x, w)
+    for _ in range(3):
+        assert torch.equal(pkg.gemm_2d(xd, wd), y)
+    ws = pkg._lib.stream_workspace(dev, "gemm_split", nbytes)
+    torch.cuda.synchronize()
+    assert not ws[:16384].any(), "split counters not reset"
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yg = pkg.gemm_2d(xd, wd)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y)
+        assert torch.equal(pkg.gemm_2d(xd, wd), y)

@@ -7,7 +7,6 @@ bit-identical; the oracle check uses the attention tolerance (max-abs 2e-2,
 mean-abs 2e-3).  The ticket counters must be left at zero by every launch.
 """
 
-import importlib
 import sys
 
 import pytest
@@ -54,8 +53,7 @@ def queue_bytes(pkg, lengths):
 
 
 def counters(pkg, dev):
-    mod = importlib.import_module(pkg.__name__ + ".gqa_attention_varlen_causal")
-    return mod._queue_counters(dev)
+    return pkg._lib.stream_workspace(dev, "prefill_queue", 8).view(torch.int32)
 
 
 @pytest.mark.parametrize("lengths", [
