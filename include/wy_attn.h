@@ -171,7 +171,7 @@ int wy_varlen_causal_prefill(const void *q, const int64_t *q_strides,
  * Workspace bytes wy_varlen_causal_prefill uses for its queue launch on the
  * current device: 8 (two int32 counters), or 0 when the grid of
  * ceil(max_seqlen / 32) * batch * num_kv_heads query blocks fits the device's
- * CUs in one round or batch + ceil(max_seqlen / 32) + 1 exceeds 4096 (then the
+ * CUs in one round or 2 batch + ceil(max_seqlen / 32) + 2 exceeds 4096 (then the
  * one-workgroup-per-block launch is used).  No counterpart in the reference
  * (its launch takes no workspace).
  */

@@ -60,7 +60,7 @@ constexpr int kLdsBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 Ki
 // Exponentials are taken against a per-row reference fixed by the first KV
 // tile; a later score may exceed it by a factor up to 2^64 (P stays finite in
 // bf16 and fp32).  Beyond that the block is recomputed exactly.
-// LDS of the queue launch's ticket -> block map: n_seq + n_qblocks + 1 ints.
+// LDS of the queue launch's ticket -> block map: 2 n_seq + n_qblocks + 2 ints.
 constexpr int kPlanLds = 4096;
 constexpr float kHeadroomScale = 18446744073709551616.0f;  // 2^64
 
@@ -149,10 +149,15 @@ void varlen_causal_prefill_kernel(
   int item = int(blockIdx.x);
   int n_items = 0;
   int *const lens = plan_lds;               // [n_seq] sequence lengths
-  int *const pre = plan_lds + n_seq;        // [n_qblocks + 1] tickets before slice s
+  int *const cu_l = plan_lds + n_seq;       // [n_seq + 1] cu_seqlens
+  int *const pre = cu_l + n_seq + 1;        // [n_qblocks + 1] tickets before slice s
   if constexpr (kList) {
     if (tid == 0) s_next_item = atomicAdd(&counters[0], 1);
-    for (int i = tid; i < n_seq; i += 256) lens[i] = cu[i + 1] - cu[i];
+    for (int i = tid; i <= n_seq; i += 256) {
+      const int c0 = cu[i];
+      cu_l[i] = c0;
+      if (i < n_seq) lens[i] = cu[i + 1] - c0;
+    }
     __syncthreads();
     // pre[s + 1] = H_kv * #{b : len_b > 32 * qb(s)}, qb(s) = n_qblocks - 1 - s;
     // then an exclusive scan: each thread sums a contiguous run of slices,
@@ -236,8 +241,8 @@ void varlen_causal_prefill_kernel(
   }
   int next_ticket = 0;
   if (kList && tid == 0) next_ticket = atomicAdd(&counters[0], 1);
-  const int start = cu[b];
-  const int n = cu[b + 1] - start;
+  const int start = kList ? cu_l[b] : cu[b];
+  const int n = kList ? lens[b] : cu[b + 1] - start;
   const int q0 = qb * kBQ;
   if (q0 >= n) return;  // direct launch only (the queue holds active blocks only)
 
@@ -584,7 +589,7 @@ extern "C" int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_k
   const int cus = device_cus();
   // A grid that fits the chip in one round gains nothing from the queue; the
   // ticket -> block map must fit its LDS.
-  if (cus <= 0 || n_wg <= cus || n_wg > INT32_MAX || batch + n_qblocks + 1 > kPlanLds) return 0;
+  if (cus <= 0 || n_wg <= cus || n_wg > INT32_MAX || 2 * int64_t(batch) + n_qblocks + 2 > kPlanLds) return 0;
   return 2 * int64_t(sizeof(int32_t));
 }
 
