@@ -365,6 +365,13 @@ def main():
         lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
         lens4 = [int(x) for x in lens4.round().tolist()]
         extra["config4_prefill_mixed"] = prefill_bench(pkg, dev, lens4, seed=4)
+    # ---- the prefill attention path after q/k norm: op sequence vs block ---------
+    if want("pblock"):
+        extra["config3_prefill_attention_path"] = prefill_path_bench(pkg, dev, [128] * 32, 3)
+        g4 = torch.Generator().manual_seed(4)
+        lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
+        extra["config4_prefill_attention_path"] = prefill_path_bench(
+            pkg, dev, [int(x) for x in lens4.round().tolist()], 4)
     # ---- config 5: B=64 x 32768 ------------------------------------------------
     if want("c5"):
         w5 = decode_workload([32768] * 64, dev, seed=5, kv_scale=0.5)
@@ -439,6 +446,39 @@ def prefill_bench(pkg, dev, lengths, seed):
             "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "attainable_TFLOP/s": round(attain, 1), "frac_of_attainable": round(tf / attain, 4),
             "total_tokens": total, "lengths": lengths if len(lengths) <= 32 else None}
+
+
+def prefill_path_bench(pkg, dev, lengths, seed):
+    """The prefill attention path of one layer after the q/k norm (engine/
+    runner.py:336-384): RoPE q/k, varlen attention, gate pack, K/V page scatter.
+    Timed as the reference's op sequence (6 launches incl. the .contiguous()
+    copies) and as the two-launch attention block; both graph-timed."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    T = sum(lengths)
+
+    def rnd(*shape):
+        return torch.randn(*shape, device=dev, generator=gen).to(torch.bfloat16)
+
+    q, k, v, gate = rnd(T, HQ, D), rnd(T, HKV, D), rnd(T, HKV * D), rnd(T, HQ * D)
+    packed = pkg.build_packed_batch(lengths, device=dev)
+    max_pages = -(-max(lengths) // 16)
+    num_pages = len(lengths) * max_pages
+    bt = torch.randperm(num_pages, device=dev, generator=gen).view(
+        len(lengths), max_pages).to(torch.int32)
+    kc = torch.zeros(num_pages, HKV, 16, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    inv = pkg.rope_inv_freq(64, 1e7, device=dev)
+    ms_seq = time_graph_events(
+        lambda: pkg.prefill_attention_packed(q, k, v, gate, inv, 64, packed, kc, vc, bt), 10)
+    ms_blk = time_graph_events(
+        lambda: pkg.prefill_attention_block(q, k, v, gate, inv, 64, packed, kc, vc, bt), 10)
+    log(f"prefill path {len(lengths)} seqs total {T}: op sequence {ms_seq*1e3:.1f} us, "
+        f"block {ms_blk*1e3:.1f} us")
+    return {"op_sequence_us": round(ms_seq * 1e3, 2), "block_us": round(ms_blk * 1e3, 2),
+            "total_tokens": T,
+            "what": "after q/k norm: RoPE q/k + varlen attention + gate pack + K/V page "
+                    "scatter; op sequence (reference order, 6 launches) vs the two-launch "
+                    "prefill attention block (bit-identical)"}
 
 
 def elementwise_bench(pkg, dev):

@@ -16,6 +16,7 @@ from .attention import (
     build_packed_batch,
     decode_attention_block,
     decode_attention_step,
+    prefill_attention_block,
     prefill_attention_packed,
 )
 from .attention_gate_pack import attention_gate_pack

@@ -29,6 +29,7 @@ from .gqa_attention_decode_paged import (
     paged_kv_fill_varlen,
 )
 from .gqa_attention_varlen_causal import gqa_attention_varlen_causal
+from .gqa_attention_varlen_causal import prefill_attention_block as _prefill_attention_block_op
 from .partial_rope import partial_rope
 
 
@@ -116,6 +117,32 @@ def prefill_attention_packed(
     if trace is not None:
         trace["rope_q"], trace["rope_k"], trace["ctx"], trace["packed"] = q4, k4, ctx, gated
     return gated
+
+
+def prefill_attention_block(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    gate: torch.Tensor,
+    inv_freq: torch.Tensor,
+    rotary_dim: int,
+    packed: PackedBatch,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_table: torch.Tensor,
+) -> torch.Tensor:
+    """``prefill_attention_packed`` in two launches (``wy_lib::prefill_attention_block``),
+    bit-identical: same arguments, same ``[T, Hq*D]`` result and page contents.
+    Rotary widths other than 64 take the op sequence."""
+    token_num, nh, d = q.shape
+    nkv = k.shape[1]
+    if rotary_dim != 64:
+        return prefill_attention_packed(q, k, v, gate, inv_freq, rotary_dim, packed, k_cache,
+                                        v_cache, block_table)
+    return _prefill_attention_block_op(
+        q, k, v.reshape(token_num, nkv, d), gate.view(token_num, nh, d), packed.position_ids,
+        inv_freq, rotary_dim, k_cache, v_cache, block_table, packed.cu_seqlens,
+        packed.max_seqlen)
 
 
 def decode_attention_step(

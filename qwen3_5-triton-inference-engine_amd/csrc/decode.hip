@@ -111,7 +111,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const bf16_t *base) 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t *>(base), 0, -1, 0x00020000);
 }
 
-__device__ __forceinline__ float sigmoidf(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
 
 // ctx = bf16(A / L), then optionally bf16(ctx * sigmoid(gate)): the same two
 // roundings as the reference's combine kernel followed by its gate pack.
@@ -122,7 +122,7 @@ __device__ __forceinline__ void store_out4(const DecodeArgs &a, int b, int hq, i
   if (a.gate) {
     const bf16_t *g = a.gate + b * a.g_b + hq * a.g_h;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = o[e] * sigmoidf(bf16_to_f32(g[(d + e) * a.g_d]));
+    for (int e = 0; e < 4; ++e) o[e] = o[e] * gate_sigmoid(bf16_to_f32(g[(d + e) * a.g_d]));
   }
   bf16_t *orow = a.out + b * a.o_b + hq * a.o_h;
   if (a.o_d == 1) {

@@ -95,7 +95,110 @@ __global__ __launch_bounds__(256) void paged_kv_fill_varlen_kernel(
   }
 }
 
+// ------------------------------------------------- varlen fill with RoPE --
+// The K/V half of the prefill attention block: the varlen fill above, with
+// each K row rotated on dims [0, R) at its token's position id before it is
+// written, to the page and to the packed roped-K buffer the attention kernel
+// reads.  The rotation is the standalone RoPE's device math (rope_sincos,
+// rope_rotate, one bf16 rounding), so the pages hold exactly what
+// partial_rope followed by paged_kv_fill_varlen writes
+// (engine/runner.py:338-340, 381-384).  One work unit is a pair of K chunks
+// (c, c + R/16) for c < R/16, a K chunk >= R/8, or a V chunk.
+__global__ __launch_bounds__(256) void prefill_kv_rope_fill_kernel(
+    bf16_t *__restrict__ kc, bf16_t *__restrict__ vc, int64_t kc_p, int64_t kc_h,
+    int64_t kc_s, int64_t vc_p, int64_t vc_h, int64_t vc_s, const bf16_t *__restrict__ k,
+    int64_t k_t, int64_t k_h, const bf16_t *__restrict__ v, int64_t v_t, int64_t v_h,
+    bf16_t *__restrict__ kr, int64_t kr_t, int64_t kr_h, const int32_t *__restrict__ bt,
+    int64_t bt_b, const int32_t *__restrict__ cu, const void *__restrict__ pos, int64_t ps_t,
+    int pos64, const float *__restrict__ inv_freq, int R, int D) {
+  const int lp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int start = cu[b];
+  const int n = cu[b + 1] - start;
+  const int t0 = lp * kPage;
+  if (t0 >= n) return;
+  const int rows = min(kPage, n - t0);
+  const int64_t phys = int64_t(bt[b * bt_b + lp]);
+  bf16_t *kdst = kc + phys * kc_p + h * kc_h;
+  bf16_t *vdst = vc + phys * vc_p + h * vc_h;
+  const int64_t tok0 = int64_t(start) + t0;
+  const bf16_t *ksrc = k + h * k_h + tok0 * k_t;
+  const bf16_t *vsrc = v + h * v_h + tok0 * v_t;
+  bf16_t *krow0 = kr + h * kr_h + tok0 * kr_t;
+  const int cpr = D / 8, hr = R / 16;  // chunks per row; rotated chunk pairs per row
+  const int ku = cpr - hr;             // K work units per row
+  const int total_k = rows * ku, total = total_k + rows * cpr;
+  for (int i = threadIdx.x; i < total; i += 256) {
+    if (i < total_k) {
+      const int r = i / ku, ci = i - r * ku;
+      const bf16_t *src = ksrc + r * k_t;
+      bf16_t *dst = kdst + r * kc_s;
+      bf16_t *kdup = krow0 + r * kr_t;
+      if (ci < hr) {
+        const u32x4_t a = ld16(src + ci * 8), bb = ld16(src + R / 2 + ci * 8);
+        const float p = load_pos(pos, (tok0 + r) * ps_t, pos64 != 0);
+        u32x4_t oa, ob;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float s0, c0, s1, c1, o1l, o2l, o1h, o2h;
+          rope_sincos(p, inv_freq[ci * 8 + 2 * w], s0, c0);
+          rope_sincos(p, inv_freq[ci * 8 + 2 * w + 1], s1, c1);
+          rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), c0, s0, o1l, o2l);
+          rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), c1, s1, o1h, o2h);
+          oa[w] = pack_bf16x2(o1l, o1h);
+          ob[w] = pack_bf16x2(o2l, o2h);
+        }
+        st16(dst + ci * 8, oa);
+        st16(dst + R / 2 + ci * 8, ob);
+        st16(kdup + ci * 8, oa);
+        st16(kdup + R / 2 + ci * 8, ob);
+      } else {
+        const int c = (ci + hr) * 8;
+        const u32x4_t x = ld16(src + c);
+        st16(dst + c, x);
+        st16(kdup + c, x);
+      }
+    } else {
+      const int j = i - total_k;
+      const int r = j / cpr, c = (j - r * cpr) * 8;
+      st16(vdst + r * vc_s + c, ld16(vsrc + r * v_t + c));
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int wy_prefill_kv_rope_fill(void *k_cache, void *v_cache, const int64_t *kcs,
+                                       const int64_t *vcs, const void *k, const int64_t *ks,
+                                       const void *v, const int64_t *vs, void *k_roped,
+                                       const int64_t *krs, const int32_t *block_table,
+                                       int64_t bt_stride0, const int32_t *cu_seqlens,
+                                       const void *position_ids, int64_t pos_stride,
+                                       int pos_is_int64, const float *inv_freq, int rotary_dim,
+                                       int batch, int num_kv_heads, int head_dim,
+                                       int max_seqlen, void *stream) {
+  if (!k_cache || !v_cache || !kcs || !vcs || !k || !ks || !v || !vs || !k_roped || !krs ||
+      !block_table || !cu_seqlens || !position_ids || !inv_freq)
+    return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen < 0) return WY_E_SHAPE;
+  if (head_dim % 8 || rotary_dim <= 0 || rotary_dim % 16 || rotary_dim > head_dim)
+    return WY_E_SHAPE;
+  const bool vec = kcs[3] == 1 && vcs[3] == 1 && ks[2] == 1 && vs[2] == 1 && krs[2] == 1 &&
+                   kcs[0] % 8 == 0 && kcs[1] % 8 == 0 && kcs[2] % 8 == 0 && vcs[0] % 8 == 0 &&
+                   vcs[1] % 8 == 0 && vcs[2] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 &&
+                   vs[0] % 8 == 0 && vs[1] % 8 == 0 && krs[0] % 8 == 0 && krs[1] % 8 == 0 &&
+                   wyh::aligned16(k_cache) && wyh::aligned16(v_cache) && wyh::aligned16(k) &&
+                   wyh::aligned16(v) && wyh::aligned16(k_roped);
+  if (!vec) return WY_E_LAYOUT;
+  if (batch == 0 || max_seqlen == 0) return WY_OK;
+  dim3 grid((max_seqlen + kPage - 1) / kPage, num_kv_heads, batch);
+  prefill_kv_rope_fill_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<bf16_t *>(k_cache), static_cast<bf16_t *>(v_cache), kcs[0], kcs[1], kcs[2],
+      vcs[0], vcs[1], vcs[2], static_cast<const bf16_t *>(k), ks[0], ks[1],
+      static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(k_roped), krs[0],
+      krs[1], block_table, bt_stride0, cu_seqlens, position_ids, pos_stride, pos_is_int64,
+      inv_freq, rotary_dim, head_dim);
+  return wyh::launch_status();
+}
 
 extern "C" int wy_paged_kv_append(void *k_cache, void *v_cache, const int64_t *kcs,
                                   const int64_t *vcs, const void *k_new,

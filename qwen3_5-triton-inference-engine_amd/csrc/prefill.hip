@@ -108,7 +108,19 @@ __device__ __forceinline__ int k_row_token(int row) {
 
 
 // ------------------------------------------------------------------ attention
-template <bool kList>
+// Attention-block extras (kRot > 0): the raw q rows get the partial RoPE on
+// dims [0, kRot) at their position ids, and the output is multiplied by
+// sigmoid(gate) in the epilogue.
+struct BlockArgs {
+  const bf16_t *gate;  // [T, H_q, D] view, unit innermost stride
+  int64_t gs_t, gs_h;
+  const void *pos;     // position ids [T], int32 or int64
+  int64_t ps_t;
+  int pos64;
+  const float *inv_freq;
+};
+
+template <bool kList, int kRot>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h,
@@ -116,7 +128,7 @@ void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t *__restrict__ out,
     int64_t os_t,
     int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
-    int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters) {
+    int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters, const BlockArgs blk) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_next_item;
   __shared__ int s_scan[256];
@@ -335,6 +347,30 @@ void varlen_causal_prefill_kernel(
 #pragma unroll
     for (int kk = 0; kk < 16; ++kk) xr[kk] = ld16(qp + 16 * kk);
     issue_first();
+    if constexpr (kRot > 0) {
+      // Partial RoPE of the raw row, the standalone kernel's device math and
+      // bf16 rounding (partial_rope.py:74-98): k-step kk < kRot/32 holds dims
+      // 16kk + 8g .. +7 of the first half, k-step kk + kRot/32 their partners.
+      static_assert(kRot % 32 == 0 && kRot <= kD, "rotary dims in whole k-step pairs");
+      constexpr int kH = kRot / 32;
+      const float p = load_pos(blk.pos, (int64_t(start) + qc) * blk.ps_t, blk.pos64 != 0);
+#pragma unroll
+      for (int kk = 0; kk < kH; ++kk) {
+        u32x4_t a = xr[kk], bb = xr[kk + kH];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float s0, c0, s1, c1, o1l, o2l, o1h, o2h;
+          rope_sincos(p, blk.inv_freq[16 * kk + 8 * g + 2 * w], s0, c0);
+          rope_sincos(p, blk.inv_freq[16 * kk + 8 * g + 2 * w + 1], s1, c1);
+          rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), c0, s0, o1l, o2l);
+          rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), c1, s1, o1h, o2h);
+          a[w] = pack_bf16x2(o1l, o1h);
+          bb[w] = pack_bf16x2(o2l, o2h);
+        }
+        xr[kk] = a;
+        xr[kk + kH] = bb;
+      }
+    }
 #pragma unroll
     for (int kk = 0; kk < 16; ++kk) {
       u32x4_t x = xr[kk];
@@ -539,12 +575,23 @@ void varlen_causal_prefill_kernel(
   const float inv_l = 1.0f / l;
   if (qrow < n) {
     bf16_t *op = out + (int64_t(start) + qrow) * os_t + hq * os_h;
+    const bf16_t *gp = nullptr;
+    if constexpr (kRot > 0) gp = blk.gate + (int64_t(start) + qrow) * blk.gs_t + hq * blk.gs_h;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
-                           pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
+        u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
+                     pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
+        if constexpr (kRot > 0) {
+          // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
+          // gate pack computes it
+          const u32x2_t gv = *reinterpret_cast<const u32x2_t *>(gp + dt * 32 + 8 * j + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            w[e] = pack_bf16x2(bf16_lo(w[e]) * gate_sigmoid(bf16_lo(gv[e])),
+                               bf16_hi(w[e]) * gate_sigmoid(bf16_hi(gv[e])));
+        }
         *reinterpret_cast<u32x2_t *>(op + dt * 32 + 8 * j + 4 * g) = w;
       }
   }
@@ -595,38 +642,39 @@ extern "C" int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_k
   return 2 * int64_t(sizeof(int32_t));
 }
 
-extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const void *k,
-                                        const int64_t *ks, const void *v,
-                                        const int64_t *vs, void *out, const int64_t *os,
-                                        const int32_t *cu_seqlens, int batch,
-                                        int num_q_heads, int num_kv_heads, int head_dim,
-                                        int max_seqlen, int64_t total_tokens, void *workspace,
-                                        int64_t workspace_bytes, void *stream) {
-  if (!q || !qs || !k || !ks || !v || !vs || !out || !os || !cu_seqlens) return WY_E_NULL;
-  if (batch < 0 || num_kv_heads <= 0 || max_seqlen < 0 || total_tokens < 0)
-    return WY_E_SHAPE;
-  if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
-  if (qs[2] != 1 || ks[2] != 1 || vs[2] != 1 || os[2] != 1 || qs[0] % 8 || qs[1] % 8 ||
-      ks[0] % 8 || ks[1] % 8 || vs[0] % 8 || vs[1] % 8 || os[0] % 4 || os[1] % 4 ||
-      !wyh::aligned16(q) || !wyh::aligned16(k) || !wyh::aligned16(v) ||
-      (reinterpret_cast<uintptr_t>(out) & 7u))
-    return WY_E_LAYOUT;
-  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
-      (reinterpret_cast<uintptr_t>(workspace) & 3u))
-    return WY_E_LAYOUT;
-  if (batch == 0 || max_seqlen == 0) return WY_OK;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<false>),
+namespace {
+
+template <bool kList, int kRot>
+int set_prefill_lds() {
+  static bool done = false;
+  if (!done) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<kList, kRot>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return int(e);
-    attr_set = true;
+    done = true;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return WY_OK;
+}
+
+bool prefill_layout_ok(const void *q, const int64_t *qs, const void *k, const int64_t *ks,
+                       const void *v, const int64_t *vs, const void *out, const int64_t *os) {
+  return !(qs[2] != 1 || ks[2] != 1 || vs[2] != 1 || os[2] != 1 || qs[0] % 8 || qs[1] % 8 ||
+           ks[0] % 8 || ks[1] % 8 || vs[0] % 8 || vs[1] % 8 || os[0] % 4 || os[1] % 4 ||
+           !wyh::aligned16(q) || !wyh::aligned16(k) || !wyh::aligned16(v) ||
+           (reinterpret_cast<uintptr_t>(out) & 7u));
+}
+
+// Validated arguments -> one launch (direct or queue).
+template <int kRot>
+int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_t *ks,
+                   const void *v, const int64_t *vs, void *out, const int64_t *os,
+                   const int32_t *cu_seqlens, int batch, int num_kv_heads, int head_dim,
+                   int max_seqlen, void *workspace, int64_t workspace_bytes,
+                   const BlockArgs &blk, hipStream_t s) {
+  int rc = set_prefill_lds<false, kRot>();
+  if (rc == WY_OK) rc = set_prefill_lds<true, kRot>();
+  if (rc != WY_OK) return rc;
   const int n_qblocks = (max_seqlen + kBQ - 1) / kBQ;
   const int64_t n_wg = prefill_blocks(batch, num_kv_heads, max_seqlen);
   if (n_wg > INT32_MAX) return WY_E_SHAPE;
@@ -643,11 +691,75 @@ extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const 
     counters = static_cast<int32_t *>(workspace);
     grid = unsigned(device_cus());
   }
-  auto *kern = counters ? varlen_causal_prefill_kernel<true> : varlen_causal_prefill_kernel<false>;
+  auto *kern = counters ? varlen_causal_prefill_kernel<true, kRot>
+                        : varlen_causal_prefill_kernel<false, kRot>;
   kern<<<dim3(grid), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
       ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],
-      os[1], cu_seqlens,
-      kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks, counters);
+      os[1], cu_seqlens, kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks,
+      counters, blk);
   return wyh::launch_status();
+}
+
+}  // namespace
+
+extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const void *k,
+                                        const int64_t *ks, const void *v,
+                                        const int64_t *vs, void *out, const int64_t *os,
+                                        const int32_t *cu_seqlens, int batch,
+                                        int num_q_heads, int num_kv_heads, int head_dim,
+                                        int max_seqlen, int64_t total_tokens, void *workspace,
+                                        int64_t workspace_bytes, void *stream) {
+  if (!q || !qs || !k || !ks || !v || !vs || !out || !os || !cu_seqlens) return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || max_seqlen < 0 || total_tokens < 0)
+    return WY_E_SHAPE;
+  if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
+  if (!prefill_layout_ok(q, qs, k, ks, v, vs, out, os)) return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return WY_E_LAYOUT;
+  if (batch == 0 || max_seqlen == 0) return WY_OK;
+  return launch_prefill<0>(q, qs, k, ks, v, vs, out, os, cu_seqlens, batch, num_kv_heads,
+                           head_dim, max_seqlen, workspace, workspace_bytes, BlockArgs{},
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int wy_prefill_attention_block(
+    const void *q, const int64_t *qs, const void *k, const int64_t *ks, const void *v,
+    const int64_t *vs, const void *gate, const int64_t *gs, const void *position_ids,
+    int64_t pos_stride, int pos_is_int64, const float *inv_freq, int rotary_dim,
+    void *k_cache, void *v_cache, const int64_t *kcs, const int64_t *vcs,
+    const int32_t *block_table, int64_t bt_stride0, const int32_t *cu_seqlens, int batch,
+    int num_q_heads, int num_kv_heads, int head_dim, int max_seqlen, int64_t total_tokens,
+    void *k_roped, void *out, void *workspace, int64_t workspace_bytes, void *stream) {
+  if (!q || !qs || !k || !ks || !v || !vs || !gate || !gs || !position_ids || !inv_freq ||
+      !k_cache || !v_cache || !kcs || !vcs || !block_table || !cu_seqlens || !k_roped || !out)
+    return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0 || max_seqlen < 0 || total_tokens < 0)
+    return WY_E_SHAPE;
+  if (head_dim != kD || num_q_heads != kG * num_kv_heads || rotary_dim != 64)
+    return WY_E_UNSUPPORTED;
+  // k_roped and out are the block's own contiguous buffers: [T, H_kv, D] and
+  // [T, H_q * D]
+  const int64_t krs[3] = {int64_t(num_kv_heads) * head_dim, head_dim, 1};
+  const int64_t os[3] = {int64_t(num_q_heads) * head_dim, head_dim, 1};
+  if (!prefill_layout_ok(q, qs, k_roped, krs, v, vs, out, os) || ks[2] != 1 || gs[2] != 1 ||
+      gs[0] % 4 || gs[1] % 4 || (reinterpret_cast<uintptr_t>(gate) & 7u))
+    return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return WY_E_LAYOUT;
+  if (batch == 0 || max_seqlen == 0) return WY_OK;
+  // 1. RoPE of K, K/V into the pages, roped K packed for the attention
+  int rc = wy_prefill_kv_rope_fill(k_cache, v_cache, kcs, vcs, k, ks, v, vs, k_roped, krs,
+                                   block_table, bt_stride0, cu_seqlens, position_ids,
+                                   pos_stride, pos_is_int64, inv_freq, rotary_dim, batch,
+                                   num_kv_heads, head_dim, max_seqlen, stream);
+  if (rc != WY_OK) return rc;
+  // 2. attention with q's RoPE at load and the gate in the epilogue
+  const BlockArgs blk{static_cast<const bf16_t *>(gate), gs[0], gs[1], position_ids,
+                      pos_stride, pos_is_int64, inv_freq};
+  return launch_prefill<64>(q, qs, k_roped, krs, v, vs, out, os, cu_seqlens, batch,
+                            num_kv_heads, head_dim, max_seqlen, workspace, workspace_bytes,
+                            blk, static_cast<hipStream_t>(stream));
 }

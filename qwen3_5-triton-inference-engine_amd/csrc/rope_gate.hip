@@ -8,10 +8,6 @@ using namespace wy;
 
 namespace {
 
-__device__ __forceinline__ float load_pos(const void *pos, int64_t off, bool is64) {
-  return is64 ? float(static_cast<const int64_t *>(pos)[off])
-              : float(static_cast<const int32_t *>(pos)[off]);
-}
 
 // ------------------------------------------------------------ partial RoPE --
 // Fast path.  The grid's first part rotates: a lane owns chunk c (8 dims) of
@@ -145,8 +141,8 @@ __global__ __launch_bounds__(256) void gate_pack_vec_kernel(
   u32x4_t o;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const float sl = 1.0f / (1.0f + __expf(-bf16_lo(gv[w])));
-    const float sh = 1.0f / (1.0f + __expf(-bf16_hi(gv[w])));
+    const float sl = gate_sigmoid(bf16_lo(gv[w]));
+    const float sh = gate_sigmoid(bf16_hi(gv[w]));
     o[w] = pack_bf16x2(bf16_lo(xv[w]) * sl, bf16_hi(xv[w]) * sh);
   }
   st16(out + gid * 8, o);
@@ -163,7 +159,7 @@ __global__ __launch_bounds__(256) void gate_pack_generic_kernel(
   const int h = r / D, d = r - h * D;
   const float xv = bf16_to_f32(x[h * xs_h + t * xs_t + d * xs_d]);
   const float gv = bf16_to_f32(g[h * gs_h + t * gs_t + d * gs_d]);
-  out[gid] = bf16_t(f32_to_bf16_bits(xv * (1.0f / (1.0f + __expf(-gv)))));
+  out[gid] = bf16_t(f32_to_bf16_bits(xv * gate_sigmoid(gv)));
 }
 
 inline unsigned blocks_for(int64_t n) { return unsigned((n + 255) / 256); }

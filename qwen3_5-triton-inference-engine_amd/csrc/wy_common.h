@@ -78,6 +78,14 @@ __device__ __forceinline__ void rope_sincos(float pos, float inv_freq_j, float &
   sincosf(__fmul_rn(pos, inv_freq_j), &s, &c);
 }
 
+// Position id as float (int32 or int64 tensor).
+__device__ __forceinline__ float load_pos(const void *pos, int64_t off, bool is64) {
+  return is64 ? float(static_cast<const int64_t *>(pos)[off])
+              : float(static_cast<const int32_t *>(pos)[off]);
+}
+// sigmoid(g) in fp32 as the gate pack computes it (attention_gate_pack.py:56).
+__device__ __forceinline__ float gate_sigmoid(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
 // RMSNorm of one row held by a group of 32 consecutive lanes, lane l holding
 // 8 consecutive elements of each 256-element block k (elements 8(32k+l) ..).
 // The sum of squares runs over the lane's elements in order, then an xor

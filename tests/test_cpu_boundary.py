@@ -59,6 +59,14 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
         rc = lib.wy_varlen_causal_prefill(dummy, s3p, dummy, s3k, dummy, s3k, dummy, s3p, dummy,
                                           1, 8, 2, 256, 16, 16, ws, nbytes, None)
         assert rc == -3
+    # prefill block: rotary widths other than 64 are unsupported; NULL gate
+    pos = ctypes.c_void_p(64)
+    args = [dummy, s3p, dummy, s3k, dummy, s3k, dummy, s3p, pos, 1, 0, dummy]
+    tail = [dummy, dummy, s4, s4, dummy, 4, dummy, 1, 8, 2, 256, 16, 16, dummy, dummy, None, 0,
+            None]
+    assert lib.wy_prefill_attention_block(*args, 32, *tail) == -4
+    args[6] = None
+    assert lib.wy_prefill_attention_block(*args, 64, *tail) == -1
     # no work list for an empty launch
     assert lib.wy_varlen_causal_prefill_workspace_bytes(0, 2, 4096) == 0
     assert lib.wy_varlen_causal_prefill_workspace_bytes(4, 2, 0) == 0
@@ -131,7 +139,8 @@ def test_op_schemas_match_reference():
         args = s[len(f"wy_lib::{name}"):]
         assert args.replace("SymInt", "int") == sig.replace("SymInt", "int"), s
     for name in ("paged_kv_fill_varlen", "paged_gqa_attention_decode_split",
-                 "paged_gqa_attention_decode_combine", "partial_rope"):
+                 "paged_gqa_attention_decode_combine", "partial_rope",
+                 "prefill_attention_block"):
         assert hasattr(torch.ops.wy_lib, name)
 
 
@@ -149,6 +158,15 @@ def test_fake_impls_give_reference_shapes(pkg):
         xg = torch.empty(7, 1024, dtype=torch.bfloat16, device="cuda")
         wg = torch.empty(5120, 1024, dtype=torch.bfloat16, device="cuda")
         assert torch.ops.wy_lib.gemm_2d(xg, wg).shape == (7, 5120)
+        qb = torch.empty(9, 8, 256, dtype=torch.bfloat16, device="cuda")
+        kb = torch.empty(9, 2, 256, dtype=torch.bfloat16, device="cuda")
+        cache = torch.empty(4, 2, 16, 256, dtype=torch.bfloat16, device="cuda")
+        out = torch.ops.wy_lib.prefill_attention_block(
+            qb, kb, kb, qb, torch.empty(1, 9, dtype=torch.int32, device="cuda"),
+            torch.empty(32, device="cuda"), 64, cache, cache,
+            torch.empty(1, 4, dtype=torch.int32, device="cuda"),
+            torch.empty(2, dtype=torch.int32, device="cuda"), 9)
+        assert out.shape == (9, 2048) and out.dtype == torch.bfloat16
 
 
 def test_gemm_2d_asserts_reference_preconditions(pkg):
