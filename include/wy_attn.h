@@ -190,9 +190,11 @@ int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_kv_heads, in
  * rows), position_ids [T] (element stride pos_stride; int32, or int64 with
  * pos_is_int64 = 1), inv_freq [rotary_dim / 2] fp32, rotary_dim 64.
  * Launch 1 rotates K, writes K and V into the pages (block_table /
- * cu_seqlens as in wy_paged_kv_fill_varlen) and the roped K into k_roped
- * ([T, H_kv, D] contiguous, caller-owned scratch).  Launch 2 is the varlen
- * causal attention with q's RoPE applied at load and out [T, H_q * D]
+ * cu_seqlens as in wy_paged_kv_fill_varlen), the roped K into k_roped
+ * ([T, H_kv, D] contiguous) and each token's sin / cos into rope_table
+ * ([T][rotary_dim] fp32: sin of the rotary_dim/2 angles, then cos; 16-byte
+ * aligned); both are caller-owned scratch.  Launch 2 is the varlen causal
+ * attention with q's RoPE (from that table) applied at load and out [T, H_q * D]
  * (contiguous) = bf16(bf16(attention) * sigmoid(gate)).  workspace as in
  * wy_varlen_causal_prefill.  Allocates nothing.
  */
@@ -206,21 +208,24 @@ int wy_prefill_attention_block(const void *q, const int64_t *q_strides, const vo
                                const int32_t *block_table, int64_t bt_stride0,
                                const int32_t *cu_seqlens, int batch, int num_q_heads,
                                int num_kv_heads, int head_dim, int max_seqlen,
-                               int64_t total_tokens, void *k_roped, void *out,
-                               void *workspace, int64_t workspace_bytes, void *stream);
+                               int64_t total_tokens, void *k_roped, float *rope_table,
+                               void *out, void *workspace, int64_t workspace_bytes,
+                               void *stream);
 
 /*
  * Launch 1 of wy_prefill_attention_block on its own: the varlen K/V page fill
- * with K rotated (partial RoPE on dims [0, rotary_dim), rotary_dim % 16 == 0)
+ * with K rotated (partial RoPE on dims [0, rotary_dim), rotary_dim % 16 == 0, at most 128)
  * before it is written, to the pages and to k_roped ([T, H_kv, D], strides
- * kr_strides).  Equals partial_rope(k) followed by paged_kv_fill_varlen
+ * kr_strides); rope_table (optional, NULL to skip) receives each token's
+ * sin / cos as in wy_prefill_attention_block.  Equals partial_rope(k) followed by paged_kv_fill_varlen
  * (triton_kernels/partial_rope.py:145-198, gqa_attention_decode_paged.py:492-561).
  * Unit inner strides and 16-byte aligned rows everywhere (else WY_E_LAYOUT).
  */
 int wy_prefill_kv_rope_fill(void *k_cache, void *v_cache, const int64_t *kc_strides,
                             const int64_t *vc_strides, const void *k, const int64_t *k_strides,
                             const void *v, const int64_t *v_strides, void *k_roped,
-                            const int64_t *kr_strides, const int32_t *block_table,
+                            const int64_t *kr_strides, float *rope_table,
+                            const int32_t *block_table,
                             int64_t bt_stride0, const int32_t *cu_seqlens,
                             const void *position_ids, int64_t pos_stride, int pos_is_int64,
                             const float *inv_freq, int rotary_dim, int batch, int num_kv_heads,

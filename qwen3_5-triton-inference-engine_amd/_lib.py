@@ -43,11 +43,11 @@ _SIGNATURES = {
     "wy_qwen_rmsnorm": [_vp, _c_i64p, _vp, _vp, _c_i64p, _i, _i, _i, _f, _vp],
     "wy_prefill_attention_block": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
                                    _vp, _i64, _i, _vp, _i, _vp, _vp, _c_i64p, _c_i64p, _vp,
-                                   _i64, _vp, _i, _i, _i, _i, _i, _i64, _vp, _vp, _vp, _i64,
-                                   _vp],
+                                   _i64, _vp, _i, _i, _i, _i, _i, _i64, _vp, _vp, _vp, _vp,
+                                   _i64, _vp],
     "wy_prefill_kv_rope_fill": [_vp, _vp, _c_i64p, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
-                                _c_i64p, _vp, _i64, _vp, _vp, _i64, _i, _vp, _i, _i, _i, _i,
-                                _i, _vp],
+                                _c_i64p, _vp, _vp, _i64, _vp, _vp, _i64, _i, _vp, _i, _i, _i,
+                                _i, _i, _vp],
     "wy_gemm_2d": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _vp, _i64, _vp],
     "wy_paged_decode_block": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
                               _vp, _f, _vp, _i, _vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp,

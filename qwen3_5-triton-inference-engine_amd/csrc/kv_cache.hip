@@ -102,65 +102,109 @@ __global__ __launch_bounds__(256) void paged_kv_fill_varlen_kernel(
 // reads.  The rotation is the standalone RoPE's device math (rope_sincos,
 // rope_rotate, one bf16 rounding), so the pages hold exactly what
 // partial_rope followed by paged_kv_fill_varlen writes
-// (engine/runner.py:338-340, 381-384).  One work unit is a pair of K chunks
-// (c, c + R/16) for c < R/16, a K chunk >= R/8, or a V chunk.
+// (engine/runner.py:338-340, 381-384).  One workgroup per (logical page, KV
+// head, sequence), as the plain fill; the page's sin/cos go to LDS and, from
+// the head-0 workgroup, to tab[t] = [sin of the R/2 angles | cos] for the
+// attention kernel's q rotation.  Work units: a rotated chunk pair
+// (c, c + R/16) of one row, an unrotated K chunk, a V chunk.  Each thread
+// requests all of its units' chunks before it computes or stores any
+// (kRopeFillUnits per pass), so a pass costs one memory round trip.
+constexpr int kRopeFillUnits = 4;
+constexpr int kRopeFillMaxR = 128;
+
 __global__ __launch_bounds__(256) void prefill_kv_rope_fill_kernel(
     bf16_t *__restrict__ kc, bf16_t *__restrict__ vc, int64_t kc_p, int64_t kc_h,
     int64_t kc_s, int64_t vc_p, int64_t vc_h, int64_t vc_s, const bf16_t *__restrict__ k,
     int64_t k_t, int64_t k_h, const bf16_t *__restrict__ v, int64_t v_t, int64_t v_h,
-    bf16_t *__restrict__ kr, int64_t kr_t, int64_t kr_h, const int32_t *__restrict__ bt,
-    int64_t bt_b, const int32_t *__restrict__ cu, const void *__restrict__ pos, int64_t ps_t,
-    int pos64, const float *__restrict__ inv_freq, int R, int D) {
-  const int lp = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    bf16_t *__restrict__ kr, int64_t kr_t, int64_t kr_h, float *__restrict__ tab,
+    const int32_t *__restrict__ bt, int64_t bt_b, const int32_t *__restrict__ cu,
+    const void *__restrict__ pos, int64_t ps_t, int pos64, const float *__restrict__ inv_freq,
+    int R, int D, int H) {
+  __shared__ float sn_l[kPage][kRopeFillMaxR / 2], cs_l[kPage][kRopeFillMaxR / 2];
+  const int lp = blockIdx.x, h0 = blockIdx.y, b = blockIdx.z;
   const int start = cu[b];
   const int n = cu[b + 1] - start;
   const int t0 = lp * kPage;
   if (t0 >= n) return;
   const int rows = min(kPage, n - t0);
   const int64_t phys = int64_t(bt[b * bt_b + lp]);
-  bf16_t *kdst = kc + phys * kc_p + h * kc_h;
-  bf16_t *vdst = vc + phys * vc_p + h * vc_h;
   const int64_t tok0 = int64_t(start) + t0;
-  const bf16_t *ksrc = k + h * k_h + tok0 * k_t;
-  const bf16_t *vsrc = v + h * v_h + tok0 * v_t;
-  bf16_t *krow0 = kr + h * kr_h + tok0 * kr_t;
-  const int cpr = D / 8, hr = R / 16;  // chunks per row; rotated chunk pairs per row
-  const int ku = cpr - hr;             // K work units per row
-  const int total_k = rows * ku, total = total_k + rows * cpr;
-  for (int i = threadIdx.x; i < total; i += 256) {
-    if (i < total_k) {
-      const int r = i / ku, ci = i - r * ku;
-      const bf16_t *src = ksrc + r * k_t;
-      bf16_t *dst = kdst + r * kc_s;
-      bf16_t *kdup = krow0 + r * kr_t;
-      if (ci < hr) {
-        const u32x4_t a = ld16(src + ci * 8), bb = ld16(src + R / 2 + ci * 8);
-        const float p = load_pos(pos, (tok0 + r) * ps_t, pos64 != 0);
+  const int cpr = D / 8, hr = R / 16;   // chunks per row; rotated chunk pairs per row
+  const int kcopy = cpr - 2 * hr;       // unrotated K chunks per (row, head)
+  const int n_rot = rows * hr, n_kcopy = rows * kcopy;
+  const int total = n_rot + n_kcopy + rows * cpr;
+  const int h = h0;
+  const int half = R / 2;
+  for (int base = 0; base < total; base += 256 * kRopeFillUnits) {
+    // 1. request every chunk of this pass
+    u32x4_t x0[kRopeFillUnits], x1[kRopeFillUnits];
+#pragma unroll
+    for (int u = 0; u < kRopeFillUnits; ++u) {
+      const int i = base + u * 256 + int(threadIdx.x);
+      x0[u] = x1[u] = u32x4_t{0u, 0u, 0u, 0u};
+      if (i < n_rot) {
+        const int r = i / hr, c = i - r * hr;
+        const bf16_t *src = k + h * k_h + (tok0 + r) * k_t + c * 8;
+        x0[u] = ld16(src);
+        x1[u] = ld16(src + half);
+      } else if (i < n_rot + n_kcopy) {
+        const int j = i - n_rot;
+        const int r = j / kcopy, c = 2 * hr + (j - r * kcopy);
+        x0[u] = ld16(k + h * k_h + (tok0 + r) * k_t + c * 8);
+      } else if (i < total) {
+        const int j = i - n_rot - n_kcopy;
+        const int r = j / cpr, c = j - r * cpr;
+        x0[u] = ld16(v + h * v_h + (tok0 + r) * v_t + c * 8);
+      }
+    }
+    // 2. the page's sin / cos (first pass only; overlaps the loads)
+    if (base == 0) {
+      for (int e = threadIdx.x; e < rows * half; e += 256) {
+        const int r = e / half, jj = e - r * half;
+        float sv, cv;
+        rope_sincos(load_pos(pos, (tok0 + r) * ps_t, pos64 != 0), inv_freq[jj], sv, cv);
+        sn_l[r][jj] = sv;
+        cs_l[r][jj] = cv;
+        if (tab && h == 0) {
+          tab[(tok0 + r) * R + jj] = sv;
+          tab[(tok0 + r) * R + half + jj] = cv;
+        }
+      }
+      __syncthreads();
+    }
+    // 3. rotate / store
+#pragma unroll
+    for (int u = 0; u < kRopeFillUnits; ++u) {
+      const int i = base + u * 256 + int(threadIdx.x);
+      if (i < n_rot) {
+        const int r = i / hr, c = i - r * hr;
         u32x4_t oa, ob;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          float s0, c0, s1, c1, o1l, o2l, o1h, o2h;
-          rope_sincos(p, inv_freq[ci * 8 + 2 * w], s0, c0);
-          rope_sincos(p, inv_freq[ci * 8 + 2 * w + 1], s1, c1);
-          rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), c0, s0, o1l, o2l);
-          rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), c1, s1, o1h, o2h);
+          const int j0 = c * 8 + 2 * w;
+          float o1l, o2l, o1h, o2h;
+          rope_rotate(bf16_lo(x0[u][w]), bf16_lo(x1[u][w]), cs_l[r][j0], sn_l[r][j0], o1l, o2l);
+          rope_rotate(bf16_hi(x0[u][w]), bf16_hi(x1[u][w]), cs_l[r][j0 + 1], sn_l[r][j0 + 1],
+                      o1h, o2h);
           oa[w] = pack_bf16x2(o1l, o1h);
           ob[w] = pack_bf16x2(o2l, o2h);
         }
-        st16(dst + ci * 8, oa);
-        st16(dst + R / 2 + ci * 8, ob);
-        st16(kdup + ci * 8, oa);
-        st16(kdup + R / 2 + ci * 8, ob);
-      } else {
-        const int c = (ci + hr) * 8;
-        const u32x4_t x = ld16(src + c);
-        st16(dst + c, x);
-        st16(kdup + c, x);
+        bf16_t *dst = kc + phys * kc_p + h * kc_h + r * kc_s + c * 8;
+        bf16_t *kdup = kr + h * kr_h + (tok0 + r) * kr_t + c * 8;
+        st16(dst, oa);
+        st16(dst + half, ob);
+        st16(kdup, oa);
+        st16(kdup + half, ob);
+      } else if (i < n_rot + n_kcopy) {
+        const int j = i - n_rot;
+        const int r = j / kcopy, c = 2 * hr + (j - r * kcopy);
+        st16(kc + phys * kc_p + h * kc_h + r * kc_s + c * 8, x0[u]);
+        st16(kr + h * kr_h + (tok0 + r) * kr_t + c * 8, x0[u]);
+      } else if (i < total) {
+        const int j = i - n_rot - n_kcopy;
+        const int r = j / cpr, c = j - r * cpr;
+        st16(vc + phys * vc_p + h * vc_h + r * vc_s + c * 8, x0[u]);
       }
-    } else {
-      const int j = i - total_k;
-      const int r = j / cpr, c = (j - r * cpr) * 8;
-      st16(vdst + r * vc_s + c, ld16(vsrc + r * v_t + c));
     }
   }
 }
@@ -170,7 +214,8 @@ __global__ __launch_bounds__(256) void prefill_kv_rope_fill_kernel(
 extern "C" int wy_prefill_kv_rope_fill(void *k_cache, void *v_cache, const int64_t *kcs,
                                        const int64_t *vcs, const void *k, const int64_t *ks,
                                        const void *v, const int64_t *vs, void *k_roped,
-                                       const int64_t *krs, const int32_t *block_table,
+                                       const int64_t *krs, float *rope_table,
+                                       const int32_t *block_table,
                                        int64_t bt_stride0, const int32_t *cu_seqlens,
                                        const void *position_ids, int64_t pos_stride,
                                        int pos_is_int64, const float *inv_freq, int rotary_dim,
@@ -180,7 +225,8 @@ extern "C" int wy_prefill_kv_rope_fill(void *k_cache, void *v_cache, const int64
       !block_table || !cu_seqlens || !position_ids || !inv_freq)
     return WY_E_NULL;
   if (batch < 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen < 0) return WY_E_SHAPE;
-  if (head_dim % 8 || rotary_dim <= 0 || rotary_dim % 16 || rotary_dim > head_dim)
+  if (head_dim % 8 || rotary_dim <= 0 || rotary_dim % 16 || rotary_dim > head_dim ||
+      rotary_dim > kRopeFillMaxR)
     return WY_E_SHAPE;
   const bool vec = kcs[3] == 1 && vcs[3] == 1 && ks[2] == 1 && vs[2] == 1 && krs[2] == 1 &&
                    kcs[0] % 8 == 0 && kcs[1] % 8 == 0 && kcs[2] % 8 == 0 && vcs[0] % 8 == 0 &&
@@ -190,13 +236,14 @@ extern "C" int wy_prefill_kv_rope_fill(void *k_cache, void *v_cache, const int64
                    wyh::aligned16(v) && wyh::aligned16(k_roped);
   if (!vec) return WY_E_LAYOUT;
   if (batch == 0 || max_seqlen == 0) return WY_OK;
+  if (rope_table && (reinterpret_cast<uintptr_t>(rope_table) & 15u)) return WY_E_LAYOUT;
   dim3 grid((max_seqlen + kPage - 1) / kPage, num_kv_heads, batch);
   prefill_kv_rope_fill_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<bf16_t *>(k_cache), static_cast<bf16_t *>(v_cache), kcs[0], kcs[1], kcs[2],
       vcs[0], vcs[1], vcs[2], static_cast<const bf16_t *>(k), ks[0], ks[1],
       static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(k_roped), krs[0],
-      krs[1], block_table, bt_stride0, cu_seqlens, position_ids, pos_stride, pos_is_int64,
-      inv_freq, rotary_dim, head_dim);
+      krs[1], rope_table, block_table, bt_stride0, cu_seqlens, position_ids, pos_stride,
+      pos_is_int64, inv_freq, rotary_dim, head_dim, num_kv_heads);
   return wyh::launch_status();
 }
 

@@ -118,6 +118,7 @@ struct BlockArgs {
   int64_t ps_t;
   int pos64;
   const float *inv_freq;
+  const float *rope_tab;  // [T][kRot]: sin of the kRot/2 angles, then cos
 };
 
 template <bool kList, int kRot>
@@ -340,28 +341,54 @@ void varlen_causal_prefill_kernel(
   // The q loads are issued before the first tiles' DMA, so they do not queue
   // behind it; the conversion waits for q only.
   bf16x8_t qb_op[16];
+  // Attention block: the row's gate values, requested with q so that their
+  // latency is hidden behind the block (one 8-byte chunk per output chunk of
+  // the epilogue; the loads are all issued before any is used).
+  u32x2_t gate_v[8][4];
   {
     const int qc = qrow < n ? qrow : n - 1;
     const bf16_t *qp = q + (int64_t(start) + qc) * qs_t + hq * qs_h + g * 8;
     u32x4_t xr[16];
 #pragma unroll
     for (int kk = 0; kk < 16; ++kk) xr[kk] = ld16(qp + 16 * kk);
+    // the row's sin / cos for its rotary dims (written by the K/V launch)
+    f32x4_t tsn[kRot > 0 ? kRot / 16 : 1], tcs[kRot > 0 ? kRot / 16 : 1];
+    if constexpr (kRot > 0) {
+      const float *tr = blk.rope_tab + (int64_t(start) + qc) * kRot + 8 * g;
+#pragma unroll
+      for (int kk = 0; kk < kRot / 32; ++kk)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          tsn[2 * kk + u] = *reinterpret_cast<const f32x4_t *>(tr + 16 * kk + 4 * u);
+          tcs[2 * kk + u] = *reinterpret_cast<const f32x4_t *>(tr + kRot / 2 + 16 * kk + 4 * u);
+        }
+    }
     issue_first();
+    if constexpr (kRot > 0) {
+      const bf16_t *gp = blk.gate + (int64_t(start) + qc) * blk.gs_t + hq * blk.gs_h + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          gate_v[dt][j] = *reinterpret_cast<const u32x2_t *>(gp + dt * 32 + 8 * j);
+    }
     if constexpr (kRot > 0) {
       // Partial RoPE of the raw row, the standalone kernel's device math and
       // bf16 rounding (partial_rope.py:74-98): k-step kk < kRot/32 holds dims
       // 16kk + 8g .. +7 of the first half, k-step kk + kRot/32 their partners.
+      // sin / cos come from the K/V launch's table (the same rope_sincos
+      // values the standalone kernel computes).
       static_assert(kRot % 32 == 0 && kRot <= kD, "rotary dims in whole k-step pairs");
       constexpr int kH = kRot / 32;
-      const float p = load_pos(blk.pos, (int64_t(start) + qc) * blk.ps_t, blk.pos64 != 0);
 #pragma unroll
       for (int kk = 0; kk < kH; ++kk) {
         u32x4_t a = xr[kk], bb = xr[kk + kH];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          float s0, c0, s1, c1, o1l, o2l, o1h, o2h;
-          rope_sincos(p, blk.inv_freq[16 * kk + 8 * g + 2 * w], s0, c0);
-          rope_sincos(p, blk.inv_freq[16 * kk + 8 * g + 2 * w + 1], s1, c1);
+          const f32x4_t &sv = tsn[2 * kk + w / 2], &cv = tcs[2 * kk + w / 2];
+          const float s0 = sv[2 * (w & 1)], s1 = sv[2 * (w & 1) + 1];
+          const float c0 = cv[2 * (w & 1)], c1 = cv[2 * (w & 1) + 1];
+          float o1l, o2l, o1h, o2h;
           rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), c0, s0, o1l, o2l);
           rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), c1, s1, o1h, o2h);
           a[w] = pack_bf16x2(o1l, o1h);
@@ -575,8 +602,6 @@ void varlen_causal_prefill_kernel(
   const float inv_l = 1.0f / l;
   if (qrow < n) {
     bf16_t *op = out + (int64_t(start) + qrow) * os_t + hq * os_h;
-    const bf16_t *gp = nullptr;
-    if constexpr (kRot > 0) gp = blk.gate + (int64_t(start) + qrow) * blk.gs_t + hq * blk.gs_h;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -586,7 +611,7 @@ void varlen_causal_prefill_kernel(
         if constexpr (kRot > 0) {
           // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
           // gate pack computes it
-          const u32x2_t gv = *reinterpret_cast<const u32x2_t *>(gp + dt * 32 + 8 * j + 4 * g);
+          const u32x2_t gv = gate_v[dt][j];
 #pragma unroll
           for (int e = 0; e < 2; ++e)
             w[e] = pack_bf16x2(bf16_lo(w[e]) * gate_sigmoid(bf16_lo(gv[e])),
@@ -731,9 +756,11 @@ extern "C" int wy_prefill_attention_block(
     void *k_cache, void *v_cache, const int64_t *kcs, const int64_t *vcs,
     const int32_t *block_table, int64_t bt_stride0, const int32_t *cu_seqlens, int batch,
     int num_q_heads, int num_kv_heads, int head_dim, int max_seqlen, int64_t total_tokens,
-    void *k_roped, void *out, void *workspace, int64_t workspace_bytes, void *stream) {
+    void *k_roped, float *rope_table, void *out, void *workspace, int64_t workspace_bytes,
+    void *stream) {
   if (!q || !qs || !k || !ks || !v || !vs || !gate || !gs || !position_ids || !inv_freq ||
-      !k_cache || !v_cache || !kcs || !vcs || !block_table || !cu_seqlens || !k_roped || !out)
+      !k_cache || !v_cache || !kcs || !vcs || !block_table || !cu_seqlens || !k_roped || !rope_table ||
+      !out)
     return WY_E_NULL;
   if (batch < 0 || num_kv_heads <= 0 || max_seqlen < 0 || total_tokens < 0)
     return WY_E_SHAPE;
@@ -751,14 +778,15 @@ extern "C" int wy_prefill_attention_block(
     return WY_E_LAYOUT;
   if (batch == 0 || max_seqlen == 0) return WY_OK;
   // 1. RoPE of K, K/V into the pages, roped K packed for the attention
+  if (reinterpret_cast<uintptr_t>(rope_table) & 15u) return WY_E_LAYOUT;
   int rc = wy_prefill_kv_rope_fill(k_cache, v_cache, kcs, vcs, k, ks, v, vs, k_roped, krs,
-                                   block_table, bt_stride0, cu_seqlens, position_ids,
+                                   rope_table, block_table, bt_stride0, cu_seqlens, position_ids,
                                    pos_stride, pos_is_int64, inv_freq, rotary_dim, batch,
                                    num_kv_heads, head_dim, max_seqlen, stream);
   if (rc != WY_OK) return rc;
   // 2. attention with q's RoPE at load and the gate in the epilogue
   const BlockArgs blk{static_cast<const bf16_t *>(gate), gs[0], gs[1], position_ids,
-                      pos_stride, pos_is_int64, inv_freq};
+                      pos_stride, pos_is_int64, inv_freq, rope_table};
   return launch_prefill<64>(q, qs, k_roped, krs, v, vs, out, os, cu_seqlens, batch,
                             num_kv_heads, head_dim, max_seqlen, workspace, workspace_bytes,
                             blk, static_cast<hipStream_t>(stream));

@@ -101,6 +101,7 @@ def prefill_attention_block(
     assert batch >= 1
     pos = position_ids.reshape(-1)
     k_roped = torch.empty((total_tokens, num_kv_head, d_model), dtype=q.dtype, device=q.device)
+    rope_table = torch.empty((total_tokens, rotary_dim), dtype=torch.float32, device=q.device)
     out = torch.empty((total_tokens, num_q_head * d_model), dtype=q.dtype, device=q.device)
     ws_bytes = _lib.load().wy_varlen_causal_prefill_workspace_bytes(
         batch, num_kv_head, max_seqlen
@@ -113,7 +114,8 @@ def prefill_attention_block(
         int(pos.dtype == torch.int64), _lib.ptr(inv_freq), rotary_dim, _lib.ptr(k_cache),
         _lib.ptr(v_cache), _lib.strides(k_cache), _lib.strides(v_cache), _lib.ptr(block_table),
         block_table.stride(0), _lib.ptr(cu_seqlens), batch, num_q_head, num_kv_head, d_model,
-        max_seqlen, total_tokens, _lib.ptr(k_roped), _lib.ptr(out), _lib.ptr(ws),
+        max_seqlen, total_tokens, _lib.ptr(k_roped), _lib.ptr(rope_table), _lib.ptr(out),
+        _lib.ptr(ws),
         ws.numel() if ws is not None else 0, _lib.stream(q.device),
     )
     return out

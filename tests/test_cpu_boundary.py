@@ -62,8 +62,8 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
     # prefill block: rotary widths other than 64 are unsupported; NULL gate
     pos = ctypes.c_void_p(64)
     args = [dummy, s3p, dummy, s3k, dummy, s3k, dummy, s3p, pos, 1, 0, dummy]
-    tail = [dummy, dummy, s4, s4, dummy, 4, dummy, 1, 8, 2, 256, 16, 16, dummy, dummy, None, 0,
-            None]
+    tail = [dummy, dummy, s4, s4, dummy, 4, dummy, 1, 8, 2, 256, 16, 16, dummy, dummy, dummy,
+            None, 0, None]
     assert lib.wy_prefill_attention_block(*args, 32, *tail) == -4
     args[6] = None
     assert lib.wy_prefill_attention_block(*args, 64, *tail) == -1
