@@ -409,6 +409,10 @@ def main():
     if want("gemm"):
         extra["gemm_2d"] = gemm_bench(pkg, dev)
 
+    # ---- Gated DeltaNet recurrence (the other mixer of the model) -------------
+    if want("gdn"):
+        extra["gdn"] = gdn_bench(pkg, dev)
+
     if extra:
         result["extra"] = extra
 
@@ -479,6 +483,46 @@ def prefill_path_bench(pkg, dev, lengths, seed):
             "what": "after q/k norm: RoPE q/k + varlen attention + gate pack + K/V page "
                     "scatter; op sequence (reference order, 6 launches) vs the two-launch "
                     "prefill attention block (bit-identical)"}
+
+
+def gdn_bench(pkg, dev):
+    """Gated DeltaNet recurrence (the linear-attention mixer, 16 heads of
+    128 x 128 fp32 state): decode graph-timed as algorithmic HBM GB/s (state
+    read + written once, q/k/v/out, beta/g), sequential prefill as tokens/s."""
+    gen = torch.Generator(device=dev).manual_seed(5)
+    H, DK, DV = 16, 128, 128
+
+    def qkv(T):
+        q = torch.nn.functional.normalize(torch.randn(T, H, DK, device=dev, generator=gen), dim=-1)
+        k = torch.nn.functional.normalize(torch.randn(T, H, DK, device=dev, generator=gen), dim=-1)
+        v = torch.randn(T, H, DV, device=dev, generator=gen)
+        beta = torch.sigmoid(torch.randn(T, H, device=dev, generator=gen))
+        g = -torch.nn.functional.softplus(torch.randn(T, H, device=dev, generator=gen))
+        return ((q * DK ** -0.5).to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16),
+                beta, g)
+
+    out = {}
+    for B in (1, 32, 256):
+        q, k, v, beta, g = qkv(B)
+        state = torch.randn(B, H, DK, DV, device=dev, generator=gen) * 0.1
+        nbytes = B * H * (2 * DK * DV * 4 + (2 * DK + 2 * DV) * 2 + 8)
+        ms = time_graph_events(lambda: pkg.gdn_recurrent_decode(q, k, v, beta, g, state), 20)
+        out[f"gdn_recurrent_decode B={B}"] = {
+            "us": round(ms * 1e3, 2), "GB/s": round(nbytes / ms / 1e6, 1),
+            "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    for lengths in ([128] * 32, [4096]):
+        T = sum(lengths)
+        q, k, v, beta, g = qkv(T)
+        cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32,
+                          device=dev)
+        # the op reads cu_seqlens[-1] on the host (reference assertion): not capturable
+        ms = time_events(lambda: pkg.gdn_recurrent_prefill_sequential(q, k, v, beta, g, cu), 5)
+        name = f"gdn_recurrent_prefill_sequential {len(lengths)} x {lengths[0]}"
+        out[name] = {"us": round(ms * 1e3, 2), "tokens/s": round(T / ms * 1e3, 1),
+                     "us_per_token_step": round(ms * 1e3 / max(lengths), 4)}
+    for name, r in out.items():
+        log(f"gdn {name}: {r}")
+    return out
 
 
 def elementwise_bench(pkg, dev):

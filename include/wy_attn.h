@@ -327,6 +327,44 @@ int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w,
  */
 int64_t wy_gemm_2d_workspace_bytes(int M, int N, int K);
 
+/*
+ * Gated DeltaNet delta-rule decode: one token per sequence, the fp32 state
+ * updated in place.  For each (b, h):  S = exp(g) S;  delta = beta (v - k^T S);
+ * S += k delta^T;  out = bf16(q^T S).
+ * q, k [B, H, key_dim], v, out [B, H, value_dim] bf16 (element strides, any);
+ * beta, g [B, H] fp32; state [B, H, key_dim, value_dim] fp32 (unit inner
+ * stride, 16-byte aligned rows).  key_dim 128, value_dim a multiple of 128
+ * (else WY_E_UNSUPPORTED).  Allocates nothing; one launch.
+ * Replaces wy_lib::gdn_recurrent_decode
+ *   (triton_kernels/gdn_recurrent_prefill.py:1185-1260, kernel :151-246).
+ */
+int wy_gdn_recurrent_decode(const void *q, const int64_t *q_strides, const void *k,
+                            const int64_t *k_strides, const void *v, const int64_t *v_strides,
+                            const float *beta, const int64_t *beta_strides, const float *g,
+                            const int64_t *g_strides, void *out, const int64_t *out_strides,
+                            float *state, const int64_t *state_strides, int batch,
+                            int num_heads, int key_dim, int value_dim, void *stream);
+
+/*
+ * Gated DeltaNet sequential prefill over a packed varlen batch: sequence b
+ * owns tokens [cu_seqlens[b], cu_seqlens[b+1]) of q, k [T, H, key_dim],
+ * v, out [T, H, value_dim] (bf16), beta, g [T, H] fp32, and starts from a
+ * zero state; its final state goes to state[b] ([B, H, key_dim, value_dim]
+ * fp32, unit inner stride).  cu_seqlens [B+1] int32 on the device.  Same
+ * step as wy_gdn_recurrent_decode.  Allocates nothing; one launch.
+ * Replaces wy_lib::gdn_recurrent_prefill_sequential
+ *   (triton_kernels/gdn_recurrent_prefill.py:1050-1146, kernel :52-143).
+ */
+int wy_gdn_recurrent_prefill_sequential(const void *q, const int64_t *q_strides, const void *k,
+                                        const int64_t *k_strides, const void *v,
+                                        const int64_t *v_strides, const float *beta,
+                                        const int64_t *beta_strides, const float *g,
+                                        const int64_t *g_strides, void *out,
+                                        const int64_t *out_strides, float *state,
+                                        const int64_t *state_strides,
+                                        const int32_t *cu_seqlens, int batch, int num_heads,
+                                        int key_dim, int value_dim, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

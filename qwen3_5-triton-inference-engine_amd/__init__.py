@@ -39,6 +39,12 @@ from .gqa_attention_decode_paged import (
     paged_kv_fill_varlen,
     physical_rows,
 )
+from .gdn_recurrent_prefill import (
+    call_gdn_recurrent_decode_triton,
+    call_gdn_recurrent_prefill_sequential_triton,
+    gdn_recurrent_decode,
+    gdn_recurrent_prefill_sequential,
+)
 from .gqa_attention_varlen_causal import build_cu_seqlens, gqa_attention_varlen_causal
 from .paging import PagePool, SequencePages, allocate_block_table
 from .partial_rope import partial_rope, rope_inv_freq
@@ -56,6 +62,7 @@ def install_as_triton_kernels() -> None:
         ("triton_kernels.attention_gate_pack", "attention_gate_pack"),
         ("triton_kernels.qwen_rmsnorm", "qwen_rmsnorm"),
         ("triton_kernels.gemm_2d", "gemm_2d"),
+        ("triton_kernels.gdn_recurrent_prefill", "gdn_recurrent_prefill"),
         ("engine.paging", "paging"),
     ):
         # the submodule itself: several share their name with the op they define

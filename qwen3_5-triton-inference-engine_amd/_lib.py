@@ -53,6 +53,11 @@ _SIGNATURES = {
                               _vp, _f, _vp, _i, _vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp,
                               _vp, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _i, _i,
                               _i, _i, _i, _i, _vp],
+    "wy_gdn_recurrent_decode": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
+                                _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _i, _i, _i, _vp],
+    "wy_gdn_recurrent_prefill_sequential": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
+                                            _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
+                                            _vp, _i, _i, _i, _i, _vp],
 }
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)

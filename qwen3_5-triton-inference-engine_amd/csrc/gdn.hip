@@ -1,0 +1,312 @@
+// Gated DeltaNet (GDN) delta-rule recurrence on gfx950: the decode update of
+// the cached state and the varlen sequential prefill.
+//
+// Per token t and value head h, with the state S [DK, DV] fp32:
+//   S      = exp(g_t) * S
+//   mem    = k_t^T S                         [DV]
+//   delta  = beta_t * (v_t - mem)            [DV]
+//   S      = S + k_t delta^T
+//   out_t  = q_t^T S                         [DV]  (stored as bf16)
+// Reference: gdn_recurrent_prefill.py:52-143 (sequential kernel), :151-246
+// (decode kernel), ops :1050-1146 and :1185-1260.
+//
+// Layout on the chip: one wavefront owns 16 value columns of one (sequence,
+// head) with all DK = 128 key rows.  Lane = kg + 16 * cg: kg (0..15) picks
+// key rows 8kg..8kg+7, cg (0..3) picks columns 4cg..4cg+3 of the wave's 16,
+// so a lane holds 8 x 4 fp32 state values and every reduction over the key
+// rows stays inside one 16-lane DPP row (no LDS, no barrier per token).
+// The output uses q^T S_new = q^T S_decayed + (q^T k) delta, the same value
+// as the reference's q^T S_new, so the two reductions of a token (k^T S and
+// q^T S, plus q^T k) run together, before the update.
+#include "wy_common.h"
+
+using namespace wy;
+
+namespace {
+
+constexpr int kDK = 128;      // key rows per state (Qwen3.5 linear attention)
+constexpr int kRows = 8;      // key rows per lane
+constexpr int kCols = 4;      // value columns per lane
+constexpr int kWaveCols = 16; // value columns per wavefront
+
+struct GdnArgs {
+  const bf16_t *q, *k, *v;
+  int64_t q_t, q_h, q_d, k_t, k_h, k_d, v_t, v_h, v_d;
+  const float *beta, *g;
+  int64_t beta_t, beta_h, g_t, g_h;
+  bf16_t *out;
+  int64_t o_t, o_h, o_d;
+  float *state;
+  int64_t s_b, s_h, s_k, s_v;
+  const int32_t *cu_seqlens;  // prefill only
+  int heads, dv;
+};
+
+template <int kRor>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + kRor, 0xf, 0xf,
+                                                    false));
+}
+// Sum over each 16-lane row; the rotation butterfly gives every lane of the
+// row the same value (each level pairs lanes symmetrically).
+__device__ __forceinline__ float sum16(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return v;
+}
+
+// 8 consecutive bf16 (key rows 8kg..8kg+7) as fp32.
+template <bool kContig>
+__device__ __forceinline__ void load8(const bf16_t *p, int64_t stride, float (&x)[kRows]) {
+  if constexpr (kContig) {
+    const u32x4_t w = ld16(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf16_lo(w[e]);
+      x[2 * e + 1] = bf16_hi(w[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kRows; ++e) x[e] = bf16_to_f32(p[e * stride]);
+  }
+}
+template <bool kContig>
+__device__ __forceinline__ void load4(const bf16_t *p, int64_t stride, float (&x)[kCols]) {
+  if constexpr (kContig) {
+    const u32x2_t w = *reinterpret_cast<const u32x2_t *>(p);
+    x[0] = bf16_lo(w[0]);
+    x[1] = bf16_hi(w[0]);
+    x[2] = bf16_lo(w[1]);
+    x[3] = bf16_hi(w[1]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kCols; ++e) x[e] = bf16_to_f32(p[e * stride]);
+  }
+}
+template <bool kContig>
+__device__ __forceinline__ void store4(bf16_t *p, int64_t stride, const float (&x)[kCols]) {
+  if constexpr (kContig) {
+    *reinterpret_cast<u32x2_t *>(p) = u32x2_t{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  } else {
+#pragma unroll
+    for (int e = 0; e < kCols; ++e) p[e * stride] = bf16_t(f32_to_bf16_bits(x[e]));
+  }
+}
+
+// One token's inputs for one lane.
+struct TokenIn {
+  float k[kRows], q[kRows], v[kCols];
+  float g, beta;
+};
+
+template <bool kContig>
+__device__ __forceinline__ void load_token(const GdnArgs &a, int64_t t, int h, int kg, int col,
+                                           TokenIn &in) {
+  load8<kContig>(a.k + t * a.k_t + h * a.k_h + kg * kRows * a.k_d, a.k_d, in.k);
+  load8<kContig>(a.q + t * a.q_t + h * a.q_h + kg * kRows * a.q_d, a.q_d, in.q);
+  load4<kContig>(a.v + t * a.v_t + h * a.v_h + col * a.v_d, a.v_d, in.v);
+  in.g = a.g[t * a.g_t + h * a.g_h];
+  in.beta = a.beta[t * a.beta_t + h * a.beta_h];
+}
+
+// One delta-rule step on the lane's 8 x 4 block of S; returns the lane's 4
+// output columns (identical in all 16 lanes of the row).
+__device__ __forceinline__ void gdn_step(float (&s)[kRows][kCols], const TokenIn &in,
+                                         float (&o)[kCols]) {
+  const float e = __expf(in.g);
+  float mem[kCols], qs[kCols], qk = 0.f;
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) {
+    mem[j] = 0.f;
+    qs[j] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    qk = __fmaf_rn(in.q[i], in.k[i], qk);
+#pragma unroll
+    for (int j = 0; j < kCols; ++j) {
+      s[i][j] = e * s[i][j];
+      mem[j] = __fmaf_rn(in.k[i], s[i][j], mem[j]);
+      qs[j] = __fmaf_rn(in.q[i], s[i][j], qs[j]);
+    }
+  }
+  qk = sum16(qk);
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) {
+    mem[j] = sum16(mem[j]);
+    qs[j] = sum16(qs[j]);
+  }
+  float delta[kCols];
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) {
+    delta[j] = in.beta * (in.v[j] - mem[j]);
+    o[j] = __fmaf_rn(qk, delta[j], qs[j]);
+  }
+#pragma unroll
+  for (int i = 0; i < kRows; ++i)
+#pragma unroll
+    for (int j = 0; j < kCols; ++j) s[i][j] = __fmaf_rn(in.k[i], delta[j], s[i][j]);
+}
+
+__device__ __forceinline__ float *state_block(const GdnArgs &a, int b, int h, int kg, int col) {
+  return a.state + b * a.s_b + h * a.s_h + int64_t(kg * kRows) * a.s_k + col;
+}
+
+// Decode: one token per sequence, S read from and written back to the cache.
+// Workgroup = 8 wavefronts = 128 value columns of one (sequence, head); all
+// 8 state loads of a lane are issued before the first use.
+template <bool kContig>
+__global__ __launch_bounds__(512) void gdn_recurrent_decode_kernel(const GdnArgs a) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.heads, h = bh - b * a.heads;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kg = lane & 15, cg = lane >> 4;
+  const int col = blockIdx.y * 128 + wave * kWaveCols + cg * kCols;
+  float *sp = state_block(a, b, h, kg, col);
+  float s[kRows][kCols];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const float4 x = *reinterpret_cast<const float4 *>(sp + i * a.s_k);
+    s[i][0] = x.x;
+    s[i][1] = x.y;
+    s[i][2] = x.z;
+    s[i][3] = x.w;
+  }
+  TokenIn in;
+  load_token<kContig>(a, b, h, kg, col, in);
+  float o[kCols];
+  gdn_step(s, in, o);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i)
+    *reinterpret_cast<float4 *>(sp + i * a.s_k) = make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
+  if (kg == 0) store4<kContig>(a.out + b * a.o_t + h * a.o_h + col * a.o_d, a.o_d, o);
+}
+
+// Varlen sequential prefill: one wavefront per (sequence, head, 16 value
+// columns), walking its sequence's tokens in order from a zero state; the
+// next token's inputs are requested before the current token's update.
+template <bool kContig>
+__global__ __launch_bounds__(64) void gdn_prefill_sequential_kernel(const GdnArgs a, int batch) {
+  // grid: sequence fastest, then head, then column block
+  const int b = blockIdx.x % batch;
+  const int h = (blockIdx.x / batch) % a.heads;
+  const int vb = blockIdx.x / (batch * a.heads);
+  const int lane = threadIdx.x;
+  const int kg = lane & 15, cg = lane >> 4;
+  const int col = vb * kWaveCols + cg * kCols;
+  const int start = a.cu_seqlens[b];
+  const int len = a.cu_seqlens[b + 1] - start;
+  float s[kRows][kCols];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i)
+#pragma unroll
+    for (int j = 0; j < kCols; ++j) s[i][j] = 0.f;
+  if (len > 0) {
+    TokenIn cur, nxt;
+    load_token<kContig>(a, start, h, kg, col, cur);
+    for (int t = 0; t < len; ++t) {
+      const int64_t tok = start + t;
+      if (t + 1 < len) load_token<kContig>(a, tok + 1, h, kg, col, nxt);
+      float o[kCols];
+      gdn_step(s, cur, o);
+      if (kg == 0) store4<kContig>(a.out + tok * a.o_t + h * a.o_h + col * a.o_d, a.o_d, o);
+      cur = nxt;
+    }
+  }
+  float *sp = state_block(a, b, h, kg, col);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i)
+    *reinterpret_cast<float4 *>(sp + i * a.s_k) = make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
+}
+
+// Shared argument checks; returns WY_OK and fills a, or an error code.
+int gdn_setup(GdnArgs &a, bool &contig, const void *q, const int64_t *qs, const void *k,
+              const int64_t *ks, const void *v, const int64_t *vs, const float *beta,
+              const int64_t *bs, const float *g, const int64_t *gs, void *out,
+              const int64_t *os, float *state, const int64_t *ss, int heads, int key_dim,
+              int value_dim) {
+  if (!q || !qs || !k || !ks || !v || !vs || !beta || !bs || !g || !gs || !out || !os ||
+      !state || !ss)
+    return WY_E_NULL;
+  if (heads <= 0 || key_dim <= 0 || value_dim <= 0) return WY_E_SHAPE;
+  if (key_dim != kDK || value_dim % 128 != 0) return WY_E_UNSUPPORTED;
+  if (ss[3] != 1 || ss[2] % 4 || ss[1] % 4 || ss[0] % 4 || !wyh::aligned16(state))
+    return WY_E_LAYOUT;
+  a = GdnArgs{};
+  a.q = static_cast<const bf16_t *>(q);
+  a.k = static_cast<const bf16_t *>(k);
+  a.v = static_cast<const bf16_t *>(v);
+  a.q_t = qs[0]; a.q_h = qs[1]; a.q_d = qs[2];
+  a.k_t = ks[0]; a.k_h = ks[1]; a.k_d = ks[2];
+  a.v_t = vs[0]; a.v_h = vs[1]; a.v_d = vs[2];
+  a.beta = beta; a.beta_t = bs[0]; a.beta_h = bs[1];
+  a.g = g; a.g_t = gs[0]; a.g_h = gs[1];
+  a.out = static_cast<bf16_t *>(out);
+  a.o_t = os[0]; a.o_h = os[1]; a.o_d = os[2];
+  a.state = state;
+  a.s_b = ss[0]; a.s_h = ss[1]; a.s_k = ss[2]; a.s_v = ss[3];
+  a.heads = heads;
+  a.dv = value_dim;
+  // 16-byte q/k rows (8 bf16 per lane) and 8-byte v / out quads
+  contig = qs[2] == 1 && ks[2] == 1 && vs[2] == 1 && os[2] == 1 && qs[0] % 8 == 0 &&
+           qs[1] % 8 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && wyh::aligned16(q) &&
+           wyh::aligned16(k) && vs[0] % 4 == 0 && vs[1] % 4 == 0 && os[0] % 4 == 0 &&
+           os[1] % 4 == 0 && (reinterpret_cast<uintptr_t>(v) & 7u) == 0 &&
+           (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+  return WY_OK;
+}
+
+}  // namespace
+
+extern "C" int wy_gdn_recurrent_decode(const void *q, const int64_t *q_strides, const void *k,
+                                       const int64_t *k_strides, const void *v,
+                                       const int64_t *v_strides, const float *beta,
+                                       const int64_t *beta_strides, const float *g,
+                                       const int64_t *g_strides, void *out,
+                                       const int64_t *out_strides, float *state,
+                                       const int64_t *state_strides, int batch, int num_heads,
+                                       int key_dim, int value_dim, void *stream) {
+  GdnArgs a;
+  bool contig = false;
+  const int rc = gdn_setup(a, contig, q, q_strides, k, k_strides, v, v_strides, beta,
+                           beta_strides, g, g_strides, out, out_strides, state, state_strides,
+                           num_heads, key_dim, value_dim);
+  if (rc != WY_OK) return rc;
+  if (batch < 0) return WY_E_SHAPE;
+  if (batch == 0) return WY_OK;
+  const dim3 grid(unsigned(batch * num_heads), unsigned(value_dim / 128));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (contig)
+    gdn_recurrent_decode_kernel<true><<<grid, 512, 0, st>>>(a);
+  else
+    gdn_recurrent_decode_kernel<false><<<grid, 512, 0, st>>>(a);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_gdn_recurrent_prefill_sequential(
+    const void *q, const int64_t *q_strides, const void *k, const int64_t *k_strides,
+    const void *v, const int64_t *v_strides, const float *beta, const int64_t *beta_strides,
+    const float *g, const int64_t *g_strides, void *out, const int64_t *out_strides,
+    float *state, const int64_t *state_strides, const int32_t *cu_seqlens, int batch,
+    int num_heads, int key_dim, int value_dim, void *stream) {
+  GdnArgs a;
+  bool contig = false;
+  const int rc = gdn_setup(a, contig, q, q_strides, k, k_strides, v, v_strides, beta,
+                           beta_strides, g, g_strides, out, out_strides, state, state_strides,
+                           num_heads, key_dim, value_dim);
+  if (rc != WY_OK) return rc;
+  if (!cu_seqlens) return WY_E_NULL;
+  if (batch < 0) return WY_E_SHAPE;
+  if (batch == 0) return WY_OK;
+  a.cu_seqlens = cu_seqlens;
+  const int64_t blocks = int64_t(batch) * num_heads * (value_dim / kWaveCols);
+  if (blocks > 0x7fffffff) return WY_E_SHAPE;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (contig)
+    gdn_prefill_sequential_kernel<true><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+  else
+    gdn_prefill_sequential_kernel<false><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+  return wyh::launch_status();
+}

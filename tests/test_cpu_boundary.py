@@ -131,6 +131,11 @@ def test_op_schemas_match_reference():
         "attention_gate_pack": "(Tensor x, Tensor gate) -> Tensor",
         "qwen_rmsnorm": "(Tensor x, Tensor weight, float eps=9.9999999999999995e-07) -> Tensor",
         "gemm_2d": "(Tensor x, Tensor weight) -> Tensor",
+        "gdn_recurrent_decode": "(Tensor q, Tensor k, Tensor v, Tensor beta, Tensor g, "
+                                "Tensor(a5!) state) -> Tensor",
+        "gdn_recurrent_prefill_sequential": "(Tensor q, Tensor k, Tensor v, Tensor beta, "
+                                            "Tensor g, Tensor? cu_seqlens=None) "
+                                            "-> (Tensor, Tensor)",
     }
     for name, sig in schemas.items():
         op = getattr(torch.ops.wy_lib, name).default
@@ -167,6 +172,15 @@ def test_fake_impls_give_reference_shapes(pkg):
             torch.empty(1, 4, dtype=torch.int32, device="cuda"),
             torch.empty(2, dtype=torch.int32, device="cuda"), 9)
         assert out.shape == (9, 2048) and out.dtype == torch.bfloat16
+        qg = torch.empty(6, 16, 128, dtype=torch.bfloat16, device="cuda")
+        bg = torch.empty(6, 16, device="cuda")
+        o, st = torch.ops.wy_lib.gdn_recurrent_prefill_sequential(qg, qg, qg, bg, bg)
+        assert o.shape == (6, 16, 128) and st.shape == (16, 128, 128)
+        o, st = torch.ops.wy_lib.gdn_recurrent_prefill_sequential(
+            qg, qg, qg, bg, bg, torch.empty(3, dtype=torch.int32, device="cuda"))
+        assert st.shape == (2, 16, 128, 128) and st.dtype == torch.float32
+        sd = torch.empty(6, 16, 128, 128, device="cuda")
+        assert torch.ops.wy_lib.gdn_recurrent_decode(qg, qg, qg, bg, bg, sd).shape == (6, 16, 128)
 
 
 def test_gemm_2d_asserts_reference_preconditions(pkg):
