@@ -510,6 +510,28 @@ def gdn_bench(pkg, dev):
         out[f"gdn_recurrent_decode B={B}"] = {
             "us": round(ms * 1e3, 2), "GB/s": round(nbytes / ms / 1e6, 1),
             "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    # the whole decode mixer between the fused projection and out_proj
+    for B in (1, 32):
+        HD = H * DK
+        fused = torch.randn(B, 4 * HD + 2 * H, device=dev, generator=gen).to(torch.bfloat16)
+        cs = torch.randn(B, 4, 3 * HD, device=dev, generator=gen).to(torch.bfloat16)
+        cw = (torch.randn(4, 3 * HD, device=dev, generator=gen) * 0.5).to(torch.bfloat16)
+        a_log = torch.log(torch.rand(H, device=dev, generator=gen) * 15 + 1)
+        dt = torch.randn(H, device=dev, generator=gen).to(torch.bfloat16)
+        nw = 1 + 0.1 * torch.randn(DK, device=dev, generator=gen)
+        state = torch.randn(B, H, DK, DV, device=dev, generator=gen) * 0.1
+        ms_blk = time_graph_events(
+            lambda: pkg.gdn_decode_block(fused, cs, cw, a_log, dt, nw, state), 20)
+        ms_ops = time_graph_events(
+            lambda: pkg.gdn_decode_ops(fused, cs, cw, a_log, dt, nw, state), 20)
+        nbytes = B * H * 2 * DK * DV * 4 + B * (4 * HD + 2 * H) * 2 + B * 2 * 4 * 3 * HD * 2 \
+            + B * HD * 2
+        out[f"gdn_decode_block B={B}"] = {
+            "us": round(ms_blk * 1e3, 2), "op_sequence_us": round(ms_ops * 1e3, 2),
+            "GB/s": round(nbytes / ms_blk / 1e6, 1),
+            "frac_of_hbm_peak": round(nbytes / ms_blk / 1e6 / HBM_PEAK_GBS, 4),
+            "what": "conv4 decode + q/k norm + gates + recurrence + gated RMSNorm, one launch "
+                    "vs the 4-op sequence"}
     for lengths in ([128] * 32, [4096]):
         T = sum(lengths)
         q, k, v, beta, g = qkv(T)

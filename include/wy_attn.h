@@ -365,6 +365,70 @@ int wy_gdn_recurrent_prefill_sequential(const void *q, const int64_t *q_strides,
                                         const int32_t *cu_seqlens, int batch, int num_heads,
                                         int key_dim, int value_dim, void *stream);
 
+/*
+ * Depthwise causal conv (4 taps) decode step + SiLU.  x [B, C] bf16 (element
+ * strides); state [B, 4, C] bf16 (unit channel stride) holds the last four
+ * conv inputs and is shifted in place (x enters at tap 3); weight [4, C] bf16
+ * (unit channel stride).  out[b, c] = bf16(silu(sum_r w[r, c] * state'[b, r, c]))
+ * with fp32 accumulation in tap order.  Allocates nothing; one launch.
+ * Replaces wy_lib::depthwise_causal_conv4_decode
+ *   (triton_kernels/depthwise_causal_conv4_decode.py:152-205, kernel :86-150).
+ */
+int wy_depthwise_causal_conv4_decode(const void *x, const int64_t *x_strides, void *state,
+                                     const int64_t *state_strides, const void *weight,
+                                     const int64_t *w_strides, void *out,
+                                     const int64_t *out_strides, int batch, int channels,
+                                     void *stream);
+
+/*
+ * GDN q/k L2 norm and gates.  q, k [T, H, D] bf16 (element strides), a, b
+ * [T, H] bf16, a_log [H] fp32, dt_bias [H] bf16.  Writes q_norm, k_norm
+ * ([T, H, D] contiguous bf16): q * rsqrt(sum q^2 + 1e-6) * D^-1/2 and
+ * k * rsqrt(sum k^2 + 1e-6); beta, g ([T, H] contiguous fp32):
+ * sigmoid(b) and -exp(a_log) * softplus(a + dt_bias).  D = 128.
+ * Replaces wy_lib::gdn_qk_norm_gates
+ *   (triton_kernels/gdn_qk_norm_gates.py:127-201, kernel :19-115).
+ */
+int wy_gdn_qk_norm_gates(const void *q, const int64_t *q_strides, const void *k,
+                         const int64_t *k_strides, const void *a, const int64_t *a_strides,
+                         const void *b, const int64_t *b_strides, const float *a_log,
+                         const void *dt_bias, void *q_norm, void *k_norm, float *beta, float *g,
+                         int tokens, int num_heads, int head_dim, void *stream);
+
+/*
+ * GDN gated RMSNorm.  x, z [T, H, D] bf16 (element strides), weight [D] fp32;
+ * out [T, H, D] contiguous bf16 = x * rsqrt(mean(x^2) + 1e-6) * w * z * sigmoid(z).
+ * D = 128.
+ * Replaces wy_lib::gdn_gated_rmsnorm
+ *   (triton_kernels/gdn_gated_rmsnorm.py:88-137, kernel :21-76).
+ */
+int wy_gdn_gated_rmsnorm(const void *x, const int64_t *x_strides, const void *z,
+                         const int64_t *z_strides, const float *weight, void *out, int tokens,
+                         int num_heads, int head_dim, void *stream);
+
+/*
+ * GDN decode mixer in one launch, from the fused projection row to the
+ * out_proj input: conv4 decode + SiLU of the q/k/v channels (conv_state
+ * shifted in place), q/k L2 norm and gates, one delta-rule step (state
+ * advanced in place), gated RMSNorm.  Equals, bit for bit, the sequence
+ * wy_depthwise_causal_conv4_decode -> wy_gdn_qk_norm_gates ->
+ * wy_gdn_recurrent_decode -> wy_gdn_gated_rmsnorm.
+ * fused [B, 3HD + HD + 2H] bf16 (row stride fused_stride0): q|k|v conv
+ * inputs, z, a, b as the reference's in_proj_fused rows; conv_state
+ * [B, 4, 3HD] bf16; conv_weight [4, 3HD] bf16; a_log [H] fp32; dt_bias [H]
+ * bf16; norm_weight [D] fp32; state [B, H, D, D] fp32 (unit inner stride,
+ * 16-byte rows); out [B, H*D] bf16 (row stride out_stride0).  D = 128.
+ * Replaces the runner's GDN decode sequence between the fused projection and
+ * out_proj (engine/runner.py:431-441): depthwise_causal_conv4_decode,
+ * gdn_qk_norm_gates, gdn_recurrent_decode, gdn_gated_rmsnorm.
+ */
+int wy_gdn_decode_block(const void *fused, int64_t fused_stride0, void *conv_state,
+                        const int64_t *conv_state_strides, const void *conv_weight,
+                        int64_t conv_weight_stride0, const float *a_log, const void *dt_bias,
+                        const float *norm_weight, float *state, const int64_t *state_strides,
+                        void *out, int64_t out_stride0, int batch, int num_heads, int head_dim,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,14 @@ from .gqa_attention_decode_paged import (
     paged_kv_fill_varlen,
     physical_rows,
 )
+from .depthwise_causal_conv4_decode import (
+    call_depthwise_causal_conv4_decode_triton,
+    conv_state_from_prefill,
+    depthwise_causal_conv4_decode,
+)
+from .gdn_gated_rmsnorm import call_gdn_gated_rmsnorm_triton, gdn_gated_rmsnorm
+from .gdn_mixer import gdn_decode_block, gdn_decode_ops
+from .gdn_qk_norm_gates import call_gdn_qk_norm_gates_triton, gdn_qk_norm_gates
 from .gdn_recurrent_prefill import (
     call_gdn_recurrent_decode_triton,
     call_gdn_recurrent_prefill_sequential_triton,
@@ -63,6 +71,9 @@ def install_as_triton_kernels() -> None:
         ("triton_kernels.qwen_rmsnorm", "qwen_rmsnorm"),
         ("triton_kernels.gemm_2d", "gemm_2d"),
         ("triton_kernels.gdn_recurrent_prefill", "gdn_recurrent_prefill"),
+        ("triton_kernels.gdn_qk_norm_gates", "gdn_qk_norm_gates"),
+        ("triton_kernels.gdn_gated_rmsnorm", "gdn_gated_rmsnorm"),
+        ("triton_kernels.depthwise_causal_conv4_decode", "depthwise_causal_conv4_decode"),
         ("engine.paging", "paging"),
     ):
         # the submodule itself: several share their name with the op they define

@@ -58,6 +58,13 @@ _SIGNATURES = {
     "wy_gdn_recurrent_prefill_sequential": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
                                             _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
                                             _vp, _i, _i, _i, _i, _vp],
+    "wy_depthwise_causal_conv4_decode": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
+                                         _c_i64p, _i, _i, _vp],
+    "wy_gdn_qk_norm_gates": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _vp,
+                             _vp, _vp, _vp, _vp, _i, _i, _i, _vp],
+    "wy_gdn_gated_rmsnorm": [_vp, _c_i64p, _vp, _c_i64p, _vp, _vp, _i, _i, _i, _vp],
+    "wy_gdn_decode_block": [_vp, _i64, _vp, _c_i64p, _vp, _i64, _vp, _vp, _vp, _vp, _c_i64p,
+                            _vp, _i64, _i, _i, _i, _vp],
 }
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)

@@ -1,0 +1,371 @@
+// The Gated DeltaNet decode mixer around the recurrence, on gfx950:
+//   * depthwise causal conv4 decode (+ SiLU) with its rolling input state
+//     (depthwise_causal_conv4_decode.py:86-150, op :152-205),
+//   * per-head q/k L2 norm and the beta / g gates (gdn_qk_norm_gates.py:19-115,
+//     op :127-201),
+//   * gated RMSNorm of the recurrence output (gdn_gated_rmsnorm.py:21-76,
+//     op :88-137),
+// each as a standalone kernel, and all of them together with the recurrence
+// step as one launch per decode step (the runner's _gdn_decode between the
+// fused projection and out_proj, engine/runner.py:431-441).  The fused
+// launch calls the same device functions with the same reduction shapes as
+// the standalone kernels, so it equals the op-by-op sequence bit for bit.
+#include "gdn_common.h"
+
+using namespace wy;
+using namespace wy::gdn;
+
+namespace {
+
+// acc = x[t-3] w0 + x[t-2] w1 + x[t-1] w2 + x[t] w3 (fp32, in tap order),
+// y = acc * sigmoid(acc) rounded to bf16.
+__device__ __forceinline__ uint32_t conv4_silu(float s1, float s2, float s3, float x, float w0,
+                                               float w1, float w2, float w3) {
+  float acc = s1 * w0;
+  acc = __fmaf_rn(s2, w1, acc);
+  acc = __fmaf_rn(s3, w2, acc);
+  acc = __fmaf_rn(x, w3, acc);
+  return f32_to_bf16_bits(acc * (1.0f / (1.0f + __expf(-acc))));
+}
+
+// Sum of one value per thread over a 128-thread row held by two consecutive
+// wavefronts (waves 2r, 2r+1): xor butterfly in each wave, then wave 2r's
+// part + wave 2r+1's part.  Every thread of the block must call it (it holds
+// a barrier); part needs one float per wave.
+__device__ __forceinline__ float sum128(float v, float *part) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) part[wave] = v;
+  __syncthreads();
+  const int w0 = wave & ~1;
+  return part[w0] + part[w0 + 1];
+}
+
+// softplus(x) = max(x, 0) + log(1 + exp(-|x|)) (gdn_qk_norm_gates.py:90-93)
+__device__ __forceinline__ float softplus(float x) {
+  return fmaxf(x, 0.f) + __logf(1.0f + __expf(-fabsf(x)));
+}
+// beta = sigmoid(b); g = -exp(a_log) * softplus(a + dt_bias)
+__device__ __forceinline__ void gdn_gates(float a, float b, float a_log, float dt_bias,
+                                          float &beta, float &g) {
+  beta = 1.0f / (1.0f + __expf(-b));
+  g = -__expf(a_log) * softplus(a + dt_bias);
+}
+// z * sigmoid(z) with the two-sided form of gdn_gated_rmsnorm.py:56-62
+__device__ __forceinline__ float silu_gate(float z) {
+  const float e = __expf(-fabsf(z));
+  const float sg = z >= 0.f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+  return z * sg;
+}
+
+// ---- standalone kernels ------------------------------------------------------
+
+// conv4 decode: one thread per (sequence, channel); state [B, 4, C] with the
+// channel innermost, weight [4, C].
+__global__ __launch_bounds__(256) void conv4_decode_kernel(
+    const bf16_t *__restrict__ x, int64_t x_b, int64_t x_c, bf16_t *__restrict__ state,
+    int64_t st_b, int64_t st_k, const bf16_t *__restrict__ w, int64_t w_k,
+    bf16_t *__restrict__ out, int64_t o_b, int64_t o_c, int C) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (c >= C) return;
+  bf16_t *sp = state + b * st_b + c;
+  const bf16_t s1 = sp[st_k], s2 = sp[2 * st_k], s3 = sp[3 * st_k];
+  const bf16_t xv = x[b * x_b + c * x_c];
+  const uint32_t y = conv4_silu(bf16_to_f32(s1), bf16_to_f32(s2), bf16_to_f32(s3),
+                                bf16_to_f32(xv), bf16_to_f32(w[c]), bf16_to_f32(w[w_k + c]),
+                                bf16_to_f32(w[2 * w_k + c]), bf16_to_f32(w[3 * w_k + c]));
+  sp[0] = s1;
+  sp[st_k] = s2;
+  sp[2 * st_k] = s3;
+  sp[3 * st_k] = xv;
+  out[b * o_b + c * o_c] = bf16_t(y);
+}
+
+struct QkNormArgs {
+  const bf16_t *q, *k, *a, *b, *dt_bias;
+  const float *a_log;
+  int64_t q_t, q_h, q_d, k_t, k_h, k_d, a_t, a_h, b_t, b_h;
+  bf16_t *qn, *kn;
+  float *beta, *g;
+  int64_t qn_t, qn_h, kn_t, kn_h;  // contiguous rows
+  int heads;
+  float q_scale;
+};
+
+// One 256-thread block per (token, head): threads 0..127 normalise q's
+// elements, 128..255 k's; thread 0 writes beta and g.
+__global__ __launch_bounds__(256) void gdn_qk_norm_gates_kernel(const QkNormArgs p) {
+  __shared__ float part[4];
+  const int th = blockIdx.x;
+  const int t = th / p.heads, h = th - t * p.heads;
+  const int c = threadIdx.x & 127;
+  const bool is_k = threadIdx.x >= 128;
+  const float x = bf16_to_f32(is_k ? p.k[t * p.k_t + h * p.k_h + c * p.k_d]
+                                   : p.q[t * p.q_t + h * p.q_h + c * p.q_d]);
+  const float ss = sum128(x * x, part);
+  const float r = rsqrtf(ss + 1e-6f);
+  if (is_k)
+    p.kn[t * p.kn_t + h * p.kn_h + c] = bf16_t(f32_to_bf16_bits(x * r));
+  else
+    p.qn[t * p.qn_t + h * p.qn_h + c] = bf16_t(f32_to_bf16_bits((x * r) * p.q_scale));
+  if (threadIdx.x == 0) {
+    float beta, g;
+    gdn_gates(bf16_to_f32(p.a[t * p.a_t + h * p.a_h]), bf16_to_f32(p.b[t * p.b_t + h * p.b_h]),
+              p.a_log[h], bf16_to_f32(p.dt_bias[h]), beta, g);
+    p.beta[th] = beta;
+    p.g[th] = g;
+  }
+}
+
+// Gated RMSNorm: one 128-thread block per (token, head), D = 128.
+__global__ __launch_bounds__(128) void gdn_gated_rmsnorm_kernel(
+    const bf16_t *__restrict__ x, int64_t x_t, int64_t x_h, int64_t x_d,
+    const bf16_t *__restrict__ z, int64_t z_t, int64_t z_h, int64_t z_d,
+    const float *__restrict__ w, bf16_t *__restrict__ out, int heads) {
+  __shared__ float part[2];
+  const int th = blockIdx.x;
+  const int t = th / heads, h = th - t * heads;
+  const int c = threadIdx.x;
+  const float xv = bf16_to_f32(x[t * x_t + h * x_h + c * x_d]);
+  const float zv = bf16_to_f32(z[t * z_t + h * z_h + c * z_d]);
+  const float ss = sum128(xv * xv, part);
+  const float inv = rsqrtf(ss / float(kDK) + 1e-6f);
+  out[int64_t(th) * kDK + c] = bf16_t(f32_to_bf16_bits(((xv * inv) * w[c]) * silu_gate(zv)));
+}
+
+// ---- the fused decode block -----------------------------------------------------
+
+struct BlockArgs {
+  const bf16_t *fused;  // [B, 3*H*D + H*D + 2*H]: q|k|v conv inputs, z, a, b
+  int64_t f_b;
+  bf16_t *conv_state;   // [B, 4, 3*H*D]
+  int64_t cs_b, cs_k;
+  const bf16_t *conv_w; // [4, 3*H*D]
+  int64_t cw_k;
+  const float *a_log;
+  const bf16_t *dt_bias;
+  const float *norm_w;
+  float *state;         // [B, H, D, D]
+  int64_t s_b, s_h, s_k;
+  bf16_t *out;          // [B, H*D]
+  int64_t o_b;
+  int heads;
+  float q_scale;
+};
+
+// One 512-thread workgroup per (sequence, head).  The state loads are issued
+// first and land while the conv, norms and gates run:
+//   1. threads 0..383: conv4 + SiLU of the head's q, k, v channels (state
+//      shifted in place); the results go to LDS as bf16 values;
+//   2. waves 0-1 / 2-3: q / k L2 norm (sum128, as the standalone kernel);
+//   3. every wave: one recurrence step on its 16 value columns (gdn_step);
+//   4. waves 0-1: gated RMSNorm of the bf16 step output with z.
+__global__ __launch_bounds__(512) void gdn_decode_block_kernel(const BlockArgs p) {
+  __shared__ float y_lds[3 * kDK];  // conv outputs (bf16 values): q | k | v
+  __shared__ float qk_lds[2 * kDK]; // normalised q | k (bf16 values)
+  __shared__ float core[kDK];       // recurrence output (bf16 values)
+  __shared__ float part[8];
+  const int bh = blockIdx.x;
+  const int b = bh / p.heads, h = bh - b * p.heads;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int kg = lane & 15, cg = lane >> 4;
+  const int col = wave * kWaveCols + cg * kCols;
+  const int HD = p.heads * kDK;
+
+  float *sp = p.state + b * p.s_b + h * p.s_h + int64_t(kg * kRows) * p.s_k + col;
+  float s[kRows][kCols];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const float4 x = *reinterpret_cast<const float4 *>(sp + i * p.s_k);
+    s[i][0] = x.x;
+    s[i][1] = x.y;
+    s[i][2] = x.z;
+    s[i][3] = x.w;
+  }
+  const bf16_t *frow = p.fused + b * p.f_b;
+  float zv = 0.f;
+  if (tid < kDK) zv = bf16_to_f32(frow[3 * HD + h * kDK + tid]);
+
+  // 1. conv4 + SiLU
+  if (tid < 3 * kDK) {
+    const int region = tid >> 7, c = tid & 127;
+    const int ch = region * HD + h * kDK + c;
+    bf16_t *cs = p.conv_state + b * p.cs_b + ch;
+    const bf16_t s1 = cs[p.cs_k], s2 = cs[2 * p.cs_k], s3 = cs[3 * p.cs_k];
+    const bf16_t xv = frow[ch];
+    const bf16_t *w = p.conv_w + ch;
+    const uint32_t y = conv4_silu(bf16_to_f32(s1), bf16_to_f32(s2), bf16_to_f32(s3),
+                                  bf16_to_f32(xv), bf16_to_f32(w[0]), bf16_to_f32(w[p.cw_k]),
+                                  bf16_to_f32(w[2 * p.cw_k]), bf16_to_f32(w[3 * p.cw_k]));
+    cs[0] = s1;
+    cs[p.cs_k] = s2;
+    cs[2 * p.cs_k] = s3;
+    cs[3 * p.cs_k] = xv;
+    y_lds[tid] = bf16_to_f32(bf16_t(y));
+  }
+  float beta, g;
+  gdn_gates(bf16_to_f32(frow[4 * HD + h]), bf16_to_f32(frow[4 * HD + p.heads + h]), p.a_log[h],
+            bf16_to_f32(p.dt_bias[h]), beta, g);
+  __syncthreads();
+
+  // 2. q / k L2 norm: waves 0-1 hold q, waves 2-3 k (threads 256.. add zeros)
+  {
+    const float x = tid < 2 * kDK ? y_lds[tid] : 0.f;
+    const float ss = sum128(x * x, part);
+    const float r = rsqrtf(ss + 1e-6f);
+    if (tid < kDK)
+      qk_lds[tid] = bf16_to_f32(bf16_t(f32_to_bf16_bits((x * r) * p.q_scale)));
+    else if (tid < 2 * kDK)
+      qk_lds[tid] = bf16_to_f32(bf16_t(f32_to_bf16_bits(x * r)));
+  }
+  __syncthreads();
+
+  // 3. recurrence step
+  TokenIn in;
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    in.q[i] = qk_lds[kg * kRows + i];
+    in.k[i] = qk_lds[kDK + kg * kRows + i];
+  }
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) in.v[j] = y_lds[2 * kDK + col + j];
+  in.g = g;
+  in.beta = beta;
+  float o[kCols];
+  gdn_step(s, in, o);
+#pragma unroll
+  for (int i = 0; i < kRows; ++i)
+    *reinterpret_cast<float4 *>(sp + i * p.s_k) = make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
+  if (kg == 0) {
+#pragma unroll
+    for (int j = 0; j < kCols; ++j) core[col + j] = bf16_to_f32(bf16_t(f32_to_bf16_bits(o[j])));
+  }
+  __syncthreads();
+
+  // 4. gated RMSNorm (waves 0-1; the others add zeros to their own pairs)
+  {
+    const float x = tid < kDK ? core[tid] : 0.f;
+    const float ss = sum128(x * x, part + 0);
+    if (tid < kDK) {
+      const float inv = rsqrtf(ss / float(kDK) + 1e-6f);
+      p.out[b * p.o_b + h * kDK + tid] =
+          bf16_t(f32_to_bf16_bits(((x * inv) * p.norm_w[tid]) * silu_gate(zv)));
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int wy_depthwise_causal_conv4_decode(const void *x, const int64_t *x_strides,
+                                                void *state, const int64_t *state_strides,
+                                                const void *weight, const int64_t *w_strides,
+                                                void *out, const int64_t *out_strides, int batch,
+                                                int channels, void *stream) {
+  if (!x || !x_strides || !state || !state_strides || !weight || !w_strides || !out ||
+      !out_strides)
+    return WY_E_NULL;
+  if (batch < 0 || channels < 0) return WY_E_SHAPE;
+  if (state_strides[2] != 1 || w_strides[1] != 1) return WY_E_LAYOUT;
+  if (batch == 0 || channels == 0) return WY_OK;
+  const dim3 grid(unsigned((channels + 255) / 256), unsigned(batch));
+  conv4_decode_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(x), x_strides[0], x_strides[1], static_cast<bf16_t *>(state),
+      state_strides[0], state_strides[1], static_cast<const bf16_t *>(weight), w_strides[0],
+      static_cast<bf16_t *>(out), out_strides[0], out_strides[1], channels);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_gdn_qk_norm_gates(const void *q, const int64_t *q_strides, const void *k,
+                                    const int64_t *k_strides, const void *a,
+                                    const int64_t *a_strides, const void *b,
+                                    const int64_t *b_strides, const float *a_log,
+                                    const void *dt_bias, void *q_norm, void *k_norm, float *beta,
+                                    float *g, int tokens, int num_heads, int head_dim,
+                                    void *stream) {
+  if (!q || !q_strides || !k || !k_strides || !a || !a_strides || !b || !b_strides || !a_log ||
+      !dt_bias || !q_norm || !k_norm || !beta || !g)
+    return WY_E_NULL;
+  if (tokens < 0 || num_heads <= 0 || head_dim <= 0) return WY_E_SHAPE;
+  if (head_dim != kDK) return WY_E_UNSUPPORTED;
+  if (tokens == 0) return WY_OK;
+  if (int64_t(tokens) * num_heads > 0x7fffffff) return WY_E_SHAPE;
+  QkNormArgs p{};
+  p.q = static_cast<const bf16_t *>(q);
+  p.k = static_cast<const bf16_t *>(k);
+  p.a = static_cast<const bf16_t *>(a);
+  p.b = static_cast<const bf16_t *>(b);
+  p.dt_bias = static_cast<const bf16_t *>(dt_bias);
+  p.a_log = a_log;
+  p.q_t = q_strides[0]; p.q_h = q_strides[1]; p.q_d = q_strides[2];
+  p.k_t = k_strides[0]; p.k_h = k_strides[1]; p.k_d = k_strides[2];
+  p.a_t = a_strides[0]; p.a_h = a_strides[1];
+  p.b_t = b_strides[0]; p.b_h = b_strides[1];
+  p.qn = static_cast<bf16_t *>(q_norm);
+  p.kn = static_cast<bf16_t *>(k_norm);
+  p.qn_t = p.kn_t = int64_t(num_heads) * kDK;
+  p.qn_h = p.kn_h = kDK;
+  p.beta = beta;
+  p.g = g;
+  p.heads = num_heads;
+  p.q_scale = float(1.0 / sqrt(double(head_dim)));
+  gdn_qk_norm_gates_kernel<<<unsigned(tokens * num_heads), 256, 0,
+                             static_cast<hipStream_t>(stream)>>>(p);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_gdn_gated_rmsnorm(const void *x, const int64_t *x_strides, const void *z,
+                                    const int64_t *z_strides, const float *weight, void *out,
+                                    int tokens, int num_heads, int head_dim, void *stream) {
+  if (!x || !x_strides || !z || !z_strides || !weight || !out) return WY_E_NULL;
+  if (tokens < 0 || num_heads <= 0 || head_dim <= 0) return WY_E_SHAPE;
+  if (head_dim != kDK) return WY_E_UNSUPPORTED;
+  if (tokens == 0) return WY_OK;
+  if (int64_t(tokens) * num_heads > 0x7fffffff) return WY_E_SHAPE;
+  gdn_gated_rmsnorm_kernel<<<unsigned(tokens * num_heads), 128, 0,
+                             static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(x), x_strides[0], x_strides[1], x_strides[2],
+      static_cast<const bf16_t *>(z), z_strides[0], z_strides[1], z_strides[2], weight,
+      static_cast<bf16_t *>(out), num_heads);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_gdn_decode_block(const void *fused, int64_t fused_stride0, void *conv_state,
+                                   const int64_t *conv_state_strides, const void *conv_weight,
+                                   int64_t conv_weight_stride0, const float *a_log,
+                                   const void *dt_bias, const float *norm_weight, float *state,
+                                   const int64_t *state_strides, void *out, int64_t out_stride0,
+                                   int batch, int num_heads, int head_dim, void *stream) {
+  if (!fused || !conv_state || !conv_state_strides || !conv_weight || !a_log || !dt_bias ||
+      !norm_weight || !state || !state_strides || !out)
+    return WY_E_NULL;
+  if (batch < 0 || num_heads <= 0 || head_dim <= 0) return WY_E_SHAPE;
+  if (head_dim != kDK) return WY_E_UNSUPPORTED;
+  if (conv_state_strides[2] != 1 || state_strides[3] != 1 || state_strides[2] % 4 ||
+      state_strides[1] % 4 || state_strides[0] % 4 || !wyh::aligned16(state))
+    return WY_E_LAYOUT;
+  if (batch == 0) return WY_OK;
+  BlockArgs p{};
+  p.fused = static_cast<const bf16_t *>(fused);
+  p.f_b = fused_stride0;
+  p.conv_state = static_cast<bf16_t *>(conv_state);
+  p.cs_b = conv_state_strides[0];
+  p.cs_k = conv_state_strides[1];
+  p.conv_w = static_cast<const bf16_t *>(conv_weight);
+  p.cw_k = conv_weight_stride0;
+  p.a_log = a_log;
+  p.dt_bias = static_cast<const bf16_t *>(dt_bias);
+  p.norm_w = norm_weight;
+  p.state = state;
+  p.s_b = state_strides[0];
+  p.s_h = state_strides[1];
+  p.s_k = state_strides[2];
+  p.out = static_cast<bf16_t *>(out);
+  p.o_b = out_stride0;
+  p.heads = num_heads;
+  p.q_scale = float(1.0 / sqrt(double(head_dim)));
+  gdn_decode_block_kernel<<<unsigned(batch * num_heads), 512, 0,
+                            static_cast<hipStream_t>(stream)>>>(p);
+  return wyh::launch_status();
+}

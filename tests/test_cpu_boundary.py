@@ -101,6 +101,39 @@ def test_null_and_unsupported_arguments_are_rejected(pkg):
     assert lib.wy_gemm_2d(dummy, s2, dummy, s2, dummy, s2, 0, 8, 256, None, 0, None) == 0  # empty
 
 
+def test_gdn_entry_points_reject_before_launch(pkg):
+    lib = pkg._lib.load()
+    d = ctypes.c_void_p(256)
+    s3 = (ctypes.c_int64 * 3)(2048, 128, 1)
+    s2 = (ctypes.c_int64 * 2)(16, 1)
+    s4 = (ctypes.c_int64 * 4)(16 * 128 * 128, 128 * 128, 128, 1)
+    base = [d, s3, d, s3, d, s3, d, s2, d, s2, d, s3, d, s4]
+    # key_dim 64 has no kernel
+    assert lib.wy_gdn_recurrent_decode(*base, 2, 16, 64, 128, None) == -4
+    assert lib.wy_gdn_recurrent_prefill_sequential(*base, d, 2, 16, 64, 128, None) == -4
+    # value_dim not a multiple of 128
+    assert lib.wy_gdn_recurrent_decode(*base, 2, 16, 128, 96, None) == -4
+    # NULL cu_seqlens / NULL state
+    assert lib.wy_gdn_recurrent_prefill_sequential(*base, None, 2, 16, 128, 128, None) == -1
+    nul = list(base)
+    nul[12] = None
+    assert lib.wy_gdn_recurrent_decode(*nul, 2, 16, 128, 128, None) == -1
+    # state with a non-unit inner stride
+    bad = list(base)
+    bad[13] = (ctypes.c_int64 * 4)(16 * 128 * 128, 128 * 128, 128, 2)
+    assert lib.wy_gdn_recurrent_decode(*bad, 2, 16, 128, 128, None) == -3
+    assert lib.wy_gdn_qk_norm_gates(d, s3, d, s3, d, s2, d, s2, d, d, d, d, d, d, 4, 16, 64,
+                                    None) == -4
+    assert lib.wy_gdn_gated_rmsnorm(d, s3, d, s3, d, d, 4, 16, 256, None) == -4
+    cs = (ctypes.c_int64 * 3)(4 * 6144, 6144, 1)
+    assert lib.wy_gdn_decode_block(d, 8224, d, cs, d, 6144, d, d, d, d, s4, d, 2048, 2, 16, 64,
+                                   None) == -4
+    assert lib.wy_gdn_decode_block(None, 8224, d, cs, d, 6144, d, d, d, d, s4, d, 2048, 2, 16,
+                                   128, None) == -1
+    assert lib.wy_depthwise_causal_conv4_decode(d, s2, d, (ctypes.c_int64 * 3)(4, 1, 2), d, s2,
+                                                d, s2, 2, 6144, None) == -3
+
+
 def test_gemm_split_workspace_sizes(pkg):
     """Decode o_proj [1024, 2048] at B=32 splits K 4 ways: 16 KiB of counters
     plus 4 * 32 * 1024 fp32 partials; prefill shapes and wide N do not split."""
@@ -136,6 +169,10 @@ def test_op_schemas_match_reference():
         "gdn_recurrent_prefill_sequential": "(Tensor q, Tensor k, Tensor v, Tensor beta, "
                                             "Tensor g, Tensor? cu_seqlens=None) "
                                             "-> (Tensor, Tensor)",
+        "gdn_qk_norm_gates": "(Tensor q, Tensor k, Tensor a, Tensor b, Tensor a_log, "
+                             "Tensor dt_bias) -> (Tensor, Tensor, Tensor, Tensor)",
+        "gdn_gated_rmsnorm": "(Tensor x, Tensor z, Tensor weight) -> Tensor",
+        "depthwise_causal_conv4_decode": "(Tensor x, Tensor(a1!) state, Tensor weight) -> Tensor",
     }
     for name, sig in schemas.items():
         op = getattr(torch.ops.wy_lib, name).default
@@ -145,7 +182,7 @@ def test_op_schemas_match_reference():
         assert args.replace("SymInt", "int") == sig.replace("SymInt", "int"), s
     for name in ("paged_kv_fill_varlen", "paged_gqa_attention_decode_split",
                  "paged_gqa_attention_decode_combine", "partial_rope",
-                 "prefill_attention_block"):
+                 "prefill_attention_block", "gdn_decode_block"):
         assert hasattr(torch.ops.wy_lib, name)
 
 
