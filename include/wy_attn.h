@@ -429,6 +429,76 @@ int wy_gdn_decode_block(const void *fused, int64_t fused_stride0, void *conv_sta
                         void *out, int64_t out_stride0, int batch, int num_heads, int head_dim,
                         void *stream);
 
+/*
+ * Depthwise causal conv (4 taps) + SiLU over a prompt, optionally packed:
+ * out[t, c] = bf16(silu(sum_r w[c, r] * x[t - 3 + r, c])), taps before
+ * seq_start[t] (or before 0 when seq_start is NULL) read as zero.  x, out
+ * [T, C] bf16 (element strides); weight element (c, r) at
+ * c * w_stride_c + r * w_stride_k ([C, 4] or [C, 1, 4]); seq_start [T] int32.
+ * Same arithmetic as wy_depthwise_causal_conv4_decode.  One launch.
+ * Replaces wy_lib::depthwise_causal_conv4_prefill
+ *   (triton_kernels/depthwise_causal_conv4_prefill.py:104-176, kernel :23-92).
+ */
+int wy_depthwise_causal_conv4_prefill(const void *x, const int64_t *x_strides,
+                                      const void *weight, int64_t w_stride_c,
+                                      int64_t w_stride_k, void *out, const int64_t *out_strides,
+                                      const int32_t *seq_start, int tokens, int channels,
+                                      void *stream);
+
+/*
+ * Decode conv states after a packed prefill: state[b, r, :] = x[end_b - 4 + r, :]
+ * (end_b = cu_seqlens[b+1]), zero where that row lies before cu_seqlens[b].
+ * state [B, 4, C] bf16 (unit channel stride), x [T, C] bf16 (unit channel
+ * stride).  Replaces wy_lib::conv_state_from_packed_prefill
+ *   (triton_kernels/depthwise_causal_conv4_decode.py:332-375, kernel :253-330).
+ */
+int wy_conv_state_from_packed_prefill(void *state, const int64_t *state_strides, const void *x,
+                                      const int64_t *x_strides, const int32_t *cu_seqlens,
+                                      int batch, int channels, void *stream);
+
+/*
+ * Token embedding gather: out[t, :] = weight[input_ids[t], :] (bf16 rows of
+ * d_model, d_model % 8 == 0, 16-byte aligned rows); input_ids [T] int32 or
+ * int64 (ids_is_int64).  Replaces wy_lib::embedding_gather
+ *   (triton_kernels/embedding_gather.py:62-104, kernel :20-50).
+ */
+int wy_embedding_gather(const void *input_ids, int ids_is_int64, const void *weight,
+                        int64_t weight_row_stride, void *out, int64_t out_row_stride, int tokens,
+                        int d_model, void *stream);
+
+/*
+ * out = bf16(x + residual) over n contiguous bf16 elements (16-byte aligned).
+ * Replaces wy_lib::residual_add (triton_kernels/residual_add.py:23-52, kernel :8-20).
+ */
+int wy_residual_add(const void *x, const void *residual, void *out, int64_t n, void *stream);
+
+/*
+ * SwiGLU: out[m, n] = bf16(up * gate * sigmoid(gate)), fp32 math; gate, up
+ * [rows, cols] bf16 (element strides), out [rows, cols] contiguous.
+ * Replaces wy_lib::swiglu (triton_kernels/swiglu.py:72-111, kernel :22-60).
+ */
+int wy_swiglu(const void *gate, const int64_t *gate_strides, const void *up,
+              const int64_t *up_strides, void *out, int rows, int cols, void *stream);
+
+/*
+ * LM head fused with the vocabulary argmax: token_ids[m] = argmax_v
+ * sum_k hidden[m, k] * weight[v, k] (fp32 sums, the first index on ties),
+ * logits never written.  hidden [rows, hidden_size] bf16 (rows <= 64),
+ * weight [vocab, hidden_size] bf16, 16-byte aligned rows; hidden_size a
+ * multiple of 256; token_ids [rows] int64.  workspace: at least
+ * wy_lm_head_argmax_workspace_bytes(rows, hidden_size, vocab) bytes,
+ * 8-byte aligned, no initial contents.  Two launches.
+ * Replaces wy_lib::lm_head_argmax (triton_kernels/vocab_argmax.py:137-224,
+ * kernels :29-135).
+ */
+int wy_lm_head_argmax(const void *hidden, int64_t hidden_row_stride, const void *weight,
+                      int64_t weight_row_stride, int64_t *token_ids, int rows, int hidden_size,
+                      int vocab, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes wy_lm_head_argmax needs (per-workgroup partial keys).  No
+ * counterpart in the reference (its op allocates the partials itself). */
+int64_t wy_lm_head_argmax_workspace_bytes(int rows, int hidden_size, int vocab);
+
 #ifdef __cplusplus
 }
 #endif

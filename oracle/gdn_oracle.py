@@ -28,6 +28,8 @@ PINNED = {
     "conv4_decode": "direct 4-tap formula on a shifted window; decode chain == causal "
                     "conv over the whole sequence (torch conv1d, padding 3)",
     "gdn_gated_rmsnorm": "pure-Python brute force; z=0 -> 0; scale invariance of x",
+    "conv4_prefill": "torch conv1d (padding 3) per sequence of a packed batch",
+    "conv_state_from_packed": "direct row selection by index (last 4 rows, zero on top)",
 }
 
 
@@ -97,6 +99,36 @@ def conv4_decode(x, state, weight):
     acc = (new.float() * weight.float()[None]).sum(1)
     y = acc * torch.sigmoid(acc)
     return y.to(torch.bfloat16), new
+
+
+def conv4_prefill(x, weight_dc, seq_start=None):
+    """depthwise_causal_conv4_prefill.py:23-92: out[t, c] = bf16(silu(sum_r
+    w[c, r] x[t-3+r, c])) with taps before seq_start[t] (or 0) read as zero.
+    x ``[T, D]``, weight ``[D, 4]``."""
+    T, D = x.shape
+    xf, wf = x.float(), weight_dc.float()
+    lo = torch.zeros(T, dtype=torch.long) if seq_start is None else seq_start.long()
+    acc = torch.zeros(T, D)
+    for r in range(4):
+        src = torch.arange(T) - 3 + r
+        ok = (src >= lo) & (src >= 0)
+        tap = torch.where(ok[:, None], xf[src.clamp(min=0)], torch.zeros(()))
+        acc = acc + tap * wf[:, r][None, :]
+    return (acc * torch.sigmoid(acc)).to(torch.bfloat16)
+
+
+def conv_state_from_packed(x, cu_seqlens):
+    """depthwise_causal_conv4_decode.py:253-330: state[b, r] = x[end_b - 4 + r]
+    or zero before the sequence start."""
+    cu = [int(c) for c in cu_seqlens]
+    B, D = len(cu) - 1, x.shape[1]
+    st = torch.zeros(B, 4, D, dtype=x.dtype)
+    for b in range(B):
+        for r in range(4):
+            t = cu[b + 1] - 4 + r
+            if t >= cu[b]:
+                st[b, r] = x[t]
+    return st
 
 
 def gdn_gated_rmsnorm(x, z, weight):

@@ -21,6 +21,8 @@ from .attention import (
 )
 from .attention_gate_pack import attention_gate_pack
 from .cache import AttnCaches, allocate_attn_caches
+from .decoder import DecodeModel, DecoderConfig, GraphedDecoder, random_weights
+from .embedding_gather import call_embedding_gather_triton, embedding_gather
 from .gemm_2d import call_gemm_2d_triton, gemm_2d
 from .gqa_attention_decode_paged import (
     MAX_SPLITS,
@@ -41,8 +43,14 @@ from .gqa_attention_decode_paged import (
 )
 from .depthwise_causal_conv4_decode import (
     call_depthwise_causal_conv4_decode_triton,
+    conv_state_from_packed_prefill,
     conv_state_from_prefill,
     depthwise_causal_conv4_decode,
+)
+from .depthwise_causal_conv4_prefill import (
+    build_seq_start,
+    call_depthwise_causal_conv4_prefill_triton,
+    depthwise_causal_conv4_prefill,
 )
 from .gdn_gated_rmsnorm import call_gdn_gated_rmsnorm_triton, gdn_gated_rmsnorm
 from .gdn_mixer import gdn_decode_block, gdn_decode_ops
@@ -57,6 +65,9 @@ from .gqa_attention_varlen_causal import build_cu_seqlens, gqa_attention_varlen_
 from .paging import PagePool, SequencePages, allocate_block_table
 from .partial_rope import partial_rope, rope_inv_freq
 from .qwen_rmsnorm import call_qwen_rmsnorm_triton, qwen_rmsnorm
+from .residual_add import call_residual_add_triton, residual_add
+from .swiglu import call_swiglu_triton, swiglu
+from .vocab_argmax import call_lm_head_argmax_triton, lm_head_argmax
 
 
 def install_as_triton_kernels() -> None:
@@ -74,6 +85,11 @@ def install_as_triton_kernels() -> None:
         ("triton_kernels.gdn_qk_norm_gates", "gdn_qk_norm_gates"),
         ("triton_kernels.gdn_gated_rmsnorm", "gdn_gated_rmsnorm"),
         ("triton_kernels.depthwise_causal_conv4_decode", "depthwise_causal_conv4_decode"),
+        ("triton_kernels.depthwise_causal_conv4_prefill", "depthwise_causal_conv4_prefill"),
+        ("triton_kernels.embedding_gather", "embedding_gather"),
+        ("triton_kernels.residual_add", "residual_add"),
+        ("triton_kernels.swiglu", "swiglu"),
+        ("triton_kernels.vocab_argmax", "vocab_argmax"),
         ("engine.paging", "paging"),
     ):
         # the submodule itself: several share their name with the op they define

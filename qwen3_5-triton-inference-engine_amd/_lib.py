@@ -65,6 +65,13 @@ _SIGNATURES = {
     "wy_gdn_gated_rmsnorm": [_vp, _c_i64p, _vp, _c_i64p, _vp, _vp, _i, _i, _i, _vp],
     "wy_gdn_decode_block": [_vp, _i64, _vp, _c_i64p, _vp, _i64, _vp, _vp, _vp, _vp, _c_i64p,
                             _vp, _i64, _i, _i, _i, _vp],
+    "wy_depthwise_causal_conv4_prefill": [_vp, _c_i64p, _vp, _i64, _i64, _vp, _c_i64p, _vp,
+                                          _i, _i, _vp],
+    "wy_conv_state_from_packed_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _vp],
+    "wy_embedding_gather": [_vp, _i, _vp, _i64, _vp, _i64, _i, _i, _vp],
+    "wy_residual_add": [_vp, _vp, _vp, _i64, _vp],
+    "wy_swiglu": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _vp],
+    "wy_lm_head_argmax": [_vp, _i64, _vp, _i64, _vp, _i, _i, _i, _vp, _i64, _vp],
 }
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)
@@ -91,7 +98,8 @@ def load() -> ctypes.CDLL:
     lib.wy_status_string.restype = ctypes.c_char_p
     lib.wy_build_info.argtypes = []
     lib.wy_build_info.restype = ctypes.c_char_p
-    for fn in (lib.wy_varlen_causal_prefill_workspace_bytes, lib.wy_gemm_2d_workspace_bytes):
+    for fn in (lib.wy_varlen_causal_prefill_workspace_bytes, lib.wy_gemm_2d_workspace_bytes,
+               lib.wy_lm_head_argmax_workspace_bytes):
         fn.argtypes = [_i, _i, _i]
         fn.restype = ctypes.c_int64
     _lib = lib

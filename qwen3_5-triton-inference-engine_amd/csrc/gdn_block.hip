@@ -134,6 +134,60 @@ __global__ __launch_bounds__(128) void gdn_gated_rmsnorm_kernel(
   out[int64_t(th) * kDK + c] = bf16_t(f32_to_bf16_bits(((xv * inv) * w[c]) * silu_gate(zv)));
 }
 
+// conv4 prefill (+ SiLU) over a packed batch: one thread per channel walks
+// kConvRun consecutive tokens with the 4-tap window in registers, so each
+// input row is read once per run (plus 3 rows of halo).  Token t's taps
+// below seq_start[t] read as zero (no look-back across sequences).  Same
+// arithmetic as the decode step (conv4_silu), so prefill and decode agree bit
+// for bit on the same window.
+constexpr int kConvRun = 16;
+
+__global__ __launch_bounds__(256) void conv4_prefill_kernel(
+    const bf16_t *__restrict__ x, int64_t x_t, int64_t x_c, const bf16_t *__restrict__ w,
+    int64_t w_c, int64_t w_k, bf16_t *__restrict__ out, int64_t o_t, int64_t o_c,
+    const int32_t *__restrict__ seq_start, int T, int C) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int t0 = blockIdx.y * kConvRun;
+  if (c >= C) return;
+  const float w0 = bf16_to_f32(w[c * w_c]), w1 = bf16_to_f32(w[c * w_c + w_k]);
+  const float w2 = bf16_to_f32(w[c * w_c + 2 * w_k]), w3 = bf16_to_f32(w[c * w_c + 3 * w_k]);
+  const bf16_t *xc = x + c * x_c;
+  // window: win[j] = x[t0 - 3 + j]
+  float win[kConvRun + 3];
+#pragma unroll
+  for (int j = 0; j < kConvRun + 3; ++j) {
+    const int t = t0 - 3 + j;
+    win[j] = (t >= 0 && t < T) ? bf16_to_f32(xc[int64_t(t) * x_t]) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < kConvRun; ++i) {
+    const int t = t0 + i;
+    if (t >= T) break;
+    const int lo = seq_start ? seq_start[t] : 0;
+    const float a0 = t - 3 >= lo ? win[i] : 0.f;
+    const float a1 = t - 2 >= lo ? win[i + 1] : 0.f;
+    const float a2 = t - 1 >= lo ? win[i + 2] : 0.f;
+    out[int64_t(t) * o_t + c * o_c] = bf16_t(conv4_silu(a0, a1, a2, win[i + 3], w0, w1, w2, w3));
+  }
+}
+
+// conv state after a packed prefill: state[b, r, :] = x[end_b - 4 + r, :],
+// zero where that row precedes the sequence's start.  Every row is written
+// (zeros included), so a reused cache keeps nothing of its previous contents.
+__global__ __launch_bounds__(256) void conv_state_pack_kernel(
+    const bf16_t *__restrict__ x, int64_t x_t, bf16_t *__restrict__ state, int64_t st_b,
+    int64_t st_k, const int32_t *__restrict__ cu_seqlens, int C) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (c >= C) return;
+  const int start = cu_seqlens[b], end = cu_seqlens[b + 1];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = end - 4 + r;
+    state[b * st_b + r * st_k + c] = t >= start ? x[int64_t(t) * x_t + c] : bf16_t(0);
+  }
+}
+
 // ---- the fused decode block -----------------------------------------------------
 
 struct BlockArgs {
@@ -367,5 +421,37 @@ extern "C" int wy_gdn_decode_block(const void *fused, int64_t fused_stride0, voi
   p.q_scale = float(1.0 / sqrt(double(head_dim)));
   gdn_decode_block_kernel<<<unsigned(batch * num_heads), 512, 0,
                             static_cast<hipStream_t>(stream)>>>(p);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_depthwise_causal_conv4_prefill(const void *x, const int64_t *x_strides,
+                                                 const void *weight, int64_t w_stride_c,
+                                                 int64_t w_stride_k, void *out,
+                                                 const int64_t *out_strides,
+                                                 const int32_t *seq_start, int tokens,
+                                                 int channels, void *stream) {
+  if (!x || !x_strides || !weight || !out || !out_strides) return WY_E_NULL;
+  if (tokens < 0 || channels < 0) return WY_E_SHAPE;
+  if (tokens == 0 || channels == 0) return WY_OK;
+  const dim3 grid(unsigned((channels + 255) / 256), unsigned((tokens + kConvRun - 1) / kConvRun));
+  conv4_prefill_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(x), x_strides[0], x_strides[1],
+      static_cast<const bf16_t *>(weight), w_stride_c, w_stride_k, static_cast<bf16_t *>(out),
+      out_strides[0], out_strides[1], seq_start, tokens, channels);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_conv_state_from_packed_prefill(void *state, const int64_t *state_strides,
+                                                 const void *x, const int64_t *x_strides,
+                                                 const int32_t *cu_seqlens, int batch,
+                                                 int channels, void *stream) {
+  if (!state || !state_strides || !x || !x_strides || !cu_seqlens) return WY_E_NULL;
+  if (batch < 0 || channels < 0) return WY_E_SHAPE;
+  if (state_strides[2] != 1 || x_strides[1] != 1) return WY_E_LAYOUT;
+  if (batch == 0 || channels == 0) return WY_OK;
+  const dim3 grid(unsigned((channels + 255) / 256), unsigned(batch));
+  conv_state_pack_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(x), x_strides[0], static_cast<bf16_t *>(state),
+      state_strides[0], state_strides[1], cu_seqlens, channels);
   return wyh::launch_status();
 }

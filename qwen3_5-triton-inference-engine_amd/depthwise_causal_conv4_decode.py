@@ -67,3 +67,35 @@ def conv_state_from_prefill(x: torch.Tensor) -> torch.Tensor:
     take = min(token_num, CONV_KERNEL_SIZE)
     state[CONV_KERNEL_SIZE - take:] = x[-take:]
     return state
+
+
+@torch.library.custom_op("wy_lib::conv_state_from_packed_prefill", mutates_args=("state",),
+                         device_types="cuda")
+def conv_state_from_packed_prefill(
+    state: torch.Tensor,
+    x: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+) -> None:
+    """Batched ``conv_state_from_prefill`` written straight into the cache:
+    ``state[b]`` = the last four rows of sequence b in the packed ``x [T, D]``,
+    zero rows on top for sequences shorter than four."""
+    total_tokens, hidden_dim = x.shape
+    batch = cu_seqlens.shape[0] - 1
+    assert state.shape == (batch, CONV_KERNEL_SIZE, hidden_dim), (
+        f"state {tuple(state.shape)} does not match (B={batch}, K={CONV_KERNEL_SIZE}, "
+        f"D={hidden_dim})"
+    )
+    assert state.dtype == x.dtype
+    assert cu_seqlens.dtype == torch.int32 and cu_seqlens.ndim == 1
+    assert x.stride(1) == 1, "x must have a unit channel stride"
+    assert state.stride(2) == 1
+    _lib.call(
+        "wy_conv_state_from_packed_prefill", _lib.ptr(state), _lib.strides(state), _lib.ptr(x),
+        _lib.strides(x), _lib.ptr(cu_seqlens.contiguous()), batch, hidden_dim,
+        _lib.stream(x.device),
+    )
+
+
+@conv_state_from_packed_prefill.register_fake
+def _conv_state_from_packed_prefill_fake(state, x, cu_seqlens) -> None:
+    return None

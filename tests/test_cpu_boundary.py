@@ -173,6 +173,9 @@ def test_op_schemas_match_reference():
                              "Tensor dt_bias) -> (Tensor, Tensor, Tensor, Tensor)",
         "gdn_gated_rmsnorm": "(Tensor x, Tensor z, Tensor weight) -> Tensor",
         "depthwise_causal_conv4_decode": "(Tensor x, Tensor(a1!) state, Tensor weight) -> Tensor",
+        "depthwise_causal_conv4_prefill": "(Tensor x, Tensor weight, Tensor? seq_start=None) "
+                                          "-> Tensor",
+        "conv_state_from_packed_prefill": "(Tensor(a0!) state, Tensor x, Tensor cu_seqlens) -> ()",
     }
     for name, sig in schemas.items():
         op = getattr(torch.ops.wy_lib, name).default

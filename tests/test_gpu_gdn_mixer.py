@@ -159,3 +159,32 @@ def test_decode_block_chain_and_graph_replays(pkg, dev):
         torch.cuda.synchronize()
         assert torch.equal(out, eager[i]), f"replay {i}"
     assert torch.equal(cs, cs_e) and torch.equal(st, st_e)
+
+
+@pytest.mark.parametrize("lengths", [[5], [3, 6, 2], [1, 1, 40], [100, 17]])
+def test_conv4_prefill_vs_oracle_and_decode_chain(pkg, dev, lengths):
+    """Packed prefill conv vs the oracle; each sequence's outputs equal the
+    decode step chain from a zero state bit for bit; the packed conv-state
+    write equals the last four rows of each sequence (zero-padded on top)."""
+    say(f"conv4 prefill lengths={lengths}")
+    gen = torch.Generator().manual_seed(sum(lengths))
+    T, Cs = sum(lengths), 640
+    x = torch.randn(T, Cs, generator=gen).to(torch.bfloat16)
+    w = torch.randn(Cs, 1, 4, generator=gen).to(torch.bfloat16)
+    cu = torch.tensor([0] + torch.tensor(lengths).cumsum(0).tolist(), dtype=torch.int32)
+    starts = torch.repeat_interleave(cu[:-1], torch.tensor(lengths))
+    ref = go.conv4_prefill(x, w[:, 0], starts)
+    xd, wd = x.to(dev), w.to(dev)
+    out = pkg.depthwise_causal_conv4_prefill(xd, wd, starts.to(dev))
+    torch.cuda.synchronize()
+    close(out, ref)
+    w_dec = w[:, 0].T.contiguous().to(dev)  # [4, C] decode layout
+    for b, n in enumerate(lengths):
+        st = torch.zeros(1, 4, Cs, dtype=torch.bfloat16, device=dev)
+        for t in range(int(cu[b]), int(cu[b + 1])):
+            y = pkg.depthwise_causal_conv4_decode(xd[t:t + 1], st, w_dec)
+            assert torch.equal(y[0], out[t]), (b, t)
+    state = torch.full((len(lengths), 4, Cs), 7.0, dtype=torch.bfloat16, device=dev)
+    pkg.conv_state_from_packed_prefill(state, xd, cu.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(state.cpu(), go.conv_state_from_packed(x, cu))

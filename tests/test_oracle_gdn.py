@@ -178,3 +178,29 @@ def test_gated_rmsnorm_brute_force_and_special_cases():
                        torch.zeros(T, H, D))
     x2 = (x.float() * 4).to(torch.bfloat16)  # power-of-two scale: same output
     assert torch.allclose(go.gdn_gated_rmsnorm(x2, z, w).float(), out.float(), atol=1e-2)
+
+
+def test_conv4_prefill_packed_equals_per_sequence_conv1d():
+    gen = torch.Generator().manual_seed(12)
+    lengths, D = [5, 1, 9, 2], 6
+    T = sum(lengths)
+    x = torch.randn(T, D, generator=gen).to(torch.bfloat16)
+    w = torch.randn(D, 4, generator=gen).to(torch.bfloat16)
+    starts = torch.repeat_interleave(torch.tensor([0, 5, 6, 15], dtype=torch.int32),
+                                     torch.tensor(lengths))
+    out = go.conv4_prefill(x, w, starts)
+    s = 0
+    for n in lengths:
+        seg = x[s:s + n].float().T[None]
+        ref = torch.nn.functional.conv1d(seg, w.float()[:, None, :], padding=3, groups=D)
+        ref = torch.nn.functional.silu(ref[0, :, :n]).T
+        assert torch.allclose(out[s:s + n].float(), ref, atol=1e-2, rtol=1e-2)
+        s += n
+
+
+def test_conv_state_from_packed_selects_rows():
+    x = torch.arange(10 * 3, dtype=torch.float32).view(10, 3).to(torch.bfloat16)
+    st = go.conv_state_from_packed(x, torch.tensor([0, 2, 10], dtype=torch.int32))
+    assert torch.equal(st[0, :2], torch.zeros(2, 3, dtype=torch.bfloat16))
+    assert torch.equal(st[0, 2:], x[0:2])
+    assert torch.equal(st[1], x[6:10])
