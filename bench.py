@@ -409,6 +409,10 @@ def main():
     if want("gemm"):
         extra["gemm_2d"] = gemm_bench(pkg, dev)
 
+    # ---- the whole model's decode step as one graph ----------------------------
+    if want("model"):
+        extra["decode_step_full_model"] = decoder_bench(pkg, dev)
+
     # ---- Gated DeltaNet recurrence (the other mixer of the model) -------------
     if want("gdn"):
         extra["gdn"] = gdn_bench(pkg, dev)
@@ -483,6 +487,52 @@ def prefill_path_bench(pkg, dev, lengths, seed):
             "what": "after q/k norm: RoPE q/k + varlen attention + gate pack + K/V page "
                     "scatter; op sequence (reference order, 6 launches) vs the two-launch "
                     "prefill attention block (bit-identical)"}
+
+
+def decoder_bench(pkg, dev):
+    """The whole Qwen3.5 decode step (24 layers: 18 GDN + 6 attention, tied
+    248320-word LM head with argmax) as one HIP graph replay, random weights
+    of the checkpoint's shapes; attention contexts U[128, 2048] (config 2's
+    distribution).  Reported next to the reference's own published decode
+    step times (A100, README-EN.md:69-76)."""
+    from qwen35_amd.decoder import DecodeModel, DecoderConfig, GraphedDecoder, random_weights
+    cfg = DecoderConfig()
+    weights = random_weights(cfg, seed=11, device=dev)
+    ref_ms = {1: 2.010, 32: 4.662}
+    out = {}
+    for B in (1, 32):
+        model = DecodeModel(cfg, weights, batch=B, max_len=2064, device=dev)
+        gen = torch.Generator().manual_seed(2)
+        lens = torch.randint(128, 2049, (B,), generator=gen)
+        model.pos.copy_((lens - 1).to(dev))
+        tok = torch.randint(0, cfg.vocab, (B,), generator=gen).to(dev)
+        g = GraphedDecoder(model, tok)
+        for _ in range(10):
+            g.step()
+        torch.cuda.synchronize()
+        iters = 50
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st.record()
+        for _ in range(iters):
+            g.step()
+        en.record()
+        en.synchronize()
+        ms = st.elapsed_time(en) / iters
+        wbytes = sum(t.numel() * t.element_size() for w in model.layers
+                     for t in (w.gate_up, w.down_proj, w.in_proj, w.out_proj))
+        wbytes += weights[1].numel() * 2
+        sbytes = sum(2 * t.numel() * t.element_size() for t in model.rec_states if t is not None)
+        kvbytes = 6 * int((lens + 10).sum()) * 2048
+        out[f"B={B}"] = {
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B / ms * 1e3, 1),
+            "reference_a100_ms_per_step": ref_ms[B],
+            "speedup_vs_reference_a100": round(ref_ms[B] / ms, 2),
+            "hbm_bytes_per_step": wbytes + sbytes + kvbytes,
+            "GB/s": round((wbytes + sbytes + kvbytes) / ms / 1e6, 1)}
+        log(f"decoder B={B}: {out[f'B={B}']}")
+        del g, model
+        torch.cuda.empty_cache()
+    return out
 
 
 def gdn_bench(pkg, dev):
