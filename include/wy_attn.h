@@ -499,6 +499,35 @@ int wy_lm_head_argmax(const void *hidden, int64_t hidden_row_stride, const void 
  * counterpart in the reference (its op allocates the partials itself). */
 int64_t wy_lm_head_argmax_workspace_bytes(int rows, int hidden_size, int vocab);
 
+/*
+ * wy_gemm_2d with the RMSNorm in the A-operand load: y = bf16(qwen_rmsnorm(t)
+ * @ w^T) with t = bf16(x + residual) (residual may be NULL: t = x) and
+ * qwen_rmsnorm(t) = bf16(t * rsqrt(mean(t^2) + eps) * (1 + norm_weight)),
+ * the same roundings and reduction order as wy_qwen_rmsnorm; when x_out is
+ * not NULL it receives t (the residual stream).  Equals wy_residual_add ->
+ * wy_qwen_rmsnorm -> wy_gemm_2d bit for bit.  M <= 64 (else
+ * WY_E_UNSUPPORTED), K % 256 == 0, rows 16-byte aligned; x_out must not
+ * alias x or residual.  workspace as in wy_gemm_2d.  One launch.
+ * No counterpart in the reference: it fuses residual_add + qwen_rmsnorm +
+ * gemm_2d of the runner's decode step (engine/runner.py:538-562).
+ */
+int wy_gemm_2d_rmsnorm(const void *x, int64_t x_stride0, const void *residual,
+                       int64_t residual_stride0, const void *norm_weight, float eps, void *x_out,
+                       int64_t x_out_stride0, const void *w, int64_t w_stride0, void *y,
+                       int64_t y_stride0, int M, int N, int K, void *workspace,
+                       int64_t workspace_bytes, void *stream);
+
+/*
+ * wy_gemm_2d with SwiGLU in the A-operand load: y = bf16(swiglu(gate, up) @ w^T)
+ * where gate = gate_up[:, 0:K], up = gate_up[:, up_offset:up_offset+K] and
+ * swiglu = bf16(up * gate * sigmoid(gate)) as wy_swiglu.  Equals wy_swiglu ->
+ * wy_gemm_2d bit for bit.  M <= 64.  No counterpart in the reference: it fuses
+ * swiglu + the down projection (engine/runner.py:562-565).
+ */
+int wy_gemm_2d_swiglu(const void *gate_up, int64_t gate_up_stride0, int64_t up_offset,
+                      const void *w, int64_t w_stride0, void *y, int64_t y_stride0, int M, int N,
+                      int K, void *workspace, int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

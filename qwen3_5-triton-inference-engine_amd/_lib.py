@@ -72,6 +72,9 @@ _SIGNATURES = {
     "wy_residual_add": [_vp, _vp, _vp, _i64, _vp],
     "wy_swiglu": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _vp],
     "wy_lm_head_argmax": [_vp, _i64, _vp, _i64, _vp, _i, _i, _i, _vp, _i64, _vp],
+    "wy_gemm_2d_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _f, _vp, _i64, _vp, _i64, _vp, _i64, _i,
+                           _i, _i, _vp, _i64, _vp],
+    "wy_gemm_2d_swiglu": [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i, _i, _i, _vp, _i64, _vp],
 }
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES)

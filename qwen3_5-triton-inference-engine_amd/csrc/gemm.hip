@@ -28,11 +28,56 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kSkinnyMaxM = 64;
 constexpr int kMaxSplit = 4;  // K splits across workgroups (skinny kernel)
 
-template <int kNW, int kMT, int kNT>
+// A-operand prologues of the skinny kernel (kPro):
+//   0: A = x;
+//   1: A = qwen_rmsnorm(x [+ residual]) = bf16(t * rsigma * (1 + w)) with
+//      t = bf16(x + residual) (or x), rsigma from the same lane partition and
+//      reduction order as qwen_rmsnorm_kernel; workgroup (0, 0) also writes t
+//      to xout (the residual stream);
+//   2: A = swiglu(x[:, :K], x[:, up_off:up_off+K]) = bf16(up * gate * sigmoid(gate)).
+// Each equals the standalone kernels followed by the plain GEMM bit for bit.
+struct ProArgs {
+  const bf16_t *res;
+  int64_t res0;
+  const bf16_t *nw;
+  float eps;
+  bf16_t *xout;
+  int64_t xo0;
+  int64_t up_off;
+};
+
+__device__ __forceinline__ u32x4_t add_bf16x8(u32x4_t a, u32x4_t b) {
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(bf16_lo(a[e]) + bf16_lo(b[e]), bf16_hi(a[e]) + bf16_hi(b[e]));
+  return o;
+}
+__device__ __forceinline__ u32x4_t norm_bf16x8(u32x4_t t, float rs, u32x4_t w) {
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(rms_apply(bf16_lo(t[e]), rs, bf16_lo(w[e])),
+                       rms_apply(bf16_hi(t[e]), rs, bf16_hi(w[e])));
+  return o;
+}
+__device__ __forceinline__ float swiglu_f(float g, float u) {
+  return (u * g) * (1.0f / (1.0f + __expf(-g)));
+}
+__device__ __forceinline__ u32x4_t swiglu_bf16x8(u32x4_t g, u32x4_t u) {
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack_bf16x2(swiglu_f(bf16_lo(g[e]), bf16_lo(u[e])),
+                       swiglu_f(bf16_hi(g[e]), bf16_hi(u[e])));
+  return o;
+}
+
+template <int kNW, int kMT, int kNT, int kPro = 0>
 __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, float *__restrict__ part,
-    int32_t *__restrict__ cnt) {
+    int32_t *__restrict__ cnt, const ProArgs pro) {
   // kMT = ceil(M / 16) tiles of 16 rows, kNT tiles of 16 columns per
   // workgroup (each x load feeds kNT MFMAs); every load of a 4-step batch is
   // issued before the first MFMA consumes one, so a wave waits for memory once
@@ -64,6 +109,49 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     xok[mt] = row < M;
     xp[mt] = x + int64_t(xok[mt] ? row : 0) * xs0 + kb + 8 * g;
   }
+  float rsr[kMT];
+  const bf16_t *rp[kMT];
+  const bf16_t *nwp = nullptr;
+  if constexpr (kPro == 1) {
+    // rsigma of every row: 32 lanes per row, lane l summing the 8-element
+    // chunks (32 kk + l) * 8 in order, then the xor tree (rms_rsigma)
+    __shared__ float rs_lds[kSkinnyMaxM];
+    const int l32 = threadIdx.x & 31;
+    const bool write_x = pro.xout && blockIdx.x == 0 && blockIdx.y == 0;
+    for (int row = threadIdx.x >> 5; row < M; row += 2 * kNW) {
+      const bf16_t *hr = x + int64_t(row) * xs0;
+      const bf16_t *rr = pro.res ? pro.res + int64_t(row) * pro.res0 : nullptr;
+      float ss = 0.f;
+      for (int kk = 0; kk < K / 256; ++kk) {
+        const int c = (32 * kk + l32) * 8;
+        u32x4_t t = ld16(hr + c);
+        if (rr) t = add_bf16x8(t, ld16(rr + c));
+        if (write_x) st16(pro.xout + int64_t(row) * pro.xo0 + c, t);
+        ss = rms_acc8(t, ss);
+      }
+      const float rs = rms_rsigma(ss, K, pro.eps);
+      if (l32 == 0) rs_lds[row] = rs;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt) {
+      const int row = mt * 16 + (lane & 15);
+      rsr[mt] = xok[mt] ? rs_lds[row] : 0.f;
+      rp[mt] = pro.res ? pro.res + int64_t(xok[mt] ? row : 0) * pro.res0 + kb + 8 * g : nullptr;
+    }
+    nwp = pro.nw + kb + 8 * g;
+  }
+  // the A operand of rows tile mt at k offset kk (relative to kb + 8 g)
+  auto load_a = [&](int mt, int kk) -> u32x4_t {
+    u32x4_t v = ld16(xp[mt] + kk);
+    if constexpr (kPro == 1) {
+      if (rp[mt]) v = add_bf16x8(v, ld16(rp[mt] + kk));
+      v = norm_bf16x8(v, rsr[mt], ld16(nwp + kk));
+    } else if constexpr (kPro == 2) {
+      v = swiglu_bf16x8(v, ld16(xp[mt] + pro.up_off + kk));
+    }
+    return v;
+  };
   f32x4v_t acc[kMT][kNT];
 #pragma unroll
   for (int mt = 0; mt < kMT; ++mt)
@@ -87,7 +175,7 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xv[mt][j] = ld16(xp[mt] + k + 32 * j);
+      for (int j = 0; j < 4; ++j) xv[mt][j] = load_a(mt, k + 32 * j);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -98,7 +186,7 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) wv[nt] = ld16(wp[nt] + k);
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt) step(wv, ld16(xp[mt] + k), mt);
+    for (int mt = 0; mt < kMT; ++mt) step(wv, load_a(mt, k), mt);
   }
 
   // lane l of tile (mt, nt) holds rows mt*16 + 4(l/16) + i (i = 0..3) of
@@ -316,22 +404,36 @@ struct SkinnyArgs {
   int M, N, K, split;
   float *part;
   int32_t *cnt;
+  ProArgs pro;
 };
 
-template <int kNW, int kMT, int kNT>
+template <int kNW, int kMT, int kNT, int kPro>
 void launch_skinny(const SkinnyArgs &a, hipStream_t st) {
   const dim3 grid(unsigned((a.N + 16 * kNT - 1) / (16 * kNT)), unsigned(a.split));
-  gemm_skinny_kernel<kNW, kMT, kNT><<<grid, 64 * kNW, 0, st>>>(
-      a.x, a.xs0, a.w, a.ws0, a.y, a.ys0, a.M, a.N, a.K, a.part, a.cnt);
+  gemm_skinny_kernel<kNW, kMT, kNT, kPro><<<grid, 64 * kNW, 0, st>>>(
+      a.x, a.xs0, a.w, a.ws0, a.y, a.ys0, a.M, a.N, a.K, a.part, a.cnt, a.pro);
 }
 
-template <int kNW, int kNT>
+template <int kNW, int kNT, int kPro>
 void launch_skinny_m(const SkinnyArgs &a, hipStream_t st) {
   switch ((a.M + 15) / 16) {
-    case 1: launch_skinny<kNW, 1, kNT>(a, st); break;
-    case 2: launch_skinny<kNW, 2, kNT>(a, st); break;
-    case 3: launch_skinny<kNW, 3, kNT>(a, st); break;
-    default: launch_skinny<kNW, 4, kNT>(a, st); break;
+    case 1: launch_skinny<kNW, 1, kNT, kPro>(a, st); break;
+    case 2: launch_skinny<kNW, 2, kNT, kPro>(a, st); break;
+    case 3: launch_skinny<kNW, 3, kNT, kPro>(a, st); break;
+    default: launch_skinny<kNW, 4, kNT, kPro>(a, st); break;
+  }
+}
+
+template <int kPro>
+void launch_skinny_plan(const SkinnyArgs &a, int nt, int nw, hipStream_t st) {
+  if (nt == 1) {
+    if (nw == 4) launch_skinny_m<4, 1, kPro>(a, st);
+    else if (nw == 8) launch_skinny_m<8, 1, kPro>(a, st);
+    else launch_skinny_m<16, 1, kPro>(a, st);
+  } else {
+    if (nw == 4) launch_skinny_m<4, 2, kPro>(a, st);
+    else if (nw == 8) launch_skinny_m<8, 2, kPro>(a, st);
+    else launch_skinny_m<16, 2, kPro>(a, st);
   }
 }
 
@@ -383,6 +485,27 @@ extern "C" int64_t wy_gemm_2d_workspace_bytes(int M, int N, int K) {
   return kSplitPartOffset + int64_t(p.split) * M * N * 4;
 }
 
+// Plan, pick the split-K workspace if one is given, and launch the skinny
+// kernel with prologue `pro` (0 plain, 1 RMSNorm, 2 SwiGLU).
+static int run_skinny(SkinnyArgs a, int pro, void *workspace, int64_t workspace_bytes,
+                      hipStream_t st) {
+  SkinnyPlan p = skinny_plan(a.N, a.K);
+  const int64_t need = wy_gemm_2d_workspace_bytes(a.M, a.N, a.K);
+  if (p.split > 1 && need > 0 && workspace_bytes >= need) {
+    a.split = p.split;
+    a.cnt = static_cast<int32_t *>(workspace);
+    a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + kSplitPartOffset);
+  } else if (p.split > 1) {  // no workspace: one workgroup per column block
+    p.split = 1;
+    p.nw = 4;
+    while (p.nw < 16 && p.blocks * p.nw < 2048 && a.K / (2 * p.nw) >= 128) p.nw *= 2;
+  }
+  if (pro == 1) launch_skinny_plan<1>(a, p.nt, p.nw, st);
+  else if (pro == 2) launch_skinny_plan<2>(a, p.nt, p.nw, st);
+  else launch_skinny_plan<0>(a, p.nt, p.nw, st);
+  return wyh::launch_status();
+}
+
 extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w,
                           const int64_t *w_strides, void *y, const int64_t *y_strides, int M,
                           int N, int K, void *workspace, int64_t workspace_bytes,
@@ -402,32 +525,62 @@ extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w
   const bf16_t *wb = static_cast<const bf16_t *>(w);
   bf16_t *yb = static_cast<bf16_t *>(y);
   if (M <= kSkinnyMaxM) {
-    SkinnyPlan p = skinny_plan(N, K);
     SkinnyArgs a{xb, x_strides[0], wb, w_strides[0], yb, y_strides[0], M, N, K, 1, nullptr,
-                 nullptr};
-    const int64_t need = wy_gemm_2d_workspace_bytes(M, N, K);
-    if (p.split > 1 && need > 0 && workspace_bytes >= need) {
-      a.split = p.split;
-      a.cnt = static_cast<int32_t *>(workspace);
-      a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + kSplitPartOffset);
-    } else if (p.split > 1) {  // no workspace: one workgroup per column block
-      p.split = 1;
-      p.nw = 4;
-      while (p.nw < 16 && p.blocks * p.nw < 2048 && K / (2 * p.nw) >= 128) p.nw *= 2;
-    }
-    if (p.nt == 1) {
-      if (p.nw == 4) launch_skinny_m<4, 1>(a, st);
-      else if (p.nw == 8) launch_skinny_m<8, 1>(a, st);
-      else launch_skinny_m<16, 1>(a, st);
-    } else {
-      if (p.nw == 4) launch_skinny_m<4, 2>(a, st);
-      else if (p.nw == 8) launch_skinny_m<8, 2>(a, st);
-      else launch_skinny_m<16, 2>(a, st);
-    }
-    return wyh::launch_status();
+                 nullptr, ProArgs{}};
+    return run_skinny(a, 0, workspace, workspace_bytes, st);
   }
   // 32-bit buffer offsets within one 128-row band
   if (int64_t(128) * x_strides[0] * 2 >= INT32_MAX || int64_t(128) * w_strides[0] * 2 >= INT32_MAX)
     return WY_E_SHAPE;
   return launch_tiled<128>(xb, x_strides[0], wb, w_strides[0], yb, y_strides[0], M, N, K, st);
+}
+
+extern "C" int wy_gemm_2d_rmsnorm(const void *x, int64_t x_stride0, const void *residual,
+                                  int64_t residual_stride0, const void *norm_weight, float eps,
+                                  void *x_out, int64_t x_out_stride0, const void *w,
+                                  int64_t w_stride0, void *y, int64_t y_stride0, int M, int N,
+                                  int K, void *workspace, int64_t workspace_bytes,
+                                  void *stream) {
+  if (!x || !norm_weight || !w || !y) return WY_E_NULL;
+  if (M < 0 || N < 0 || K <= 0 || K % 256) return WY_E_SHAPE;
+  if (M > kSkinnyMaxM) return WY_E_UNSUPPORTED;
+  if (x_stride0 % 8 || w_stride0 % 8 || x_stride0 < K || w_stride0 < K || y_stride0 < N ||
+      !wyh::aligned16(x) || !wyh::aligned16(w) || !wyh::aligned16(norm_weight) ||
+      (reinterpret_cast<uintptr_t>(y) & 1u) ||
+      (residual && (residual_stride0 % 8 || residual_stride0 < K || !wyh::aligned16(residual))) ||
+      (x_out && (x_out_stride0 % 8 || x_out_stride0 < K || !wyh::aligned16(x_out))))
+    return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return WY_E_LAYOUT;
+  if (M == 0 || N == 0) return WY_OK;
+  ProArgs pro{static_cast<const bf16_t *>(residual), residual_stride0,
+              static_cast<const bf16_t *>(norm_weight), eps, static_cast<bf16_t *>(x_out),
+              x_out_stride0, 0};
+  SkinnyArgs a{static_cast<const bf16_t *>(x), x_stride0, static_cast<const bf16_t *>(w),
+               w_stride0, static_cast<bf16_t *>(y), y_stride0, M, N, K, 1, nullptr, nullptr,
+               pro};
+  return run_skinny(a, 1, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int wy_gemm_2d_swiglu(const void *gate_up, int64_t gate_up_stride0, int64_t up_offset,
+                                 const void *w, int64_t w_stride0, void *y, int64_t y_stride0,
+                                 int M, int N, int K, void *workspace, int64_t workspace_bytes,
+                                 void *stream) {
+  if (!gate_up || !w || !y) return WY_E_NULL;
+  if (M < 0 || N < 0 || K <= 0 || K % 128) return WY_E_SHAPE;
+  if (M > kSkinnyMaxM) return WY_E_UNSUPPORTED;
+  if (gate_up_stride0 % 8 || up_offset % 8 || up_offset < K || gate_up_stride0 < up_offset + K ||
+      w_stride0 % 8 || w_stride0 < K || y_stride0 < N || !wyh::aligned16(gate_up) ||
+      !wyh::aligned16(w) || (reinterpret_cast<uintptr_t>(y) & 1u))
+    return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return WY_E_LAYOUT;
+  if (M == 0 || N == 0) return WY_OK;
+  ProArgs pro{nullptr, 0, nullptr, 0.f, nullptr, 0, up_offset};
+  SkinnyArgs a{static_cast<const bf16_t *>(gate_up), gate_up_stride0,
+               static_cast<const bf16_t *>(w), w_stride0, static_cast<bf16_t *>(y), y_stride0,
+               M, N, K, 1, nullptr, nullptr, pro};
+  return run_skinny(a, 2, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

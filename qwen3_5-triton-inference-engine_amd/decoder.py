@@ -27,13 +27,20 @@ import torch
 from .attention import decode_attention_block, decode_attention_step
 from .cache import allocate_attn_caches
 from .embedding_gather import embedding_gather
-from .gemm_2d import gemm_2d
+from .gemm_2d import gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
 from .gdn_mixer import gdn_decode_block, gdn_decode_ops
 from .partial_rope import rope_inv_freq
 from .qwen_rmsnorm import qwen_rmsnorm
 from .residual_add import residual_add
 from .swiglu import swiglu
 from .vocab_argmax import lm_head_argmax
+
+
+# Above this batch the skinny GEMM's per-workgroup re-reads of its A rows
+# (every column block reads all M rows) make the fused RMSNorm / SwiGLU
+# prologues cost more than the launches they save (measured: B=32 step
+# 1.83 -> 2.02 ms with them, B=1 1.23 -> 1.15 ms).
+FUSED_PROLOGUE_MAX_BATCH = 16
 
 
 @dataclass
@@ -179,7 +186,61 @@ class DecodeModel:
     def decode_step(self, token_ids: torch.Tensor) -> torch.Tensor:
         """Advance every sequence by one token: ``token_ids [B]`` -> final-norm
         hidden ``[B, H]``.  Writes K/V at ``pos`` and advances the GDN states;
-        does not advance ``pos`` (engine/runner.py:520-567)."""
+        does not advance ``pos`` (engine/runner.py:520-567).  With
+        ``fused_mixers`` each residual add + RMSNorm runs inside the next
+        projection's launch and SwiGLU inside the down projection's
+        (bit-identical to the separate ops)."""
+        if not self.fused_mixers:
+            return self._decode_step_ops(token_ids)
+        if self.batch > FUSED_PROLOGUE_MAX_BATCH:
+            return self._decode_step_blocks(token_ids)
+        cfg = self.cfg
+        x = embedding_gather(token_ids, self.embed)
+        h = None  # the previous sub-block's output, not yet added to x
+        for i, w in enumerate(self.layers):
+            fused, x = rmsnorm_gemm_2d(x, h, w.input_layernorm, cfg.eps, w.in_proj)
+            if cfg.is_attention(i):
+                h = self._attention_from(fused, w, self.attn_index[i])
+            else:
+                h = self._gdn_from(fused, w, i)
+            gate_up, x = rmsnorm_gemm_2d(h, x, w.post_attention_layernorm, cfg.eps, w.gate_up)
+            h = swiglu_gemm_2d(gate_up, w.down_proj)
+        x = residual_add(h, x)
+        return qwen_rmsnorm(x, self.final_norm, cfg.eps)
+
+    def _attention_from(self, fused, w: LayerWeights, a: int):
+        cfg = self.cfg
+        o = decode_attention_block(fused, w.extra["q_norm"], w.extra["k_norm"], cfg.eps,
+                                   self.inv_freq, cfg.rotary_dim, self.attn.pos,
+                                   self.attn.k_caches[a], self.attn.v_caches[a],
+                                   self.attn.block_table, self.attn.split_scratch)
+        return gemm_2d(o, w.out_proj)
+
+    def _gdn_from(self, fused, w: LayerWeights, i: int):
+        normed = gdn_decode_block(fused, self.conv_states[i], w.extra["conv"], w.extra["a_log"],
+                                  w.extra["dt_bias"], w.extra["norm"], self.rec_states[i])
+        return gemm_2d(normed, w.out_proj)
+
+    def _decode_step_blocks(self, token_ids: torch.Tensor) -> torch.Tensor:
+        """Mixer blocks, separate residual add / RMSNorm / SwiGLU launches."""
+        cfg = self.cfg
+        x = embedding_gather(token_ids, self.embed)
+        for i, w in enumerate(self.layers):
+            h = qwen_rmsnorm(x, w.input_layernorm, cfg.eps)
+            fused = gemm_2d(h, w.in_proj)
+            if cfg.is_attention(i):
+                h = self._attention_from(fused, w, self.attn_index[i])
+            else:
+                h = self._gdn_from(fused, w, i)
+            x = residual_add(h, x)
+            h = qwen_rmsnorm(x, w.post_attention_layernorm, cfg.eps)
+            gate_up = gemm_2d(h, w.gate_up)
+            h = swiglu(gate_up[:, :cfg.intermediate], gate_up[:, cfg.intermediate:])
+            x = residual_add(gemm_2d(h, w.down_proj), x)
+        return qwen_rmsnorm(x, self.final_norm, cfg.eps)
+
+    def _decode_step_ops(self, token_ids: torch.Tensor) -> torch.Tensor:
+        """The reference runner's op sequence, one op per launch."""
         cfg = self.cfg
         x = embedding_gather(token_ids, self.embed)
         for i, w in enumerate(self.layers):

@@ -49,3 +49,61 @@ def _gemm_2d_fake(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 
 def call_gemm_2d_triton(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return gemm_2d(x, weight)
+
+
+def _split_workspace(x, M, N, K):
+    ws_bytes = _lib.load().wy_gemm_2d_workspace_bytes(M, N, K)
+    ws = _lib.stream_workspace(x.device, "gemm_split", ws_bytes) if ws_bytes > 0 else None
+    return ws, (ws.numel() if ws is not None else 0)
+
+
+@torch.library.custom_op("wy_lib::rmsnorm_gemm_2d", mutates_args=(), device_types="cuda")
+def rmsnorm_gemm_2d(x: torch.Tensor, residual: torch.Tensor | None, norm_weight: torch.Tensor,
+                    eps: float, weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``t = x + residual`` (or x), ``y = qwen_rmsnorm(t, norm_weight, eps) @ weight.T``
+    in one launch (decode M <= 64); returns ``(y, t)``.  Bit-identical to
+    residual_add -> qwen_rmsnorm -> gemm_2d (engine/runner.py:538-562)."""
+    assert x.ndim == 2 and x.dtype == weight.dtype == norm_weight.dtype == torch.bfloat16
+    assert x.stride(1) == 1 and weight.is_contiguous() and norm_weight.is_contiguous()
+    M, K = x.shape
+    N = weight.shape[0]
+    assert weight.shape[1] == K and norm_weight.shape == (K,) and K % 256 == 0 and M <= 64
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == x.dtype
+        assert residual.stride(1) == 1
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    t = torch.empty((M, K), dtype=x.dtype, device=x.device) if residual is not None else None
+    ws, nbytes = _split_workspace(x, M, N, K)
+    _lib.call("wy_gemm_2d_rmsnorm", _lib.ptr(x), x.stride(0), _lib.ptr(residual),
+              residual.stride(0) if residual is not None else 0, _lib.ptr(norm_weight),
+              float(eps), _lib.ptr(t), K, _lib.ptr(weight), weight.stride(0), _lib.ptr(y),
+              y.stride(0), M, N, K, _lib.ptr(ws), nbytes, _lib.stream(x.device))
+    return y, (t if t is not None else x.clone())
+
+
+@rmsnorm_gemm_2d.register_fake
+def _rmsnorm_gemm_2d_fake(x, residual, norm_weight, eps, weight):
+    return x.new_empty((x.shape[0], weight.shape[0])), torch.empty_like(x)
+
+
+@torch.library.custom_op("wy_lib::swiglu_gemm_2d", mutates_args=(), device_types="cuda")
+def swiglu_gemm_2d(gate_up: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``swiglu(gate_up[:, :I], gate_up[:, I:]) @ weight.T`` (I = weight.shape[1])
+    in one launch (M <= 64); bit-identical to swiglu -> gemm_2d
+    (engine/runner.py:562-565)."""
+    assert gate_up.ndim == 2 and gate_up.dtype == weight.dtype == torch.bfloat16
+    assert gate_up.stride(1) == 1 and weight.is_contiguous()
+    M = gate_up.shape[0]
+    N, K = weight.shape
+    assert gate_up.shape[1] == 2 * K and K % 128 == 0 and M <= 64
+    y = torch.empty((M, N), dtype=gate_up.dtype, device=gate_up.device)
+    ws, nbytes = _split_workspace(gate_up, M, N, K)
+    _lib.call("wy_gemm_2d_swiglu", _lib.ptr(gate_up), gate_up.stride(0), K, _lib.ptr(weight),
+              weight.stride(0), _lib.ptr(y), y.stride(0), M, N, K, _lib.ptr(ws), nbytes,
+              _lib.stream(gate_up.device))
+    return y
+
+
+@swiglu_gemm_2d.register_fake
+def _swiglu_gemm_2d_fake(gate_up, weight):
+    return gate_up.new_empty((gate_up.shape[0], weight.shape[0]))

@@ -42,12 +42,15 @@ def states(m):
     return ts + [t for t in m.conv_states + m.rec_states if t is not None]
 
 
-def test_fused_blocks_equal_op_sequence(pkg, dev):
-    say("decoder fused vs op sequence, 4 layers, B=5, 4 steps")
+@pytest.mark.parametrize("B", [5, 20])
+def test_fused_blocks_equal_op_sequence(pkg, dev, B):
+    """B=5 runs the fused RMSNorm / SwiGLU GEMM prologues, B=20 the separate
+    launches with the mixer blocks; both equal the op sequence."""
+    say(f"decoder fused vs op sequence, 4 layers, B={B}, 4 steps")
     cfg = tiny_cfg(pkg, layers=4)
-    a = build(pkg, dev, cfg, 5, 64, True)
-    b = build(pkg, dev, cfg, 5, 64, False)
-    tok = torch.tensor([1, 7, 100, 4095, 3], dtype=torch.int64, device=dev)
+    a = build(pkg, dev, cfg, B, 64, True)
+    b = build(pkg, dev, cfg, B, 64, False)
+    tok = torch.arange(B, dtype=torch.int64, device=dev) * 97 % 4096
     ta, tb = tok.clone(), tok.clone()
     for step in range(4):
         ha, hb = a.decode_step(ta), b.decode_step(tb)
