@@ -20,6 +20,11 @@ using namespace wy::gdn;
 
 namespace {
 
+// tokens whose inputs are in flight in the prefill: deep for the latency-
+// bound narrow layout, shallow for the wide one (registers set occupancy)
+template <int NC>
+constexpr int prefetch_depth() { return NC == 1 ? 4 : 2; }
+
 __device__ __forceinline__ float *state_block(const GdnArgs &a, int b, int h, int kg, int col) {
   return a.state + b * a.s_b + h * a.s_h + int64_t(kg * kRows) * a.s_k + col;
 }
@@ -56,8 +61,9 @@ __global__ __launch_bounds__(512) void gdn_recurrent_decode_kernel(const GdnArgs
 
 // Varlen sequential prefill: one wavefront per (sequence, head, 16 value
 // columns), walking its sequence's tokens in order from a zero state; the
-// next token's inputs are requested before the current token's update.
-template <bool kContig>
+// inputs of the next kPrefetch tokens are in flight during each update.  The
+// state is kept lazily decayed (gdn_step_scaled).
+template <bool kContig, int NC>
 __global__ __launch_bounds__(64) void gdn_prefill_sequential_kernel(const GdnArgs a, int batch) {
   // grid: sequence fastest, then head, then column block
   const int b = blockIdx.x % batch;
@@ -65,30 +71,47 @@ __global__ __launch_bounds__(64) void gdn_prefill_sequential_kernel(const GdnArg
   const int vb = blockIdx.x / (batch * a.heads);
   const int lane = threadIdx.x;
   const int kg = lane & 15, cg = lane >> 4;
-  const int col = vb * kWaveCols + cg * kCols;
+  const int col = vb * 4 * NC + cg * NC;
   const int start = a.cu_seqlens[b];
   const int len = a.cu_seqlens[b + 1] - start;
-  float s[kRows][kCols];
+  float s[kRows][NC];
+  float c = 1.f;  // the state is c * s (gdn_step_scaled)
 #pragma unroll
   for (int i = 0; i < kRows; ++i)
 #pragma unroll
-    for (int j = 0; j < kCols; ++j) s[i][j] = 0.f;
-  if (len > 0) {
-    TokenIn cur, nxt;
-    load_token<kContig>(a, start, h, kg, col, cur);
-    for (int t = 0; t < len; ++t) {
-      const int64_t tok = start + t;
-      if (t + 1 < len) load_token<kContig>(a, tok + 1, h, kg, col, nxt);
-      float o[kCols];
-      gdn_step(s, cur, o);
-      if (kg == 0) store4<kContig>(a.out + tok * a.o_t + h * a.o_h + col * a.o_d, a.o_d, o);
-      cur = nxt;
+    for (int j = 0; j < NC; ++j) s[i][j] = 0.f;
+  // kPrefetch tokens in flight: token t's inputs are requested while token
+  // t - kPrefetch is processed, so the load latency hides behind several steps.
+  constexpr int kPrefetch = prefetch_depth<NC>();
+  TokenInT<NC> buf[kPrefetch];
+#pragma unroll
+  for (int u = 0; u < kPrefetch; ++u)
+    if (u < len) load_token<kContig, NC>(a, start + u, h, kg, col, buf[u]);
+  for (int t0 = 0; t0 < len; t0 += kPrefetch) {
+#pragma unroll
+    for (int u = 0; u < kPrefetch; ++u) {
+      const int t = t0 + u;
+      if (t < len) {
+        float o[NC];
+        gdn_step_scaled(s, c, buf[u], o);
+        const int64_t tok = start + t;
+        if (kg == 0) {
+          bf16_t *op = a.out + tok * a.o_t + h * a.o_h + col * a.o_d;
+          if constexpr (NC == kCols)
+            store4<kContig>(op, a.o_d, o);
+          else
+#pragma unroll
+            for (int e = 0; e < NC; ++e) op[e * a.o_d] = bf16_t(f32_to_bf16_bits(o[e]));
+        }
+        if (t + kPrefetch < len) load_token<kContig, NC>(a, tok + kPrefetch, h, kg, col, buf[u]);
+      }
     }
   }
   float *sp = state_block(a, b, h, kg, col);
 #pragma unroll
   for (int i = 0; i < kRows; ++i)
-    *reinterpret_cast<float4 *>(sp + i * a.s_k) = make_float4(s[i][0], s[i][1], s[i][2], s[i][3]);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) sp[i * a.s_k + j] = c * s[i][j];
 }
 
 // Shared argument checks; returns WY_OK and fills a, or an error code.
@@ -171,12 +194,25 @@ extern "C" int wy_gdn_recurrent_prefill_sequential(
   if (batch < 0) return WY_E_SHAPE;
   if (batch == 0) return WY_OK;
   a.cu_seqlens = cu_seqlens;
-  const int64_t blocks = int64_t(batch) * num_heads * (value_dim / kWaveCols);
+  // 16 value columns per wavefront (4 per lane) when the grid fills the
+  // chip several times over; else 4 per wavefront (1 per lane): a token step
+  // is a chain of dependent VALU / DPP work, so fewer columns per lane
+  // shorten the chain where there are SIMDs to spare.
+  const int64_t wide = int64_t(batch) * num_heads * (value_dim / kWaveCols);
+  const bool narrow = wide < 2048;
+  const int64_t blocks = narrow ? wide * 4 : wide;
   if (blocks > 0x7fffffff) return WY_E_SHAPE;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  if (contig)
-    gdn_prefill_sequential_kernel<true><<<unsigned(blocks), 64, 0, st>>>(a, batch);
-  else
-    gdn_prefill_sequential_kernel<false><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+  if (narrow) {
+    if (contig)
+      gdn_prefill_sequential_kernel<true, 1><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+    else
+      gdn_prefill_sequential_kernel<false, 1><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+  } else {
+    if (contig)
+      gdn_prefill_sequential_kernel<true, kCols><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+    else
+      gdn_prefill_sequential_kernel<false, kCols><<<unsigned(blocks), 64, 0, st>>>(a, batch);
+  }
   return wyh::launch_status();
 }
