@@ -501,6 +501,14 @@ def decoder_bench(pkg, dev):
     ref_ms = {1: 2.010, 32: 4.662}
     out = {}
     for B in (1, 32):
+        hid = torch.randn(B, cfg.hidden, device=dev).to(torch.bfloat16)
+        ms = time_graph_events(lambda: pkg.lm_head_argmax(hid, weights[1], False), 10)
+        nbytes = weights[1].numel() * 2
+        out[f"lm_head_argmax B={B}"] = {
+            "us": round(ms * 1e3, 2), "GB/s": round(nbytes / ms / 1e6, 1),
+            "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        log(f"lm_head_argmax B={B}: {out[f'lm_head_argmax B={B}']}")
+    for B in (1, 32):
         model = DecodeModel(cfg, weights, batch=B, max_len=2064, device=dev)
         gen = torch.Generator().manual_seed(2)
         lens = torch.randint(128, 2049, (B,), generator=gen)

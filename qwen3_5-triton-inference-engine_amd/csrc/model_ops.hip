@@ -72,17 +72,17 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t *__restrict__ 
 // ---- LM head + argmax -----------------------------------------------------------------
 //
 // logits[m, v] = sum_k x[m, k] W[v, k] (fp32), token[m] = argmax_v (first
-// index on ties).  Stage 1: persistent 4-wave workgroups stage x (rows
+// index on ties).  Stage 1: persistent 8-wave workgroups stage x (rows
 // padded to MT*16, zero rows past the batch) in LDS once, then stream
 // 16-row vocabulary tiles straight from HBM into the B operand of
 // v_mfma_f32_16x16x32_bf16 (lane = vocab row l%16 x 8 consecutive k), x
 // from LDS as the A operand.  Lane l's outputs are rows 4(l/16)+j of column
 // l%16; each lane keeps its running best over the tiles it sees (strict
-// greater: the first maximum).  The workgroup folds its 4 waves x 16
+// greater: the first maximum).  The workgroup folds its 8 waves x 16
 // columns into one key per row: orderable float bits << 32 | ~index, so the
 // largest key is the largest logit with the smallest index.  Stage 2: one
 // wavefront per row takes the max key over the workgroups.
-constexpr int kArgmaxWaves = 4;
+constexpr int kArgmaxWaves = 8;
 constexpr int kKBatch = 8;  // k-steps (32 wide) whose weight loads are in flight together
 
 __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
