@@ -538,6 +538,23 @@ def decoder_bench(pkg, dev):
             "hbm_bytes_per_step": wbytes + sbytes + kvbytes,
             "GB/s": round((wbytes + sbytes + kvbytes) / ms / 1e6, 1)}
         log(f"decoder B={B}: {out[f'B={B}']}")
+        if B == 32:
+            # packed prefill of 32 x 128-token prompts into the same caches
+            # (eager: the ops read cu_seqlens on the host, as the reference's do)
+            lengths = [128] * 32
+            ptoks = torch.randint(0, cfg.vocab, (sum(lengths),), generator=gen).to(dev)
+            model.prefill(ptoks, lengths)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(3):
+                model.prefill(ptoks, lengths)
+            torch.cuda.synchronize()
+            pms = (time.perf_counter() - t0) * 1e3 / 3
+            out["prefill B=32 x T=128 (packed)"] = {
+                "ms": round(pms, 3), "tokens_per_s": round(4096 / pms * 1e3, 1),
+                "reference_a100_ms": 61.0,
+                "what": "24 layers, wall clock incl. host dispatch; reference README-EN.md:88-96"}
+            log(f"prefill 32x128: {out['prefill B=32 x T=128 (packed)']}")
         del g, model
         torch.cuda.empty_cache()
     return out

@@ -24,7 +24,17 @@ from dataclasses import dataclass, field
 
 import torch
 
-from .attention import decode_attention_block, decode_attention_step
+from .attention import (
+    build_packed_batch,
+    decode_attention_block,
+    decode_attention_step,
+    prefill_attention_block,
+)
+from .depthwise_causal_conv4_decode import conv_state_from_packed_prefill
+from .depthwise_causal_conv4_prefill import depthwise_causal_conv4_prefill
+from .gdn_gated_rmsnorm import gdn_gated_rmsnorm
+from .gdn_qk_norm_gates import gdn_qk_norm_gates
+from .gdn_recurrent_prefill import gdn_recurrent_prefill_sequential
 from .cache import allocate_attn_caches
 from .embedding_gather import embedding_gather
 from .gemm_2d import gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
@@ -258,6 +268,74 @@ class DecodeModel:
             h = gemm_2d(h, w.down_proj)
             x = residual_add(h, residual)
         return qwen_rmsnorm(x, self.final_norm, cfg.eps)
+
+    # ------------------------------------------------------------ prefill
+    def prefill(self, token_ids: torch.Tensor, lengths: list[int]) -> torch.Tensor:
+        """Packed prefill of B prompts (``token_ids`` ``[sum(lengths)]``, one
+        prompt per sequence slot, engine/runner.py:570-667): fills the K/V
+        pages, the GDN conv and recurrent states, sets ``pos[b] = lengths[b]``
+        and returns each prompt's greedy next token ``[B]`` int64."""
+        cfg = self.cfg
+        assert len(lengths) == self.batch and min(lengths) >= 1
+        assert max(lengths) <= self.attn.max_len
+        packed = build_packed_batch(list(lengths), device=self.device)
+        T = packed.total_tokens
+        x = embedding_gather(token_ids, self.embed)
+        for i, w in enumerate(self.layers):
+            residual = x
+            h = qwen_rmsnorm(x, w.input_layernorm, cfg.eps)
+            fused = gemm_2d(h, w.in_proj)
+            if cfg.is_attention(i):
+                h = self._attention_prefill(fused, w, self.attn_index[i], packed)
+            else:
+                h = self._gdn_prefill(fused, w, i, packed)
+            x = residual_add(h, residual)
+            residual = x
+            h = qwen_rmsnorm(x, w.post_attention_layernorm, cfg.eps)
+            gate_up = gemm_2d(h, w.gate_up)
+            h = gemm_2d(swiglu(gate_up[:, :cfg.intermediate], gate_up[:, cfg.intermediate:]),
+                        w.down_proj)
+            x = residual_add(h, residual)
+        last = packed.cu_seqlens[1:].long() - 1
+        hidden = qwen_rmsnorm(x[last].contiguous(), self.final_norm, cfg.eps)
+        self.attn.pos.copy_(torch.tensor(lengths, dtype=torch.int64, device=self.device))
+        assert T == token_ids.shape[0]
+        return lm_head_argmax(hidden, self.embed, False)
+
+    def _attention_prefill(self, fused, w: LayerWeights, a: int, packed):
+        cfg = self.cfg
+        T = fused.shape[0]
+        qd, kd = cfg.num_q_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+        q = qwen_rmsnorm(fused[:, :qd].view(T, cfg.num_q_heads, cfg.head_dim),
+                         w.extra["q_norm"], cfg.eps)
+        k = qwen_rmsnorm(fused[:, 2 * qd:2 * qd + kd].view(T, cfg.num_kv_heads, cfg.head_dim),
+                         w.extra["k_norm"], cfg.eps)
+        v = fused[:, 2 * qd + kd:].view(T, cfg.num_kv_heads, cfg.head_dim)
+        gate = fused[:, qd:2 * qd].view(T, cfg.num_q_heads, cfg.head_dim)
+        o = prefill_attention_block(q, k, v, gate, self.inv_freq, cfg.rotary_dim, packed,
+                                    self.attn.k_caches[a], self.attn.v_caches[a],
+                                    self.attn.block_table)
+        return gemm_2d(o, w.out_proj)
+
+    def _gdn_prefill(self, fused, w: LayerWeights, i: int, packed):
+        cfg = self.cfg
+        T = fused.shape[0]
+        H, D = cfg.lin_heads, cfg.lin_head_dim
+        HD = H * D
+        qkv = fused[:, :3 * HD]
+        # the decode conv weight [4, C] read as the prefill layout [C, 4]
+        conv = depthwise_causal_conv4_prefill(qkv, w.extra["conv"].t(), packed.seq_start)
+        q = conv[:, :HD].view(T, H, D)
+        k = conv[:, HD:2 * HD].view(T, H, D)
+        v = conv[:, 2 * HD:].view(T, H, D)
+        qn, kn, beta, g = gdn_qk_norm_gates(q, k, fused[:, 4 * HD:4 * HD + H],
+                                            fused[:, 4 * HD + H:], w.extra["a_log"],
+                                            w.extra["dt_bias"])
+        core, state = gdn_recurrent_prefill_sequential(qn, kn, v, beta, g, packed.cu_seqlens)
+        self.rec_states[i].copy_(state)
+        conv_state_from_packed_prefill(self.conv_states[i], qkv, packed.cu_seqlens)
+        normed = gdn_gated_rmsnorm(core, fused[:, 3 * HD:4 * HD].view(T, H, D), w.extra["norm"])
+        return gemm_2d(normed.view(T, HD), w.out_proj)
 
     def next_tokens(self, token_ids: torch.Tensor) -> torch.Tensor:
         """One step plus the greedy pick: ``[B]`` -> ``[B]`` int64; advances pos."""
