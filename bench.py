@@ -169,7 +169,8 @@ def main():
                     help="untimed steps first")
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
-    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-gemm"],
+    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-gemm",
+                             "pmc-gdn"],
                     help="pmc-*: eager launches only, for rocprofv3 counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -240,6 +241,30 @@ def main():
                 pkg.gemm_2d(x, wt)
         torch.cuda.synchronize()
         print(json.dumps({"mode": "pmc-gemm"}))
+        return
+    if args.mode == "pmc-gdn":
+        # GDN recurrence decode and the GDN decode block at B=32, 10 eager calls each
+        gg = torch.Generator(device=dev).manual_seed(9)
+        Bg, Hg, Dg = 32, 16, 128
+        q = (torch.randn(Bg, Hg, Dg, device=dev, generator=gg) * 0.08).to(torch.bfloat16)
+        k = (torch.randn(Bg, Hg, Dg, device=dev, generator=gg) * 0.08).to(torch.bfloat16)
+        v = torch.randn(Bg, Hg, Dg, device=dev, generator=gg).to(torch.bfloat16)
+        beta = torch.rand(Bg, Hg, device=dev, generator=gg)
+        g = -torch.rand(Bg, Hg, device=dev, generator=gg)
+        st = torch.randn(Bg, Hg, Dg, Dg, device=dev, generator=gg) * 0.1
+        fused = torch.randn(Bg, 4 * Hg * Dg + 2 * Hg, device=dev, generator=gg).to(torch.bfloat16)
+        cs = torch.randn(Bg, 4, 3 * Hg * Dg, device=dev, generator=gg).to(torch.bfloat16)
+        cw = (torch.randn(4, 3 * Hg * Dg, device=dev, generator=gg) * 0.5).to(torch.bfloat16)
+        a_log = torch.zeros(Hg, device=dev)
+        dt = torch.zeros(Hg, device=dev, dtype=torch.bfloat16)
+        nw = torch.ones(Dg, device=dev)
+        for _ in range(10):
+            pkg.gdn_recurrent_decode(q, k, v, beta, g, st)
+        for _ in range(10):
+            pkg.gdn_decode_block(fused, cs, cw, a_log, dt, nw, st)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "pmc-gdn",
+                          "decode_algorithmic_bytes": Bg * Hg * (2 * Dg * Dg * 4 + 4 * Dg * 2 + 8)}))
         return
     if args.mode == "pmc-copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
