@@ -7,7 +7,11 @@ in one HIP graph and replayed.  ``value`` is algorithmic HBM GB/s of the step
 (KV bytes read + q/gate/out/append/page-table bytes, split scratch excluded).
 
 Also reported (``extra``): config 1 latency, config 3 and 4 varlen prefill
-TFLOP/s, config 5 long-context decode GB/s.  ``roofline`` is the split kernel
+TFLOP/s, config 5 long-context decode GB/s, the attention block / layer, the
+config-3 HBM-bound companions, ``gemm_2d`` next to hipBLASLt, the Gated
+DeltaNet kernels (``gdn``) and the whole 24-layer model (``model``: LM-head
+argmax, graph-replayed decode step at B=1 / 32, packed prefill of 32 x 128
+tokens); ``--only a,b`` selects extras by name.  ``roofline`` is the split kernel
 timed alone with HIP events on its stream; ``cpu_baseline`` is the CPU oracle
 on a bounded sample of the same workload.
 
