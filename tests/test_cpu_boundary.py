@@ -134,6 +134,26 @@ def test_gdn_entry_points_reject_before_launch(pkg):
                                                 d, s2, 2, 6144, None) == -3
 
 
+def test_fused_gemm_and_lm_head_reject_before_launch(pkg):
+    lib = pkg._lib.load()
+    d = ctypes.c_void_p(256)
+    # M > 64 has no fused-prologue kernel; K % 256 for the RMSNorm prologue
+    assert lib.wy_gemm_2d_rmsnorm(d, 1024, None, 0, d, 1e-6, None, 0, d, 1024, d, 1024, 65,
+                                  1024, 1024, None, 0, None) == -4
+    assert lib.wy_gemm_2d_rmsnorm(d, 1024, None, 0, d, 1e-6, None, 0, d, 1024, d, 1024, 4,
+                                  1024, 1000, None, 0, None) == -2
+    assert lib.wy_gemm_2d_swiglu(d, 7168, 3584, d, 3584, d, 1024, 65, 1024, 3584, None, 0,
+                                 None) == -4
+    # up half overlapping the gate half
+    assert lib.wy_gemm_2d_swiglu(d, 7168, 1024, d, 3584, d, 1024, 4, 1024, 3584, None, 0,
+                                 None) == -3
+    # more than 64 rows, no workspace, unsupported hidden size
+    assert lib.wy_lm_head_argmax(d, 1024, d, 1024, d, 65, 1024, 5000, d, 1 << 20, None) == -2
+    assert lib.wy_lm_head_argmax(d, 1024, d, 1024, d, 4, 1024, 5000, None, 0, None) == -1
+    assert lib.wy_lm_head_argmax(d, 1024, d, 1024, d, 4, 1000, 5000, d, 1 << 20, None) == -4
+    assert lib.wy_lm_head_argmax_workspace_bytes(32, 1024, 248320) > 0
+
+
 def test_gemm_split_workspace_sizes(pkg):
     """Decode o_proj [1024, 2048] at B=32 splits K 4 ways: 16 KiB of counters
     plus 4 * 32 * 1024 fp32 partials; prefill shapes and wide N do not split."""
@@ -185,7 +205,9 @@ def test_op_schemas_match_reference():
         assert args.replace("SymInt", "int") == sig.replace("SymInt", "int"), s
     for name in ("paged_kv_fill_varlen", "paged_gqa_attention_decode_split",
                  "paged_gqa_attention_decode_combine", "partial_rope",
-                 "prefill_attention_block", "gdn_decode_block"):
+                 "prefill_attention_block", "gdn_decode_block", "rmsnorm_gemm_2d",
+                 "swiglu_gemm_2d", "embedding_gather", "residual_add", "swiglu",
+                 "lm_head_argmax"):
         assert hasattr(torch.ops.wy_lib, name)
 
 

@@ -126,3 +126,39 @@ def test_gemm_2d_split_k(pkg, dev, M, N, K):
         torch.cuda.synchronize()
         assert torch.equal(yg, y)
         assert torch.equal(pkg.gemm_2d(xd, wd), y)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 32, 64])
+@pytest.mark.parametrize("N", [1024, 7168])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_gemm_equals_separate_ops(pkg, dev, M, N, with_residual):
+    """wy_gemm_2d_rmsnorm == residual_add -> qwen_rmsnorm -> gemm_2d, bit for
+    bit, including the residual-stream output (N=1024 takes the split-K path)."""
+    print(f"rmsnorm_gemm M={M} N={N} residual={with_residual}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(M * 7 + N)
+    K = 1024
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    r = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16) if with_residual else None
+    nw = (torch.randn(K, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=dev, generator=g) * 0.03).to(torch.bfloat16)
+    y, t = pkg.rmsnorm_gemm_2d(x, r, nw, 1e-6, w)
+    t_ref = pkg.residual_add(x, r) if with_residual else x
+    y_ref = pkg.gemm_2d(pkg.qwen_rmsnorm(t_ref, nw, 1e-6), w)
+    torch.cuda.synchronize()
+    assert torch.equal(t, t_ref)
+    assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_swiglu_gemm_equals_separate_ops(pkg, dev, M):
+    """wy_gemm_2d_swiglu == swiglu -> gemm_2d bit for bit (down projection
+    [1024, 3584], the split-K path)."""
+    print(f"swiglu_gemm M={M}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(M)
+    I, N = 3584, 1024
+    gu = torch.randn(M, 2 * I, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, I, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    y = pkg.swiglu_gemm_2d(gu, w)
+    y_ref = pkg.gemm_2d(pkg.swiglu(gu[:, :I], gu[:, I:]), w)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
