@@ -459,12 +459,13 @@ int wy_conv_state_from_packed_prefill(void *state, const int64_t *state_strides,
 /*
  * Token embedding gather: out[t, :] = weight[input_ids[t], :] (bf16 rows of
  * d_model, d_model % 8 == 0, 16-byte aligned rows); input_ids [T] int32 or
- * int64 (ids_is_int64).  Replaces wy_lib::embedding_gather
- *   (triton_kernels/embedding_gather.py:62-104, kernel :20-50).
+ * int64 (ids_is_int64); weight has `vocab` rows, and an id outside [0, vocab)
+ * writes a zero row (never a read past the table).  Replaces
+ * wy_lib::embedding_gather (triton_kernels/embedding_gather.py:62-104, kernel :20-50).
  */
 int wy_embedding_gather(const void *input_ids, int ids_is_int64, const void *weight,
-                        int64_t weight_row_stride, void *out, int64_t out_row_stride, int tokens,
-                        int d_model, void *stream);
+                        int64_t weight_row_stride, int64_t vocab, void *out,
+                        int64_t out_row_stride, int tokens, int d_model, void *stream);
 
 /*
  * out = bf16(x + residual) over n contiguous bf16 elements (16-byte aligned).
@@ -482,8 +483,9 @@ int wy_swiglu(const void *gate, const int64_t *gate_strides, const void *up,
 
 /*
  * LM head fused with the vocabulary argmax: token_ids[m] = argmax_v
- * sum_k hidden[m, k] * weight[v, k] (fp32 sums, the first index on ties),
- * logits never written.  hidden [rows, hidden_size] bf16 (rows <= 64),
+ * sum_k hidden[m, k] * weight[v, k] (fp32 sums, the first index on ties;
+ * NaN ranks above every number, first NaN wins, as torch.argmax; the result
+ * is always in [0, vocab)), logits never written.  hidden [rows, hidden_size] bf16 (rows <= 64),
  * weight [vocab, hidden_size] bf16, 16-byte aligned rows; hidden_size a
  * multiple of 256; token_ids [rows] int64.  workspace: at least
  * wy_lm_head_argmax_workspace_bytes(rows, hidden_size, vocab) bytes,

@@ -449,6 +449,17 @@ void launch_skinny_plan(const SkinnyArgs &a, int nt, int nw, hipStream_t st) {
 struct SkinnyPlan {
   int nt, blocks, split, nw;
 };
+// Waves per workgroup for `groups` workgroups that each cover `ks` of K: grow
+// from 4 while the grid holds fewer than 2048 waves, each wave keeps at least
+// one 128-wide batch of k, and every wave's slice stays a multiple of 32
+// (the kernel's tail loop steps 32 columns and must not cross into the next
+// wave's slice).  ks is a multiple of 128, so 4 waves always divide it.
+int skinny_waves(int groups, int ks) {
+  int nw = 4;
+  while (nw < 16 && groups * nw < 2048 && ks / (2 * nw) >= 128 && ks % (64 * nw) == 0) nw *= 2;
+  return nw;
+}
+
 SkinnyPlan skinny_plan(int N, int K) {
   SkinnyPlan p;
   // 32 columns per workgroup when N is large (each x load then feeds two
@@ -464,9 +475,7 @@ SkinnyPlan skinny_plan(int N, int K) {
     p.split *= 2;
   // Waves: enough workgroups x waves to keep the CUs streaming, each wave at
   // least one 128-wide batch of k.
-  const int ks = K / p.split;
-  p.nw = 4;
-  while (p.nw < 16 && p.blocks * p.split * p.nw < 2048 && ks / (2 * p.nw) >= 128) p.nw *= 2;
+  p.nw = skinny_waves(p.blocks * p.split, K / p.split);
   return p;
 }
 
@@ -497,8 +506,7 @@ static int run_skinny(SkinnyArgs a, int pro, void *workspace, int64_t workspace_
     a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + kSplitPartOffset);
   } else if (p.split > 1) {  // no workspace: one workgroup per column block
     p.split = 1;
-    p.nw = 4;
-    while (p.nw < 16 && p.blocks * p.nw < 2048 && a.K / (2 * p.nw) >= 128) p.nw *= 2;
+    p.nw = skinny_waves(p.blocks, a.K);
   }
   if (pro == 1) launch_skinny_plan<1>(a, p.nt, p.nw, st);
   else if (pro == 2) launch_skinny_plan<2>(a, p.nt, p.nw, st);

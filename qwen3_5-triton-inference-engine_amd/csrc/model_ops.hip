@@ -12,14 +12,18 @@ namespace {
 // ---- embedding gather: one 16-byte chunk per thread ------------------------------
 __global__ __launch_bounds__(256) void embedding_gather_kernel(
     const void *__restrict__ ids, int ids_is_64, const bf16_t *__restrict__ table,
-    int64_t tbl_row, bf16_t *__restrict__ out, int64_t out_row, int T, int chunks_per_row) {
+    int64_t tbl_row, int64_t vocab, bf16_t *__restrict__ out, int64_t out_row, int T,
+    int chunks_per_row) {
   const int64_t gid = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int t = int(gid / chunks_per_row);
   const int c = int(gid - int64_t(t) * chunks_per_row);
   if (t >= T) return;
   const int64_t id = ids_is_64 ? static_cast<const int64_t *>(ids)[t]
                                : int64_t(static_cast<const int32_t *>(ids)[t]);
-  st16(out + t * out_row + c * 8, ld16(table + id * tbl_row + c * 8));
+  // an id outside [0, vocab) yields a zero row instead of a read past the table
+  const bool ok = id >= 0 && id < vocab;
+  st16(out + t * out_row + c * 8,
+       ok ? ld16(table + id * tbl_row + c * 8) : u32x4_t{0u, 0u, 0u, 0u});
 }
 
 // ---- residual add: bf16(x + r), 8 elements per thread ---------------------------
@@ -81,13 +85,16 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const bf16_t *__restrict__ 
 // greater: the first maximum).  The workgroup folds its 8 waves x 16
 // columns into one key per row: orderable float bits << 32 | ~index, so the
 // largest key is the largest logit with the smallest index.  Stage 2: one
-// wavefront per row takes the max key over the workgroups.
+// wavefront per row takes the max key over the workgroups.  NaN ranks above
+// every number (first NaN wins), as torch.argmax does, and a lane takes the
+// first valid column it sees unconditionally, so a row whose logits are all
+// -inf or NaN still yields an index in [0, V).
 constexpr int kArgmaxWaves = 8;
 constexpr int kKBatch = 8;  // k-steps (32 wide) whose weight loads are in flight together
 
 __device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
   uint32_t u = __float_as_uint(v);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  u = (v != v) ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
   return (uint64_t(u) << 32) | uint64_t(0xffffffffu - uint32_t(idx));
 }
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
@@ -154,7 +161,8 @@ __global__ __launch_bounds__(64 * kArgmaxWaves) void lm_head_argmax_stage1(
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (acc[mt][j] > best[mt][j]) {
+          if (best_i[mt][j] == 0x7fffffff || acc[mt][j] > best[mt][j] ||
+              (acc[mt][j] != acc[mt][j] && best[mt][j] == best[mt][j])) {
             best[mt][j] = acc[mt][j];
             best_i[mt][j] = vrow;
           }
@@ -219,10 +227,11 @@ int launch_stage1(int grid, size_t lds, hipStream_t st, const bf16_t *x, int64_t
 }  // namespace
 
 extern "C" int wy_embedding_gather(const void *input_ids, int ids_is_int64, const void *weight,
-                                   int64_t weight_row_stride, void *out, int64_t out_row_stride,
-                                   int tokens, int d_model, void *stream) {
+                                   int64_t weight_row_stride, int64_t vocab, void *out,
+                                   int64_t out_row_stride, int tokens, int d_model,
+                                   void *stream) {
   if (!input_ids || !weight || !out) return WY_E_NULL;
-  if (tokens < 0 || d_model <= 0) return WY_E_SHAPE;
+  if (tokens < 0 || d_model <= 0 || vocab <= 0) return WY_E_SHAPE;
   if (d_model % 8 || weight_row_stride % 8 || out_row_stride % 8 || !wyh::aligned16(weight) ||
       !wyh::aligned16(out))
     return WY_E_LAYOUT;
@@ -231,7 +240,7 @@ extern "C" int wy_embedding_gather(const void *input_ids, int ids_is_int64, cons
   const int64_t threads = int64_t(tokens) * cpr;
   embedding_gather_kernel<<<unsigned((threads + 255) / 256), 256, 0,
                             static_cast<hipStream_t>(stream)>>>(
-      input_ids, ids_is_int64, static_cast<const bf16_t *>(weight), weight_row_stride,
+      input_ids, ids_is_int64, static_cast<const bf16_t *>(weight), weight_row_stride, vocab,
       static_cast<bf16_t *>(out), out_row_stride, tokens, cpr);
   return wyh::launch_status();
 }

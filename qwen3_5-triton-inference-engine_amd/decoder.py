@@ -354,7 +354,9 @@ class GraphedDecoder:
     def __init__(self, model: DecodeModel, first_tokens: torch.Tensor):
         self.model = model
         self.tokens = first_tokens.to(torch.int64).clone()
-        # warm up on a side stream (allocator pools, workspaces), then restore
+        # warm up on the stream the capture will use: the per-stream zeroed
+        # workspaces (split-K and argmax partials, queue counters) are then
+        # allocated and cleared here, outside the graph; afterwards restore
         # every state the warm-up advanced
         saved = self._snapshot()
         side = torch.cuda.Stream()
@@ -365,7 +367,7 @@ class GraphedDecoder:
         torch.cuda.synchronize()
         self._restore(saved)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=side):
             self._step()
         torch.cuda.synchronize()
         self._restore(saved)

@@ -28,7 +28,7 @@ def embedding_gather(input_ids: torch.Tensor, weight: torch.Tensor) -> torch.Ten
     assert d_model & (d_model - 1) == 0
     out = torch.empty((token_num, d_model), dtype=weight.dtype, device=weight.device)
     _lib.call("wy_embedding_gather", _lib.ptr(input_ids), int(input_ids.dtype == torch.int64),
-              _lib.ptr(weight), weight.stride(0), _lib.ptr(out), out.stride(0), token_num,
+              _lib.ptr(weight), weight.stride(0), weight.shape[0], _lib.ptr(out), out.stride(0), token_num,
               d_model, _lib.stream(weight.device))
     return out
 

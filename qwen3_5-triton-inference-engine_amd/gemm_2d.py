@@ -51,6 +51,14 @@ def call_gemm_2d_triton(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return gemm_2d(x, weight)
 
 
+def _rows16(t):
+    """The fused-prologue kernels read 16-byte chunks of every row: rows must be
+    unit-stride, start 16-byte aligned and be 8 elements apart; copy otherwise."""
+    if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+        return t.contiguous()
+    return t
+
+
 def _split_workspace(x, M, N, K):
     ws_bytes = _lib.load().wy_gemm_2d_workspace_bytes(M, N, K)
     ws = _lib.stream_workspace(x.device, "gemm_split", ws_bytes) if ws_bytes > 0 else None
@@ -64,13 +72,14 @@ def rmsnorm_gemm_2d(x: torch.Tensor, residual: torch.Tensor | None, norm_weight:
     in one launch (decode M <= 64); returns ``(y, t)``.  Bit-identical to
     residual_add -> qwen_rmsnorm -> gemm_2d (engine/runner.py:538-562)."""
     assert x.ndim == 2 and x.dtype == weight.dtype == norm_weight.dtype == torch.bfloat16
-    assert x.stride(1) == 1 and weight.is_contiguous() and norm_weight.is_contiguous()
+    assert weight.is_contiguous() and norm_weight.is_contiguous()
+    x = _rows16(x)
     M, K = x.shape
     N = weight.shape[0]
     assert weight.shape[1] == K and norm_weight.shape == (K,) and K % 256 == 0 and M <= 64
     if residual is not None:
         assert residual.shape == x.shape and residual.dtype == x.dtype
-        assert residual.stride(1) == 1
+        residual = _rows16(residual)
     y = torch.empty((M, N), dtype=x.dtype, device=x.device)
     t = torch.empty((M, K), dtype=x.dtype, device=x.device) if residual is not None else None
     ws, nbytes = _split_workspace(x, M, N, K)
@@ -92,7 +101,8 @@ def swiglu_gemm_2d(gate_up: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     in one launch (M <= 64); bit-identical to swiglu -> gemm_2d
     (engine/runner.py:562-565)."""
     assert gate_up.ndim == 2 and gate_up.dtype == weight.dtype == torch.bfloat16
-    assert gate_up.stride(1) == 1 and weight.is_contiguous()
+    assert weight.is_contiguous()
+    gate_up = _rows16(gate_up)
     M = gate_up.shape[0]
     N, K = weight.shape
     assert gate_up.shape[1] == 2 * K and K % 128 == 0 and M <= 64

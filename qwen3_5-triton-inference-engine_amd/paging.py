@@ -1,18 +1,32 @@
 """Physical page allocation and the device block table.
 
-Same contract as the reference's ``engine/paging.py``:
+Contract kept from the reference's ``engine/paging.py:55-177`` (callers and
+existing caches depend on it):
 
-* host side: a free list of physical page ids (``PagePool``);
-* device side: ``block_table`` ``[B, max_pages]`` int32, logical page -> physical
-  page, one row per sequence.  Kernels read it when they run, so the host may
-  write newly reserved pages between graph replays; its shape never changes.
+* ``allocate_block_table`` -> zeroed ``[B, max_pages]`` int32 table, one row per
+  sequence, logical page -> physical page.  Kernels read it when they run, so
+  the host may write newly reserved pages between graph replays; its shape and
+  address never change.
+* ``PagePool.alloc`` hands out pages from the tail of the free order and
+  ``free`` puts them back at the tail, so an alloc/free cycle returns the same
+  page ids (reproducible runs); asking for more pages than are free raises
+  ``AssertionError`` on the host.
+* ``SequencePages.reserve`` takes only the pages a sequence is missing,
+  ``release`` returns them and zeroes the released rows, ``capacity`` is the
+  tokens the held pages cover.
 
 Token t of sequence b lives at row ``(block_table[b, t // 16] * H + h) * 16 +
 t % 16`` of ``k_cache.view(-1, D)``.
+
+Design here: the pool is a fixed int32 stack with a top index (alloc/free are
+slice copies, no per-page Python objects); a batch's page ownership is a host
+mirror of the device table plus a held-page count per row, and a reservation
+writes the row's new entries with one host->device copy of that slice.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .gqa_attention_decode_paged import PAGE_SIZE
@@ -21,87 +35,93 @@ from .gqa_attention_decode_paged import PAGE_SIZE
 def allocate_block_table(
     max_pages: int, *, batch: int = 1, device: torch.device | str = "cuda"
 ) -> torch.Tensor:
-    """Zeroed ``[B, max_pages]`` int32 table (reference engine/paging.py:55)."""
+    """Zeroed ``[batch, max_pages]`` int32 table (reference engine/paging.py:55)."""
     return torch.zeros((batch, max_pages), dtype=torch.int32, device=device)
 
 
 class PagePool:
-    """Host free list of physical pages (reference engine/paging.py:71-103).
-
-    ``alloc`` takes pages from the tail and ``free`` appends them back, so a
-    repeated alloc/free cycle hands out the same page ids (reproducible runs).
-    """
+    """Free physical pages as a stack: ``_stack[:_top]`` are free, the next
+    allocation takes ``_stack[_top - count:_top]`` (reference interface:
+    engine/paging.py:71-103)."""
 
     def __init__(self, num_pages: int):
-        assert num_pages > 0
+        assert num_pages > 0, f"a page pool needs at least one page (got {num_pages})"
         self.num_pages = num_pages
-        self._free: list[int] = list(range(num_pages))
+        self._stack = np.arange(num_pages, dtype=np.int32)
+        self._top = num_pages
 
     @property
     def num_free(self) -> int:
-        return len(self._free)
+        return self._top
 
     def alloc(self, count: int) -> list[int]:
-        assert count <= len(self._free), (
-            f"out of pages: need {count}, {len(self._free)} free of {self.num_pages} "
-            f"({PAGE_SIZE} tokens per page); raise num_pages or lower max_tokens"
+        assert 0 <= count <= self._top, (
+            f"page pool exhausted: {count} pages requested, {self._top} of "
+            f"{self.num_pages} free ({PAGE_SIZE}-token pages)"
         )
-        if count == 0:
-            return []
-        taken = self._free[-count:]
-        del self._free[-count:]
-        return taken
+        self._top -= count
+        return self._stack[self._top:self._top + count].tolist()
 
-    def free(self, pages: list[int]) -> None:
-        self._free.extend(pages)
+    def free(self, pages) -> None:
+        n = len(pages)
+        assert self._top + n <= self.num_pages, "more pages freed than the pool holds"
+        self._stack[self._top:self._top + n] = pages
+        self._top += n
 
     def reset(self) -> None:
-        self._free = list(range(self.num_pages))
+        self._stack[:] = np.arange(self.num_pages, dtype=np.int32)
+        self._top = self.num_pages
 
 
 class SequencePages:
-    """Block table of a batch plus the host record of each row's pages
-    (reference engine/paging.py:106-177)."""
+    """Device block table of a batch plus the host record of which pages each
+    row holds (reference interface: engine/paging.py:106-177)."""
 
     def __init__(self, max_pages: int, *, batch: int = 1,
                  device: torch.device | str = "cuda"):
         self.max_pages = max_pages
         self.batch = batch
         self.block_table = allocate_block_table(max_pages, batch=batch, device=device)
-        self.pages: list[list[int]] = [[] for _ in range(batch)]
+        self._rows = np.zeros((batch, max_pages), dtype=np.int32)   # host mirror
+        self._held = np.zeros(batch, dtype=np.int64)                  # pages per row
+
+    @property
+    def pages(self) -> list[list[int]]:
+        """Physical pages held by each sequence, in logical order."""
+        return [self._rows[b, :self._held[b]].tolist() for b in range(self.batch)]
 
     def reserve(self, token_num: int, pool: PagePool, *, seq: int = 0) -> None:
-        """Make sequence ``seq`` able to hold ``token_num`` tokens, taking only
-        the missing pages from ``pool``.  Must run before any forward that
-        writes those positions; kernels do no bounds checks."""
-        need = (token_num + PAGE_SIZE - 1) // PAGE_SIZE
-        assert need <= self.max_pages, (
-            f"{token_num} tokens need {need} pages, block table holds {self.max_pages}"
+        """Let sequence ``seq`` hold ``token_num`` tokens, taking only the missing
+        pages from ``pool``.  Call it before any forward that writes those
+        positions: the kernels do no bounds checks."""
+        want = -(-token_num // PAGE_SIZE)
+        assert want <= self.max_pages, (
+            f"sequence {seq}: {token_num} tokens span {want} pages; the block table "
+            f"has {self.max_pages} per sequence"
         )
-        held = self.pages[seq]
-        if need <= len(held):
+        have = int(self._held[seq])
+        if want <= have:
             return
-        new_pages = pool.alloc(need - len(held))
-        self.block_table[seq, len(held):need] = torch.tensor(
-            new_pages, dtype=torch.int32, device=self.block_table.device
-        )
-        held.extend(new_pages)
+        self._rows[seq, have:want] = pool.alloc(want - have)
+        self._held[seq] = want
+        self.block_table[seq, have:want].copy_(torch.from_numpy(self._rows[seq, have:want]))
 
     def reserve_all(self, token_num: int, pool: PagePool) -> None:
         for seq in range(self.batch):
             self.reserve(token_num, pool, seq=seq)
 
     def release(self, pool: PagePool, *, seq: int | None = None) -> None:
-        """Return pages to the pool (all rows when ``seq`` is None) and zero the
-        released block-table rows."""
-        targets = range(self.batch) if seq is None else [seq]
-        for b in targets:
-            pool.free(self.pages[b])
-            self.pages[b] = []
+        """Give the pages of ``seq`` (every row when None) back to the pool, in
+        row order, and zero the released block-table rows."""
+        rows = range(self.batch) if seq is None else (seq,)
+        for b in rows:
+            pool.free(self._rows[b, :self._held[b]])
+            self._rows[b] = 0
+            self._held[b] = 0
         if seq is None:
             self.block_table.zero_()
         else:
             self.block_table[seq].zero_()
 
     def capacity(self, seq: int = 0) -> int:
-        return len(self.pages[seq]) * PAGE_SIZE
+        return int(self._held[seq]) * PAGE_SIZE

@@ -292,6 +292,87 @@ def test_page_pool_and_sequence_pages(pkg):
         pool.alloc(11)
 
 
+def test_page_pool_contract(pkg):
+    """Tail-first allocation, free appends at the tail, so an alloc/free cycle
+    hands back the same ids; reset restores the initial order; over-allocation
+    is an AssertionError raised on the host (engine/paging.py:71-103)."""
+    pool = pkg.PagePool(6)
+    assert pool.alloc(0) == [] and pool.num_free == 6
+    a = pool.alloc(2)
+    assert a == [4, 5] and pool.num_free == 4
+    b = pool.alloc(3)
+    assert b == [1, 2, 3]
+    pool.free(a)
+    assert pool.alloc(2) == a                 # same ids after a cycle
+    pool.free(b)
+    pool.free([])
+    assert pool.num_free == 4 and pool.alloc(1) == [3]
+    with pytest.raises(AssertionError):
+        pool.alloc(4)
+    pool.reset()
+    assert pool.num_free == 6 and pool.alloc(6) == [0, 1, 2, 3, 4, 5]
+
+
+def test_sequence_pages_contract_random_walk(pkg):
+    """Random reserve/release sequence against a list model of the reference's
+    semantics: reserve takes only the missing pages (from the pool's tail),
+    the device table row equals the held pages, release of one row returns
+    its pages in row order and zeroes only that row."""
+    gen = np.random.default_rng(3)
+    B, max_pages = 4, 6
+    pool = pkg.PagePool(20)
+    sp = pkg.SequencePages(max_pages, batch=B, device="cpu")
+    free_model = list(range(20))
+    held_model = [[] for _ in range(B)]
+    for _ in range(300):
+        b = int(gen.integers(B))
+        if gen.random() < 0.7:
+            tokens = int(gen.integers(0, max_pages * 16 + 1))
+            need = -(-tokens // 16)
+            missing = need - len(held_model[b])
+            if missing > len(free_model):
+                with pytest.raises(AssertionError):
+                    sp.reserve(tokens, pool, seq=b)
+                continue
+            sp.reserve(tokens, pool, seq=b)
+            if missing > 0:
+                held_model[b] += free_model[-missing:]
+                del free_model[-missing:]
+        else:
+            sp.release(pool, seq=b)
+            free_model += held_model[b]
+            held_model[b] = []
+        assert sp.pages == held_model
+        assert pool.num_free == len(free_model)
+        for r in range(B):
+            row = sp.block_table[r].tolist()
+            n = len(held_model[r])
+            assert row[:n] == held_model[r] and not any(row[n:])
+            assert sp.capacity(r) == 16 * n
+    with pytest.raises(AssertionError):
+        sp.reserve(max_pages * 16 + 1, pool, seq=0)
+    sp.release(pool)
+    assert pool.num_free == 20 and not sp.block_table.any()
+
+
+def test_physical_rows_matches_page_layout(pkg):
+    """physical_rows(bt, t, H) addresses token t, head h of a pool through
+    kc.view(-1, D): checked by direct indexing kc[bt[t // 16], h, t % 16] on a
+    shuffled table and against the oracle's row_index."""
+    gen = torch.Generator().manual_seed(4)
+    H, D, npages = 2, 8, 12
+    kc = torch.randn(npages, H, 16, D, generator=gen)
+    bt = torch.randperm(npages, generator=gen)[:7].to(torch.int32)
+    t = torch.tensor([0, 1, 15, 16, 17, 50, 111], dtype=torch.int64)
+    rows = pkg.physical_rows(bt, t, H)
+    assert rows.shape == (len(t), H) and rows.dtype == torch.int64
+    flat = kc.view(-1, D)
+    for i, ti in enumerate(t.tolist()):
+        for h in range(H):
+            assert torch.equal(flat[rows[i, h]], kc[int(bt[ti // 16]), h, ti % 16])
+            assert int(rows[i, h]) == orc.row_index(bt, ti, h, H)
+
+
 def test_attn_caches_sizing(pkg):
     c = pkg.allocate_attn_caches(2, 100, batch=3, device="cpu")
     assert c.k_caches[0].shape == (3 * 8, 2, 16, 256)   # (ceil(100/16)+1) * 3 pages

@@ -162,3 +162,64 @@ def test_swiglu_gemm_equals_separate_ops(pkg, dev, M):
     y_ref = pkg.gemm_2d(pkg.swiglu(gu[:, :I], gu[:, I:]), w)
     torch.cuda.synchronize()
     assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
+
+
+@pytest.mark.parametrize("M", [1, 32, 64])
+@pytest.mark.parametrize("N,K", [(1024, 1152), (1024, 1408), (512, 2304), (5120, 1152)])
+def test_gemm_2d_skinny_odd_k(pkg, dev, M, N, K):
+    """K values whose per-wave slice is not a power-of-two multiple of 128:
+    the wave count must keep every wave's slice a multiple of 32 columns, or
+    the 32-column tail loop would run into the next wave's slice (and past
+    the row end on the last row).  Oracle bound, split and unsplit."""
+    say(f"gemm_2d skinny odd K M={M} N={N} K={K}")
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.05).bfloat16()
+    xd, wd = x.to(dev), w.to(dev)
+    check(pkg.gemm_2d(xd, wd), x, w)
+    check(_gemm_no_workspace(pkg, xd, wd), x, w)
+
+
+@pytest.mark.parametrize("M", [1, 32, 64])
+def test_rmsnorm_gemm_odd_k_vs_oracle(pkg, dev, M):
+    """wy_gemm_2d_rmsnorm at K=2304 (nine 256-column chunks, a width the
+    standalone qwen_rmsnorm op does not take) against the oracle chain
+    rmsnorm -> fp64 GEMM.  The normed operand may differ from the oracle's by
+    one bf16 rounding where the fp32 sums of squares round differently, so the
+    bound adds 1e-2 absolute to the one-rounding relative term."""
+    say(f"rmsnorm_gemm K=2304 M={M}")
+    g = torch.Generator().manual_seed(M + 2304)
+    K, N = 2304, 1024
+    x = torch.randn(M, K, generator=g).bfloat16()
+    r = torch.randn(M, K, generator=g).bfloat16()
+    nw = (torch.randn(K, generator=g) * 0.1).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.03).bfloat16()
+    y, t = pkg.rmsnorm_gemm_2d(x.to(dev), r.to(dev), nw.to(dev), 1e-6, w.to(dev))
+    t_ref = (x.float() + r.float()).bfloat16()
+    assert torch.equal(t.cpu(), t_ref)
+    ref = orc.gemm_2d(orc.qwen_rmsnorm(t_ref, nw, 1e-6), w)
+    got = y.cpu().double()
+    err = (got - ref).abs()
+    assert (err <= 2.0 ** -8 * ref.abs() + 1e-2).all(), f"max err {err.max():.3e}"
+
+
+def test_fused_prologue_gemms_accept_unaligned_row_views(pkg, dev):
+    """Row views that start off a 16-byte boundary (a column slice at an odd
+    offset) are copied to aligned rows by the ops, not rejected."""
+    say("rmsnorm_gemm / swiglu_gemm on unaligned row views")
+    g = torch.Generator(device=dev).manual_seed(11)
+    wide = torch.randn(8, 1024 + 3, device=dev, generator=g).to(torch.bfloat16)
+    x = wide[:, 3:]
+    nw = (torch.randn(1024, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    w = (torch.randn(512, 1024, device=dev, generator=g) * 0.03).to(torch.bfloat16)
+    y, _ = pkg.rmsnorm_gemm_2d(x, None, nw, 1e-6, w)
+    assert torch.equal(y, pkg.gemm_2d(pkg.qwen_rmsnorm(x.contiguous(), nw, 1e-6), w))
+    y_r, t_r = pkg.rmsnorm_gemm_2d(x, x, nw, 1e-6, w)
+    t_ref = pkg.residual_add(x.contiguous(), x.contiguous())
+    assert torch.equal(t_r, t_ref)
+    assert torch.equal(y_r, pkg.gemm_2d(pkg.qwen_rmsnorm(t_ref, nw, 1e-6), w))
+    gu_wide = torch.randn(8, 2 * 1024 + 5, device=dev, generator=g).to(torch.bfloat16)
+    gu = gu_wide[:, 5:]
+    y2 = pkg.swiglu_gemm_2d(gu, w)
+    assert torch.equal(y2, pkg.gemm_2d(pkg.swiglu(gu[:, :1024].contiguous(),
+                                                  gu[:, 1024:].contiguous()), w))

@@ -82,3 +82,39 @@ def test_lm_head_argmax_first_index_on_ties(pkg, dev):
     ref = torch.argmax(mo.lm_head_logits(h, w), dim=-1)
     got = pkg.lm_head_argmax(h.to(dev), w.to(dev), False)
     assert torch.equal(got.cpu(), ref)
+
+
+def test_lm_head_argmax_nan_and_inf_rows_give_valid_index(pkg, dev):
+    """Rows whose logits are all NaN or all -inf, and a vocabulary with NaN
+    rows: the index is torch.argmax's (NaN ranks highest, first one wins; an
+    all -inf row gives 0), never an out-of-range id that the next step's
+    embedding gather would follow."""
+    say("lm_head_argmax NaN / -inf rows")
+    gen = torch.Generator().manual_seed(13)
+    V, K = 3000, 256
+    w = torch.randn(V, K, generator=gen).to(torch.bfloat16)
+    h = torch.randn(4, K, generator=gen).to(torch.bfloat16)
+    h[1] = float("nan")
+    got = pkg.lm_head_argmax(h.to(dev), w.to(dev), False).cpu()
+    ref = torch.argmax(mo.lm_head_logits(h, w), dim=-1)
+    assert int(got[1]) == 0 and torch.equal(got, ref)
+    w_nan = w.clone()
+    w_nan[1777] = float("nan")
+    w_nan[2500] = float("nan")
+    got = pkg.lm_head_argmax(h.to(dev), w_nan.to(dev), False).cpu()
+    assert torch.equal(got, torch.argmax(mo.lm_head_logits(h, w_nan), dim=-1))
+    assert got.tolist() == [1777, 0, 1777, 1777]
+    w_inf = torch.full((V, K), float("-inf")).to(torch.bfloat16)
+    h_pos = (torch.rand(3, K, generator=gen) + 0.5).to(torch.bfloat16)
+    got = pkg.lm_head_argmax(h_pos.to(dev), w_inf.to(dev), False).cpu()
+    assert got.tolist() == [0, 0, 0]
+
+
+def test_embedding_gather_out_of_range_ids_give_zero_rows(pkg, dev):
+    say("embedding gather out-of-range ids")
+    gen = torch.Generator().manual_seed(2)
+    w = torch.randn(100, 256, generator=gen).to(torch.bfloat16)
+    ids = torch.tensor([5, -1, 100, 2 ** 31 - 1, 99], dtype=torch.int64)
+    out = pkg.embedding_gather(ids.to(dev), w.to(dev)).cpu()
+    assert torch.equal(out[0], w[5]) and torch.equal(out[4], w[99])
+    assert not out[1:4].any()
