@@ -1,21 +1,26 @@
 """Benchmark of the MI355X full-attention hot path.
 
 Headline (``value``): paged GQA decode step at B=32, per-sequence contexts
-uniform in [128, 2048] (seeded), 8 q / 2 kv heads, d=256, randperm page table,
-one step = K/V append + split-K partial + merge + sigmoid gate pack, captured
-in one HIP graph and replayed.  ``value`` is algorithmic HBM GB/s of the step
-(KV bytes read + q/gate/out/append/page-table bytes, split scratch excluded).
+uniform in [128, 2048] (seeded), 8 q / 2 kv heads, d=256, randperm page table.
+One step is the decode attention of the model's 6 full-attention layers, each
+with its own K/V page pools (~480 MB in all, twice the 256 MB MALL, so K/V
+come from HBM), sharing the block table and positions; per layer one launch
+does K/V append + split-K partial + merge + sigmoid gate.  The step is one HIP
+graph replay; ``--steps`` replays are timed per window with HIP events on the
+replay stream, windows repeat until >= 50 ms were timed, and the median window
+is reported.  ``value`` is algorithmic HBM GB/s of the step (KV bytes read +
+q/gate/out/append/page-table bytes, split scratch excluded).
 
-Also reported (``extra``): config 1 latency, config 3 and 4 varlen prefill
-TFLOP/s, config 5 long-context decode GB/s, the attention block / layer, the
-config-3 HBM-bound companions, ``gemm_2d`` next to hipBLASLt, the Gated
-DeltaNet kernels (``gdn``) and the whole 24-layer model (``model``: LM-head
-argmax, graph-replayed decode step at B=1 / 32, packed prefill of 32 x 128
-tokens); ``--only a,b`` selects extras by name.  ``roofline`` is the split kernel
-timed alone with HIP events on its stream; ``cpu_baseline`` is the CPU oracle
-on a bounded sample of the same workload.
+Also reported: ``roofline`` (the step kernel: average launch = step time / 6),
+``roofline_prefill`` (the varlen causal prefill kernel at configs 4 and 3),
+``cpu_baseline`` / ``cpu_baseline_prefill`` (the CPU oracle on all host cores,
+median of repetitions), and ``extra``: config 1 latency, configs 3/4 prefill,
+config 5 long-context decode, the attention block / layer, the config-3
+HBM-bound companions, ``gemm_2d`` next to hipBLASLt, the Gated DeltaNet
+kernels (``gdn``) and the whole 24-layer model (``model``); ``--only a,b``
+selects extras by name.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--only ...]
 """
 
 from __future__ import annotations
@@ -35,6 +40,7 @@ sys.path.insert(0, str(ROOT))
 
 HQ, HKV, D, PAGE = 8, 2, 256, 16
 HBM_PEAK_GBS = 8000.0
+ATTN_LAYERS = 6   # full-attention layers of Qwen3.5-0.8B (every 4th of 24)
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -86,8 +92,21 @@ def split_kernel_bytes(lens):
         + 8 * B
 
 
+def config4_lengths():
+    """24 lengths log-uniform in [16, 4096], seed 4 (~18.6k tokens)."""
+    g4 = torch.Generator().manual_seed(4)
+    lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
+    return [int(x) for x in lens4.round().tolist()]
+
+
 def prefill_flops(lengths):
     return sum(n * (n + 1) // 2 for n in lengths) * 4 * D * HQ
+
+
+def profile_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 counters, if committed."""
+    f = ROOT / "profiles" / f"{name}_traffic.json"
+    return json.loads(f.read_text()).get("hbm_bytes_per_launch") if f.exists() else None
 
 
 # ------------------------------------------------------------------ timing
@@ -96,28 +115,63 @@ STEPS_PER_GRAPH = 8
 
 
 def time_graph(fn, steps, warmup, per_graph=STEPS_PER_GRAPH):
-    """Capture `per_graph` back-to-back calls of fn in one graph (as a decode
-    step graph holds every attention layer), replay it until `steps` calls
-    have run after `warmup` untimed ones; return ms per call, wall clock
-    bracketed by device synchronisation."""
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
+    """`per_graph` back-to-back calls of fn in one graph (as a decode step graph
+    holds every attention layer), replayed in windows of ceil(steps/per_graph)
+    replays after ceil(warmup/per_graph) untimed ones; median window, ms per
+    call (HIP events on the replay stream)."""
+    stream = torch.cuda.Stream()
+    g = capture(lambda: [fn() for _ in range(per_graph)], stream)
+    with torch.cuda.stream(stream):
+        ev, _ = time_steps(g, max(1, -(-steps // per_graph)), -(-warmup // per_graph))
+    return median(ev) / per_graph
+
+
+def capture(fn, stream):
+    """Warm fn up once on `stream`, then capture one call of it into a graph on
+    that same stream (so per-stream workspaces exist before the capture)."""
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
         fn()
-    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for _ in range(per_graph):
-            fn()
-    for _ in range(max(1, warmup // per_graph)):
-        g.replay()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
     torch.cuda.synchronize()
-    reps = max(1, steps // per_graph)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        g.replay()
+    return g
+
+
+def time_steps(graph, steps, warmup, min_total_s=0.05, min_windows=5):
+    """`warmup` untimed replays of `graph` (one step each), then windows of
+    exactly `steps` replays, each bracketed by device synchronisation and
+    timed with HIP events recorded on the stream the replays run on (plus the
+    host clock).  Windows repeat until at least `min_windows` ran and
+    `min_total_s` of replays was timed.  Returns per-window ms per step
+    (events) and per-window wall ms per step."""
+    for _ in range(warmup):
+        graph.replay()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / (reps * per_graph)
+    ev, wall, total = [], [], 0.0
+    while len(ev) < min_windows or total < min_total_s:
+        st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        st.record()
+        for _ in range(steps):
+            graph.replay()
+        en.record()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        total += dt
+        ev.append(st.elapsed_time(en) / steps)
+        wall.append(dt * 1e3 / steps)
+    return ev, wall
+
+
+def median(xs):
+    ys = sorted(xs)
+    n = len(ys)
+    return ys[n // 2] if n % 2 else 0.5 * (ys[n // 2 - 1] + ys[n // 2])
 
 
 def time_events(fn, iters, warmup=3):
@@ -173,7 +227,7 @@ def main():
                     help="untimed steps first")
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
-    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-gemm",
+    ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-prefill3", "pmc-gemm",
                              "pmc-gdn"],
                     help="pmc-*: eager launches only, for rocprofv3 counter runs")
     args = ap.parse_args()
@@ -191,47 +245,67 @@ def main():
     pkg._lib.load()
 
     # ---- headline: config 2 decode step ----------------------------------------
+    # One step = the decode attention of every full-attention layer of the
+    # model (ATTN_LAYERS): each layer has its own page pools (80 MB of K/V at
+    # config 2) and its own q / new K,V / gate, while the sequences (block
+    # table, pos) are shared, as in the engine.  The 6 pools (~480 MB) exceed
+    # the 256 MB MALL, so replays read K/V from HBM, not from the cache.
     gen = torch.Generator().manual_seed(2)
     lens = torch.randint(128, 2049, (32,), generator=gen).tolist()
-    w = decode_workload(lens, dev, seed=2)
+    layers = [decode_workload(lens, dev, seed=2 if i == 0 else 200 + i)
+              for i in range(ATTN_LAYERS)]
+    for lw in layers[1:]:
+        lw["bt"], lw["pos"] = layers[0]["bt"], layers[0]["pos"]
+    w = layers[0]
     scratch = pkg.allocate_split_scratch(HQ, D, batch=32, device=dev)
 
     m_p, l_p, acc_p = scratch
-    gate3 = w["gate"][0].permute(1, 0, 2)  # [B, Hq, D] view
+
+    def layer_step(lw):
+        return torch.ops.wy_lib.paged_gqa_attention_decode_fused(
+            lw["q"], lw["kn"], lw["vn"], lw["kc"], lw["vc"], lw["bt"], lw["pos"], m_p, l_p,
+            acc_p, scratch.counters, lw["gate"][0].permute(1, 0, 2))
 
     def step():
-        return torch.ops.wy_lib.paged_gqa_attention_decode_fused(
-            w["q"], w["kn"], w["vn"], w["kc"], w["vc"], w["bt"], w["pos"], m_p, l_p, acc_p,
-            scratch.counters, gate3)
+        for lw in layers:
+            layer_step(lw)
 
-    def step_three_ops():
+    def step_one_pool():
+        return layer_step(w)
+
+    def step_three_ops(lw):
         ctx = pkg.call_paged_gqa_attention_decode_triton(
-            w["q"], w["kn"], w["vn"], w["kc"], w["vc"], w["bt"], w["pos"], tuple(scratch))
-        return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), w["gate"])
+            lw["q"], lw["kn"], lw["vn"], lw["kc"], lw["vc"], lw["bt"], lw["pos"], tuple(scratch))
+        return pkg.attention_gate_pack(ctx.permute(1, 0, 2).unsqueeze(0), lw["gate"])
 
     if args.mode == "pmc-step":
         for _ in range(10):
             step()
         torch.cuda.synchronize()
-        print(json.dumps({"mode": "pmc-step", "algorithmic_bytes": decode_bytes(lens)}))
+        print(json.dumps({"mode": "pmc-step", "launches": 10 * ATTN_LAYERS,
+                          "algorithmic_bytes_per_launch": decode_bytes(lens)}))
         return
-    if args.mode == "pmc-prefill":
-        g4 = torch.Generator().manual_seed(4)
-        lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
-        lens4 = [int(x) for x in lens4.round().tolist()]
-        gq = torch.Generator(device=dev).manual_seed(4)
-        tot = sum(lens4)
-        qp = torch.randn(tot, HQ, D, device=dev, generator=gq).to(torch.bfloat16)
-        kp = torch.randn(tot, HKV, D, device=dev, generator=gq).to(torch.bfloat16)
-        vp = torch.randn(tot, HKV, D, device=dev, generator=gq).to(torch.bfloat16)
-        cu_l = [0]
-        for n_ in lens4:
-            cu_l.append(cu_l[-1] + n_)
-        cu4 = torch.tensor(cu_l, dtype=torch.int32, device=dev)
-        for _ in range(3):
-            pkg.gqa_attention_varlen_causal(qp, kp, vp, cu4, max(lens4))
+    if args.mode in ("pmc-prefill", "pmc-prefill3"):
+        # config 4 (pmc-prefill) or config 3 (pmc-prefill3): 0.3 s of eager
+        # launches first (steady clocks), then 20 more; counters per dispatch
+        if args.mode == "pmc-prefill3":
+            lens_p, seed_p = [128] * 32, 3
+        else:
+            lens_p, seed_p = config4_lengths(), 4
+        qp, kp, vp, cup = prefill_inputs(dev, lens_p, seed_p)
+        run_p = lambda: pkg.gqa_attention_varlen_causal(qp, kp, vp, cup, max(lens_p))
+        t_end = time.perf_counter() + 0.3
+        n_calls = 0
+        while time.perf_counter() < t_end:
+            run_p()
+            torch.cuda.synchronize()
+            n_calls += 1
+        for _ in range(20):
+            run_p()
         torch.cuda.synchronize()
-        print(json.dumps({"mode": "pmc-prefill", "flops": prefill_flops(lens4)}))
+        print(json.dumps({"mode": args.mode, "flops": prefill_flops(lens_p),
+                          "calls": n_calls + 20,
+                          "min_hbm_bytes": sum(lens_p) * (HQ * D * 4 + HKV * D * 4)}))
         return
     if args.mode == "pmc-gemm":
         # gemm_2d on the decode (B=32) and prefill (T=4096) projection shapes,
@@ -280,18 +354,30 @@ def main():
                           "bytes_written": 256 << 20}))
         return
 
-    log(f"decode config2: sum(L)={sum(lens)} B=32")
-    ms = time_graph(step, args.steps, args.warmup)
-    step_bytes = decode_bytes(lens)
+    log(f"decode config2: sum(L)={sum(lens)} B=32, {ATTN_LAYERS} layers per step")
+    stream = torch.cuda.Stream()
+    g_step = capture(step, stream)
+    with torch.cuda.stream(stream):
+        ev, wall = time_steps(g_step, args.steps, args.warmup)
+    ms = median(ev)
+    layer_bytes = decode_bytes(lens)
+    step_bytes = ATTN_LAYERS * layer_bytes
     gbs = step_bytes / (ms * 1e-3) / 1e9
-    # the step is one kernel: time it alone, back to back inside one graph
-    kern_ms = time_graph_events(step, 100)
-    kern_gbs = step_bytes / (kern_ms * 1e-3) / 1e9
-    ms3 = time_graph(step_three_ops, args.steps, args.warmup)
-    traffic = None
-    tfile = ROOT / "profiles" / "decode_step_config2_traffic.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    # the step is ATTN_LAYERS launches of one kernel, back to back in the graph
+    kern_ms = ms / ATTN_LAYERS
+    kern_gbs = layer_bytes / (kern_ms * 1e-3) / 1e9
+    # the same kernel replayed on one pool (80 MB, stays in the MALL)
+    g_one = capture(step_one_pool, stream)
+    with torch.cuda.stream(stream):
+        ev1, _ = time_steps(g_one, 100, 200)
+    ms_one = median(ev1)
+    # the reference's three-op path, same rotated pools
+    g3 = capture(lambda: [step_three_ops(lw) for lw in layers], stream)
+    with torch.cuda.stream(stream):
+        ev3, _ = time_steps(g3, max(args.steps, 20), max(args.warmup, 20))
+    ms3 = median(ev3) / ATTN_LAYERS
+    del g_one, g3
+    traffic = profile_traffic("decode_step_config2")
 
     result = {
         "metric": "decode-attn HBM GB/s (B=32 paged GQA decode step, contexts U[128,2048])",
@@ -301,26 +387,39 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
-        "us_per_step": round(ms * 1e3, 2),
+        "us_per_layer": round(kern_ms * 1e3, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) bf16 q/k/v/gate, randperm page table)",
-        "config": {"workload": "config2: paged GQA decode step B=32, L~U[128,2048], "
-                               "8q/2kv heads, d=256, 16-token pages",
+        "config": {"workload": f"config2: paged GQA decode step B=32, L~U[128,2048], "
+                               f"8q/2kv heads, d=256, 16-token pages; one step = the "
+                               f"{ATTN_LAYERS} full-attention layers of the model, each "
+                               f"with its own K/V page pools",
                    "global_batch": 32, "sum_context_tokens": sum(lens),
-                   "step": "one-launch append+split+merge+gate; 8 steps per HIP graph, "
-                           "as a decode graph holds every attention layer",
+                   "layers_per_step": ATTN_LAYERS,
+                   "working_set_MB": round(ATTN_LAYERS * 2 * w["kc"].numel() * 2 / 1e6, 1),
+                   "step": "per layer one launch: append + split-K + merge + sigmoid gate; "
+                           "the step is one HIP graph replay",
+                   "timing": f"{len(ev)} windows of exactly {args.steps} steps after "
+                             f"{args.warmup} untimed steps; HIP events on the replay stream; "
+                             f"median window (wall-clock median "
+                             f"{median(wall) * 1e3:.2f} us/step)",
                    "parallelism": "single GPU"},
-        "roofline": {"kernel": "paged_decode_split_kernel<true, 4> (fused step)", "bound": "hbm",
+        "roofline": {"kernel": "paged_decode_split_kernel<true, 4> (one-launch step)",
+                     "bound": "hbm",
                      "achieved": round(kern_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": step_bytes,
-                     "avg_launch_us": round(kern_ms * 1e3, 3)},
-        "three_op_path_us_per_step": round(ms3 * 1e3, 2),
+                     "algorithmic_bytes_per_launch": layer_bytes,
+                     "avg_launch_us": round(kern_ms * 1e3, 3),
+                     "single_pool_mall_warm_us": round(ms_one * 1e3, 3),
+                     "single_pool_mall_warm_frac": round(
+                         layer_bytes / (ms_one * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "three_op_path_us_per_layer": round(ms3 * 1e3, 2),
     }
-    log(f"  step {ms*1e3:.2f} us {gbs:.0f} GB/s; kernel {kern_ms*1e3:.2f} us; 3-op {ms3*1e3:.2f} us")
+    log(f"  step {ms*1e3:.2f} us ({kern_ms*1e3:.2f} per layer) {gbs:.0f} GB/s; "
+        f"one pool {ms_one*1e3:.2f} us; 3-op {ms3*1e3:.2f} us/layer")
 
     extra = {}
     only = set(filter(None, args.only.split(",")))
@@ -390,17 +489,12 @@ def main():
         extra["config3_prefill_32x128"] = prefill_bench(pkg, dev, [128] * 32, seed=3)
     # ---- config 4: mixed lengths log-uniform [16, 4096] ------------------------
     if want("c4"):
-        g4 = torch.Generator().manual_seed(4)
-        lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
-        lens4 = [int(x) for x in lens4.round().tolist()]
-        extra["config4_prefill_mixed"] = prefill_bench(pkg, dev, lens4, seed=4)
+        extra["config4_prefill_mixed"] = prefill_bench(pkg, dev, config4_lengths(), seed=4)
     # ---- the prefill attention path after q/k norm: op sequence vs block ---------
     if want("pblock"):
         extra["config3_prefill_attention_path"] = prefill_path_bench(pkg, dev, [128] * 32, 3)
-        g4 = torch.Generator().manual_seed(4)
-        lens4 = torch.exp(torch.empty(24).uniform_(math.log(16), math.log(4096), generator=g4))
         extra["config4_prefill_attention_path"] = prefill_path_bench(
-            pkg, dev, [int(x) for x in lens4.round().tolist()], 4)
+            pkg, dev, config4_lengths(), 4)
     # ---- config 5: B=64 x 32768 ------------------------------------------------
     if want("c5"):
         w5 = decode_workload([32768] * 64, dev, seed=5, kv_scale=0.5)
@@ -446,17 +540,42 @@ def main():
     if want("gdn"):
         extra["gdn"] = gdn_bench(pkg, dev)
 
+    # ---- prefill roofline: the varlen causal kernel at configs 4 and 3 ----------
+    rp = {}
+    c4 = extra.get("config4_prefill_mixed")
+    if c4:
+        rp["config4"] = {
+            "kernel": "varlen_causal_prefill_kernel (queue launch)", "bound": "mfma",
+            "achieved": c4["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": c4["frac_of_mfma_peak"], "traffic": profile_traffic("prefill_config4"),
+            "algorithmic_flops_per_launch": int(c4["GFLOP"] * 1e9),
+            "avg_launch_us": c4["us"]}
+    c3 = extra.get("config3_prefill_32x128")
+    if c3:
+        rp["config3"] = {
+            "kernel": "varlen_causal_prefill_kernel (direct launch)",
+            "bound": "hbm (arithmetic intensity 51.6 flop/B < ridge 312)",
+            "achieved": c3["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": c3["frac_of_mfma_peak"],
+            "attainable": c3["attainable_TFLOP/s"], "frac_of_attainable": c3["frac_of_attainable"],
+            "traffic": profile_traffic("prefill_config3"),
+            "algorithmic_flops_per_launch": int(c3["GFLOP"] * 1e9),
+            "min_hbm_bytes_per_launch": c3["min_hbm_bytes"],
+            "avg_launch_us": c3["us"]}
+    if rp:
+        result["roofline_prefill"] = rp
     if extra:
         result["extra"] = extra
 
     # ---- CPU baseline: oracle on a bounded sample of config 2 -------------------
     if not args.quick and (not only or "cpu" in only):
         result["cpu_baseline"] = cpu_baseline(w, lens)
+        result["cpu_baseline_prefill"] = cpu_baseline_prefill(dev)
 
     print(json.dumps(result), flush=True)
 
 
-def prefill_bench(pkg, dev, lengths, seed):
+def prefill_inputs(dev, lengths, seed):
     gen = torch.Generator(device=dev).manual_seed(seed)
     total = sum(lengths)
 
@@ -467,7 +586,13 @@ def prefill_bench(pkg, dev, lengths, seed):
     cu_list = [0]
     for n in lengths:
         cu_list.append(cu_list[-1] + n)
-    cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
+    return q, k, v, torch.tensor(cu_list, dtype=torch.int32, device=dev)
+
+
+def prefill_bench(pkg, dev, lengths, seed):
+    """Varlen causal prefill kernel alone, graph-timed with steady clocks."""
+    q, k, v, cu = prefill_inputs(dev, lengths, seed)
+    total = sum(lengths)
     mx = max(lengths)
 
     def run():
@@ -480,6 +605,7 @@ def prefill_bench(pkg, dev, lengths, seed):
     attain = min(MFMA_BF16_PEAK_TFLOPS, fl / (min_bytes / (HBM_PEAK_GBS * 1e9)) / 1e12)
     log(f"prefill {len(lengths)} seqs total {total}: {ms*1e3:.1f} us {tf:.1f} TFLOP/s")
     return {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "GFLOP": round(fl / 1e9, 3),
+            "min_hbm_bytes": min_bytes,
             "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "attainable_TFLOP/s": round(attain, 1), "frac_of_attainable": round(tf / attain, 4),
             "total_tokens": total, "lengths": lengths if len(lengths) <= 32 else None}
@@ -729,27 +855,55 @@ def gemm_bench(pkg, dev):
     return out
 
 
+def _timed_median(fn, budget_s, min_reps=3):
+    """Median seconds of fn over repetitions filling about budget_s (at least
+    min_reps), after one untimed call."""
+    fn()
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < min_reps or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return median(ts), len(ts)
+
+
 def cpu_baseline(w, lens):
-    """CPU oracle (fp32 torch, the build's own restatement) on the first
-    sequences of the config-2 workload, repeated for >= 10 s."""
+    """The CPU oracle (fp32 torch restatement of the same math, the build's own
+    port) on the whole config-2 decode step of one layer: gather of every
+    sequence's pages, softmax(q K^T / 16) V per KV group.  All host cores
+    (torch.set_num_threads(os.cpu_count())), median of the repetitions that
+    fill ~10 s."""
     from oracle import attention_oracle as orc
 
-    cores = torch.get_num_threads()
-    nseq = 8
-    sample = lens[:nseq]
-    q = w["q"][:nseq].cpu()
-    kc, vc = w["kc"].cpu(), w["vc"].cpu()
-    bt = w["bt"][:nseq].cpu()
-    orc.paged_decode(q, kc, vc, bt, sample)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 10.0:
-        orc.paged_decode(q, kc, vc, bt, sample)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
-    gbs = split_kernel_bytes(sample) / dt / 1e9
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    q, kc, vc, bt = w["q"].cpu(), w["kc"].cpu(), w["vc"].cpu(), w["bt"].cpu()
+    dt, reps = _timed_median(lambda: orc.paged_decode(q, kc, vc, bt, lens), 10.0)
+    gbs = split_kernel_bytes(lens) / dt / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{nseq} of the 32 config-2 sequences (sum L={sum(sample)}), "
-                      f"{reps} reps, {dt*1e3:.2f} ms each",
+            "sample": f"one layer's decode attention of all 32 config-2 sequences "
+                      f"(sum L={sum(lens)}); median of {reps} reps: {dt*1e3:.1f} ms "
+                      f"(GPU: one launch of the same step)",
+            "ms_per_sample": round(dt * 1e3, 3)}
+
+
+def cpu_baseline_prefill(dev):
+    """The CPU oracle's varlen causal attention on the whole config-3 batch
+    (32 x 128 tokens, the same seeded inputs as the GPU leg), all host cores,
+    median of the repetitions that fill ~10 s; TFLOP/s over the causal FLOPs."""
+    from oracle import attention_oracle as orc
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    lengths = [128] * 32
+    q, k, v, cu = prefill_inputs(dev, lengths, seed=3)
+    q, k, v, cu = q.cpu(), k.cpu(), v.cpu(), cu.cpu()
+    dt, reps = _timed_median(lambda: orc.varlen_causal(q, k, v, cu), 10.0)
+    tf = prefill_flops(lengths) / dt / 1e12
+    return {"value": round(tf, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"config 3 whole (32 x 128 tokens, {prefill_flops(lengths)/1e9:.3f} "
+                      f"GFLOP); median of {reps} reps: {dt*1e3:.1f} ms",
             "ms_per_sample": round(dt * 1e3, 3)}
 
 
