@@ -37,6 +37,7 @@ extern "C" {
 #define WY_E_SHAPE (-2)       /* a size is out of the supported range           */
 #define WY_E_LAYOUT (-3)      /* a stride / alignment the kernel cannot address */
 #define WY_E_UNSUPPORTED (-4) /* head_dim / group size without a kernel         */
+#define WY_E_CAPACITY (-5)    /* larger than a fixed-capacity entry point holds */
 
 /* Human-readable text for a return code (static storage). */
 const char *wy_status_string(int code);
@@ -140,6 +141,35 @@ int wy_paged_decode_step(const void *q, const int64_t *q_strides, const void *k_
                          const int64_t *out_strides, int batch, int num_q_heads,
                          int num_kv_heads, int head_dim, int max_pages,
                          int min_pages_per_split, void *stream);
+
+/*
+ * wy_paged_decode_step without a caller workspace: the split partials and
+ * merge counters live in a static device array of the library (64 MiB +
+ * 514 KiB on each GPU the library is used on, held until the process ends),
+ * so the call allocates nothing and needs no scratch argument.  Same
+ * arguments, semantics and results (bit for bit) as wy_paged_decode_step
+ * otherwise.  batch * num_q_heads must not exceed
+ * wy_paged_decode_step_noalloc_max_rows() (512), else WY_E_CAPACITY and
+ * nothing is launched.  The first call on a device resolves the array's
+ * address and clears its counters on `stream`.  All calls on one GPU share
+ * the array: calls that may overlap on one GPU (concurrent streams, host
+ * threads) race.  No counterpart in the reference; for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid allocation).
+ */
+int wy_paged_decode_step_noalloc(const void *q, const int64_t *q_strides, const void *k_new,
+                                 const void *v_new, const int64_t *kn_strides,
+                                 const int64_t *vn_strides, void *k_cache, void *v_cache,
+                                 const int64_t *kc_strides, const int64_t *vc_strides,
+                                 const int32_t *block_table, int64_t bt_stride0,
+                                 const int64_t *pos, const void *gate,
+                                 const int64_t *gate_strides, void *out,
+                                 const int64_t *out_strides, int batch, int num_q_heads,
+                                 int num_kv_heads, int head_dim, int max_pages,
+                                 int min_pages_per_split, void *stream);
+
+/* The row capacity (batch * num_q_heads) of wy_paged_decode_step_noalloc. */
+int64_t wy_paged_decode_step_noalloc_max_rows(void);
 
 /*
  * Packed varlen causal GQA prefill attention on bf16 MFMA.

@@ -9,6 +9,8 @@ extern "C" const char *wy_status_string(int code) {
     case WY_E_LAYOUT: return "a stride or alignment the kernel cannot address";
     case WY_E_UNSUPPORTED:
       return "no kernel for this head_dim / group size (built for head_dim 256, 4 query heads per KV head)";
+    case WY_E_CAPACITY:
+      return "the problem exceeds the fixed capacity of this entry point's static scratch";
     default:
       return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }

@@ -32,6 +32,7 @@
 // With min_pps = 1 this is exactly the reference partition
 // (gqa_attention_decode_paged.py:675-682, 779-784); a larger min_pps trades
 // split count for less fp32 scratch traffic.
+#include <mutex>
 #include <type_traits>
 
 #include "wy_common.h"
@@ -924,4 +925,92 @@ extern "C" int wy_paged_decode_block(const void *q_raw, const int64_t *qs, const
   a.rope_dim = rotary_dim;
   return launch_split<true, true>(a, batch, num_kv_heads, max_pages, min_pages_per_split,
                                   stream);
+}
+
+// ---- decode step without a caller workspace -----------------------------------
+//
+// The split partials and merge counters of wy_paged_decode_step live in this
+// file-scope device array instead of caller memory: m and l [rows][128] fp32,
+// acc [rows][128][256] fp32 and the counters, for rows = batch * num_q_heads <=
+// kNoAllocMaxRows (64 MiB + 514 KiB per GPU, held until the process ends).  In
+// host code `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+namespace {
+constexpr int kNoAllocMaxRows = 512;
+constexpr size_t kNoAllocMlFloats = size_t(kNoAllocMaxRows) * kMaxSplits;
+constexpr size_t kNoAllocAccFloats = kNoAllocMlFloats * kD;
+constexpr size_t kNoAllocCounters = kNoAllocMaxRows;  // >= batch * num_kv_heads
+constexpr size_t kNoAllocBytes = (2 * kNoAllocMlFloats + kNoAllocAccFloats) * 4 +
+                                 kNoAllocCounters * 4;
+constexpr int kNoAllocMaxDevices = 64;
+
+__global__ void zero_ints_kernel(int32_t *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+std::mutex g_noalloc_mu;
+unsigned char *g_noalloc_ptr[kNoAllocMaxDevices];
+
+// Device address of this device's `scratch`, resolved on the first call; that
+// call also clears the counters on `st` (a fill kernel, ordered before the
+// step it precedes on the same stream).
+int noalloc_scratch(hipStream_t st, unsigned char **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return int(e);
+  if (dev < 0 || dev >= kNoAllocMaxDevices) return WY_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return int(e);
+    if (!p) return int(hipErrorInvalidSymbol);
+    int32_t *cnt = reinterpret_cast<int32_t *>(static_cast<unsigned char *>(p) +
+                                               (2 * kNoAllocMlFloats + kNoAllocAccFloats) * 4);
+    zero_ints_kernel<<<(int(kNoAllocCounters) + 255) / 256, 256, 0, st>>>(
+        cnt, int(kNoAllocCounters));
+    e = hipGetLastError();
+    if (e != hipSuccess) return int(e);
+    g_noalloc_ptr[dev] = static_cast<unsigned char *>(p);
+  }
+  *out = g_noalloc_ptr[dev];
+  return WY_OK;
+}
+}  // namespace
+
+extern "C" int64_t wy_paged_decode_step_noalloc_max_rows(void) { return kNoAllocMaxRows; }
+
+extern "C" int wy_paged_decode_step_noalloc(const void *q, const int64_t *qs, const void *k_new,
+                                            const void *v_new, const int64_t *kns,
+                                            const int64_t *vns, void *k_cache, void *v_cache,
+                                            const int64_t *kcs, const int64_t *vcs,
+                                            const int32_t *block_table, int64_t bt_stride0,
+                                            const int64_t *pos, const void *gate,
+                                            const int64_t *gs, void *out, const int64_t *os,
+                                            int batch, int num_q_heads, int num_kv_heads,
+                                            int head_dim, int max_pages,
+                                            int min_pages_per_split, void *stream) {
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0) return WY_E_SHAPE;
+  if (int64_t(batch) * num_q_heads > kNoAllocMaxRows) return WY_E_CAPACITY;
+  if (head_dim != kD || num_q_heads != kG * num_kv_heads) return WY_E_UNSUPPORTED;
+  if (batch == 0) return WY_OK;
+  unsigned char *base = nullptr;
+  const int rc = noalloc_scratch(static_cast<hipStream_t>(stream), &base);
+  if (rc != WY_OK) return rc;
+  float *m = reinterpret_cast<float *>(base);
+  float *l = m + kNoAllocMlFloats;
+  float *acc = l + kNoAllocMlFloats;
+  int32_t *cnt = reinterpret_cast<int32_t *>(acc + kNoAllocAccFloats);
+  // packed [batch, num_q_heads, 128(, 256)] views of the array
+  const int64_t mls[3] = {int64_t(num_q_heads) * kMaxSplits, kMaxSplits, 1};
+  const int64_t as[4] = {int64_t(num_q_heads) * kMaxSplits * kD, int64_t(kMaxSplits) * kD, kD, 1};
+  return wy_paged_decode_step(q, qs, k_new, v_new, kns, vns, k_cache, v_cache, kcs, vcs,
+                              block_table, bt_stride0, pos, m, l, acc, mls, as, cnt, gate, gs,
+                              out, os, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
+                              min_pages_per_split, stream);
 }

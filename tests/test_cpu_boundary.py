@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "wy_attn.h"
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|size_t|const char \*)\s*(wy_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int64_t|int|size_t|const char \*)\s*(wy_\w+)\(", text, re.M)))
 
 
 def test_header_declares_expected_entry_points():
@@ -34,6 +34,19 @@ def test_library_exports_every_declared_symbol(pkg):
         assert hasattr(lib, name), name
     assert set(_declared()) == set(pkg._lib.EXPORTED)
     assert lib.wy_build_info().decode().endswith("gfx950")
+
+
+def test_noalloc_step_rejects_over_capacity_before_any_launch(pkg):
+    """The scratch-free decode step refuses batch * num_q_heads above its static
+    capacity with WY_E_CAPACITY before touching the GPU (safe without one)."""
+    lib = pkg._lib.load()
+    cap = lib.wy_paged_decode_step_noalloc_max_rows()
+    assert cap == 512
+    d = ctypes.c_void_p(16)
+    s3, s4 = pkg._lib.i64_array([2048, 256, 1]), pkg._lib.i64_array([8192, 4096, 256, 1])
+    rc = lib.wy_paged_decode_step_noalloc(d, s3, d, d, s3, s3, d, d, s4, s4, d, 1, d, None,
+                                          None, d, s3, cap // 8 + 1, 8, 2, 256, 1, 16, None)
+    assert rc == -5 and b"capacity" in lib.wy_status_string(rc)
 
 
 def test_null_and_unsupported_arguments_are_rejected(pkg):
