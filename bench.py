@@ -168,6 +168,11 @@ def time_steps(graph, steps, warmup, min_total_s=0.05, min_windows=5):
     return ev, wall
 
 
+def rnd(x, scale, digits):
+    """round(x * scale, digits), None stays None."""
+    return None if x is None else round(x * scale, digits)
+
+
 def median(xs):
     ys = sorted(xs)
     n = len(ys)
@@ -271,7 +276,8 @@ def main():
             layer_step(lw)
 
     def step_one_pool():
-        return layer_step(w)
+        for _ in layers:
+            layer_step(w)
 
     def step_three_ops(lw):
         ctx = pkg.call_paged_gqa_attention_decode_triton(
@@ -366,17 +372,27 @@ def main():
     # the step is ATTN_LAYERS launches of one kernel, back to back in the graph
     kern_ms = ms / ATTN_LAYERS
     kern_gbs = layer_bytes / (kern_ms * 1e-3) / 1e9
-    # the same kernel replayed on one pool (80 MB, stays in the MALL)
-    g_one = capture(step_one_pool, stream)
-    with torch.cuda.stream(stream):
-        ev1, _ = time_steps(g_one, 100, 200)
-    ms_one = median(ev1)
-    # the reference's three-op path, same rotated pools
-    g3 = capture(lambda: [step_three_ops(lw) for lw in layers], stream)
-    with torch.cuda.stream(stream):
-        ev3, _ = time_steps(g3, max(args.steps, 20), max(args.warmup, 20))
-    ms3 = median(ev3) / ATTN_LAYERS
-    del g_one, g3
+    kv_bytes = sum(lens) * HKV * D * 2 * 2
+    ms_one = ms_floor = ms3 = None
+    if not args.quick:  # companions of the headline (a --quick run times the headline only)
+        # the same graph with all 6 launches on one pool (80 MB, stays in the MALL)
+        g_one = capture(step_one_pool, stream)
+        with torch.cuda.stream(stream):
+            ev1, _ = time_steps(g_one, 100, 200)
+        ms_one = median(ev1) / ATTN_LAYERS
+        # the streaming floor: the same 6 x 80 MB of pages read once, no math,
+        # perfectly balanced over 2048 wavefronts (wy_page_stream_read)
+        g_fl = capture(lambda: [pkg.page_stream_read(lw["kc"], lw["vc"], lw["bt"], lw["pos"])
+                                for lw in layers], stream)
+        with torch.cuda.stream(stream):
+            evf, _ = time_steps(g_fl, max(args.steps, 20), max(args.warmup, 20))
+        ms_floor = median(evf) / ATTN_LAYERS
+        # the reference's three-op path, same rotated pools
+        g3 = capture(lambda: [step_three_ops(lw) for lw in layers], stream)
+        with torch.cuda.stream(stream):
+            ev3, _ = time_steps(g3, max(args.steps, 20), max(args.warmup, 20))
+        ms3 = median(ev3) / ATTN_LAYERS
+        del g_one, g3, g_fl
     traffic = profile_traffic("decode_step_config2")
 
     result = {
@@ -413,13 +429,16 @@ def main():
                      "frac": round(kern_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": layer_bytes,
                      "avg_launch_us": round(kern_ms * 1e3, 3),
-                     "single_pool_mall_warm_us": round(ms_one * 1e3, 3),
-                     "single_pool_mall_warm_frac": round(
-                         layer_bytes / (ms_one * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
-        "three_op_path_us_per_layer": round(ms3 * 1e3, 2),
+                     "stream_floor_us": rnd(ms_floor, 1e3, 3),
+                     "stream_floor_GB/s": rnd(ms_floor and kv_bytes / ms_floor, 1e-6, 1),
+                     "frac_of_stream_floor": rnd(ms_floor and ms_floor / kern_ms, 1, 4),
+                     "single_pool_mall_warm_us": rnd(ms_one, 1e3, 3),
+                     "single_pool_mall_warm_frac": rnd(
+                         ms_one and layer_bytes / (ms_one * 1e-3) / 1e9 / HBM_PEAK_GBS, 1, 4)},
+        "three_op_path_us_per_layer": rnd(ms3, 1e3, 2),
     }
     log(f"  step {ms*1e3:.2f} us ({kern_ms*1e3:.2f} per layer) {gbs:.0f} GB/s; "
-        f"one pool {ms_one*1e3:.2f} us; 3-op {ms3*1e3:.2f} us/layer")
+        f"one pool {ms_one} ms; stream floor {ms_floor} ms; 3-op {ms3} ms/layer")
 
     extra = {}
     only = set(filter(None, args.only.split(",")))

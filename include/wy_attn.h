@@ -172,6 +172,26 @@ int wy_paged_decode_step_noalloc(const void *q, const int64_t *q_strides, const 
 int64_t wy_paged_decode_step_noalloc_max_rows(void);
 
 /*
+ * Measurement kernel: reads the K and V rows of every page a decode step
+ * attends (pages [0, ceil((pos[b]+1)/16)) of every sequence and KV head, each
+ * once) with no attention math, the pages cut into equal contiguous ranges
+ * over wy_page_stream_read_waves() wavefronts (8 per CU), one page in flight
+ * per wave.  sums[w] (fp32, one per wavefront) = the sum of every element
+ * wave w read.  Its duration is the HBM floor of the decode step's access
+ * pattern at perfect balance, the practical roofline the decode kernel is
+ * measured against.  Pools as wy_paged_decode_step with 512-byte rows
+ * (head_dim 256, unit stride).  No counterpart in the reference (a
+ * measurement of this build).
+ */
+int wy_page_stream_read(const void *k_cache, const void *v_cache, const int64_t *kc_strides,
+                        const int64_t *vc_strides, const int32_t *block_table,
+                        int64_t bt_stride0, const int64_t *pos, int batch, int num_kv_heads,
+                        int head_dim, float *sums, void *stream);
+
+/* Wavefronts (= entries of `sums`) of wy_page_stream_read. */
+int64_t wy_page_stream_read_waves(void);
+
+/*
  * Packed varlen causal GQA prefill attention on bf16 MFMA.
  *   out[t, hq, :] = softmax_{j<=i}(q_i . k_j / sqrt(D)) V  within each sequence
  * q/out [total, H_q, D], k/v [total, H_kv, D] bf16 (innermost stride must be

@@ -39,6 +39,7 @@ from .gqa_attention_decode_paged import (
     paged_kv_append,
     paged_kv_fill,
     paged_kv_fill_varlen,
+    page_stream_read,
     physical_rows,
 )
 from .depthwise_causal_conv4_decode import (

@@ -38,6 +38,7 @@ _SIGNATURES = {
     "wy_paged_decode_step_noalloc": [_vp, _c_i64p, _vp, _vp, _c_i64p, _c_i64p, _vp, _vp,
                                      _c_i64p, _c_i64p, _vp, _i64, _vp, _vp, _c_i64p, _vp,
                                      _c_i64p, _i, _i, _i, _i, _i, _i, _vp],
+    "wy_page_stream_read": [_vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp, _i, _i, _i, _vp, _vp],
     "wy_varlen_causal_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
                                  _vp, _i, _i, _i, _i, _i, _i64, _vp, _i64, _vp],
     "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,
@@ -82,7 +83,8 @@ _SIGNATURES = {
 
 # entry points returning a size (int64) rather than a status
 _SIZE_QUERIES = ("wy_varlen_causal_prefill_workspace_bytes", "wy_gemm_2d_workspace_bytes",
-                 "wy_lm_head_argmax_workspace_bytes", "wy_paged_decode_step_noalloc_max_rows")
+                 "wy_lm_head_argmax_workspace_bytes", "wy_paged_decode_step_noalloc_max_rows",
+                 "wy_page_stream_read_waves")
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES, *_SIZE_QUERIES)
 
@@ -112,8 +114,9 @@ def load() -> ctypes.CDLL:
                lib.wy_lm_head_argmax_workspace_bytes):
         fn.argtypes = [_i, _i, _i]
         fn.restype = ctypes.c_int64
-    lib.wy_paged_decode_step_noalloc_max_rows.argtypes = []
-    lib.wy_paged_decode_step_noalloc_max_rows.restype = ctypes.c_int64
+    for fn in (lib.wy_paged_decode_step_noalloc_max_rows, lib.wy_page_stream_read_waves):
+        fn.argtypes = []
+        fn.restype = ctypes.c_int64
     _lib = lib
     return lib
 

@@ -1014,3 +1014,112 @@ extern "C" int wy_paged_decode_step_noalloc(const void *q, const int64_t *qs, co
                               out, os, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
                               min_pages_per_split, stream);
 }
+
+// ---- streaming floor of the decode step's K/V reads ------------------------------
+//
+// Reads every K/V page row a decode step attends (pages [0, ceil((pos+1)/16))
+// of every sequence and KV head) exactly once, with no attention math.  The
+// units (one page of one KV head: 8 KiB of K + 8 KiB of V) are cut into equal
+// contiguous ranges over kStreamWaves wavefronts (8 per CU); a wave keeps the
+// next unit in flight while it sums the current one.  sums[w] = fp32 sum of
+// every element wave w read.  Its time is the HBM floor of the step's access
+// pattern with perfect balance: what the decode kernel is measured against.
+namespace {
+constexpr int kStreamWaves = 2048;
+constexpr int kMaxSegsStream = 1024;  // batch * H_kv
+
+__global__ __launch_bounds__(256) void page_stream_kernel(
+    const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vc, int64_t kc_p, int64_t kc_h,
+    int64_t vc_p, int64_t vc_h, const int32_t *__restrict__ bt, int64_t bt_b,
+    const int64_t *__restrict__ pos, int batch, int hkv, float *__restrict__ sums) {
+  __shared__ int prefix[kMaxSegsStream + 1];
+  const int lane = threadIdx.x & 63;
+  const int nseg = batch * hkv;
+  if (threadIdx.x < 64) {  // segment prefix sums, 64 segments per pass
+    int carry = 0;
+    if (lane == 0) prefix[0] = 0;
+    for (int c0 = 0; c0 < nseg; c0 += 64) {
+      const int sg = c0 + lane;
+      int x = sg < nseg ? (int(pos[sg / hkv]) + kPage) / kPage : 0;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+      }
+      if (sg < nseg) prefix[sg + 1] = carry + x;
+      carry += __shfl(x, 63);
+    }
+  }
+  __syncthreads();
+  const int units = prefix[nseg];
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int u0 = int(int64_t(gw) * units / kStreamWaves);
+  const int u1 = int(int64_t(gw + 1) * units / kStreamWaves);
+  int seg = 0;
+  {
+    int lo = 0, hi = nseg - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (prefix[mid] <= u0) lo = mid;
+      else hi = mid - 1;
+    }
+    seg = lo;
+  }
+  auto phys_of = [&](int u) -> int64_t {  // advances seg monotonically
+    while (u >= prefix[seg + 1]) ++seg;
+    const int b = seg / hkv;
+    return int64_t(bt[b * bt_b + (u - prefix[seg])]);
+  };
+  u32x4_t buf[2][16];
+  auto issue = [&](int d, int u) {
+    const int64_t phys = phys_of(u);
+    const int hh = seg % hkv;
+    const __amdgpu_buffer_rsrc_t rk = page_rsrc(kc + phys * kc_p + hh * kc_h);
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(vc + phys * vc_p + hh * vc_h);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      buf[d][e] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 1024 * e, 0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      buf[d][8 + e] = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 1024 * e, 0);
+  };
+  float acc = 0.f;
+  auto consume = [&](int d) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc += bf16_lo(buf[d][e][w]) + bf16_hi(buf[d][e][w]);
+  };
+  if (u0 < u1) issue(0, u0);
+  for (int u = u0; u < u1; u += 2) {
+    if (u + 1 < u1) issue(1, u + 1);
+    consume(0);
+    if (u + 1 < u1) {
+      if (u + 2 < u1) issue(0, u + 2);
+      consume(1);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) sums[gw] = acc;
+}
+}  // namespace
+
+extern "C" int64_t wy_page_stream_read_waves(void) { return kStreamWaves; }
+
+extern "C" int wy_page_stream_read(const void *k_cache, const void *v_cache,
+                                   const int64_t *kcs, const int64_t *vcs,
+                                   const int32_t *block_table, int64_t bt_stride0,
+                                   const int64_t *pos, int batch, int num_kv_heads,
+                                   int head_dim, float *sums, void *stream) {
+  if (!k_cache || !v_cache || !kcs || !vcs || !block_table || !pos || !sums) return WY_E_NULL;
+  if (batch < 0 || num_kv_heads <= 0) return WY_E_SHAPE;
+  if (head_dim != kD || batch * num_kv_heads > kMaxSegsStream) return WY_E_UNSUPPORTED;
+  // whole 512-byte rows, 16 rows per page: the loads address row e of a page as 1024 e
+  if (!cache_layout_ok(k_cache, v_cache, kcs, vcs) || kcs[2] != kD || vcs[2] != kD)
+    return WY_E_LAYOUT;
+  if (batch == 0) return WY_OK;
+  page_stream_kernel<<<kStreamWaves / 4, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(k_cache), static_cast<const bf16_t *>(v_cache), kcs[0], kcs[1],
+      vcs[0], vcs[1], block_table, bt_stride0, pos, batch, num_kv_heads, sums);
+  return wyh::launch_status();
+}

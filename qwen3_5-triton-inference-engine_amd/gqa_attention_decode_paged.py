@@ -517,3 +517,24 @@ def _fused_ok(k_new: torch.Tensor, v_new: torch.Tensor) -> bool:
 
 
 paged_gqa_attention_decode = call_paged_gqa_attention_decode_triton
+
+
+def page_stream_read(k_cache: torch.Tensor, v_cache: torch.Tensor, block_table: torch.Tensor,
+                     pos: torch.Tensor) -> torch.Tensor:
+    """Measurement helper, no counterpart in the reference: read every K/V page
+    row a decode step at ``pos`` attends, once, with no attention math
+    (``wy_page_stream_read``); returns the per-wavefront fp32 sums.  Its time
+    is the HBM floor of the decode step's access pattern."""
+    batch = pos.shape[0]
+    num_kv_heads = k_cache.shape[1]
+    assert k_cache.shape == v_cache.shape and k_cache.dtype == torch.bfloat16
+    assert block_table.dtype == torch.int32 and block_table.stride(1) == 1
+    assert pos.dtype == torch.int64 and pos.is_contiguous()
+    lib = _lib.load()
+    sums = torch.empty(lib.wy_page_stream_read_waves(), dtype=torch.float32,
+                       device=k_cache.device)
+    _lib.call("wy_page_stream_read", _lib.ptr(k_cache), _lib.ptr(v_cache),
+              _lib.strides(k_cache), _lib.strides(v_cache), _lib.ptr(block_table),
+              block_table.stride(0), _lib.ptr(pos), batch, num_kv_heads, k_cache.shape[3],
+              _lib.ptr(sums), _lib.stream(k_cache.device))
+    return sums

@@ -650,3 +650,28 @@ def test_decode_block_graph_replays(pkg, dev):
         torch.cuda.synchronize()
         assert torch.equal(out_g, out_e), rep
         assert torch.equal(kc_g, kc_e) and torch.equal(vc_g, vc_e), rep
+
+
+@pytest.mark.parametrize("lens", [[300, 2048, 129, 17, 1000, 1], [5], [4096] * 20])
+def test_page_stream_read_reads_each_attended_page_once(pkg, dev, lens):
+    """The measurement kernel reads exactly the pages a decode step attends:
+    K rows hold 1, V rows 2, every other page 1000, so the total of the
+    per-wave sums is 3 * 4096 * (attended pages x heads) exactly (integers in
+    fp32 per wave, added in fp64 here) and any extra or missing page shows."""
+    say(f"page stream read lens={lens}")
+    gen = torch.Generator().manual_seed(len(lens))
+    B = len(lens)
+    max_pages = -(-max(lens) // 16) + 1
+    num_pages = B * max_pages + 3
+    bt = torch.randperm(num_pages, generator=gen)[:B * max_pages].view(B, max_pages)
+    kc = torch.full((num_pages, HKV, 16, D), 1000.0, dtype=torch.bfloat16)
+    vc = kc.clone()
+    units = 0
+    for b, n in enumerate(lens):
+        npg = -(-n // 16)
+        units += npg * HKV
+        kc[bt[b, :npg].long()] = 1.0
+        vc[bt[b, :npg].long()] = 2.0
+    pos = torch.tensor([n - 1 for n in lens])
+    sums = pkg.page_stream_read(kc.to(dev), vc.to(dev), bt.to(torch.int32).to(dev), pos.to(dev))
+    assert float(sums.double().sum()) == 3.0 * 16 * D * units
