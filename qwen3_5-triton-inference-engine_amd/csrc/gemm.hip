@@ -10,11 +10,14 @@
 //     l%16, 8 consecutive k at 8(l/16)), x rows into the A operand, one MFMA
 //     per 16 rows of M, so every W byte is read once.  The waves' partial
 //     16-column tiles are summed through LDS.
-//   * M > 64 (prefill: M is the token count): 128 x 128 output tiles, 4 waves
-//     of 64 x 64 on v_mfma_f32_32x32x16_bf16, K in 64-wide steps.  x and W
-//     tiles move global -> LDS with buffer loads carrying the LDS-DMA bit
-//     (no registers), two stages; rows past M / N lie outside the buffer
-//     range and read as zero.
+//   * M > 64 (prefill: M is the token count): 128 x 128 (4 waves of 64 x 64)
+//     or 256 x 256 (8 waves of 128 x 64) output tiles on
+//     v_mfma_f32_32x32x16_bf16, K in 64-wide steps.  x and W tiles move
+//     global -> LDS with buffer loads carrying the LDS-DMA bit (no
+//     registers), two stages; rows past M / N lie outside the buffer range
+//     and read as zero.
+#include <type_traits>
+
 #include "wy_common.h"
 
 using namespace wy;
@@ -255,10 +258,16 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
 }
 
 // ------------------------------------------------------------ tiled (M > 64)
-// Output tile kTile x kTile, 4 waves in a 2 x 2 grid, each (kTile/2)^2 as
-// (kTile/64)^2 MFMA tiles of 32 x 32; K in 64-wide steps, two LDS stages.
-// kTile = 128: 72 KiB of LDS, two workgroups per CU.  (A 256-wide tile with
-// one workgroup per CU measured slower: 284 vs 256 us at 16384 x 6144 x 1024.)
+// Output tile BM x BN, WM x WN waves of (BM/WM) x (BN/WN) as 32 x 32 MFMA
+// tiles; K in 64-wide steps through a two-stage LDS ring filled by LDS-DMA
+// buffer loads (rows past M / N lie outside the buffer range and read zero).
+// The MFMA operands are read from LDS with explicit waits: the reads of
+// k-step ks+1 are issued before the MFMAs of ks and awaited after them, so
+// the LDS latency hides behind the MFMAs (left to the compiler, each read
+// pair was awaited right before its MFMA).
+//   <128, 128, 2, 2>: 72 KiB of LDS, two workgroups per CU (small grids);
+//   <256, 256, 2, 4>: 8 waves of 128 x 64, 144 KiB, one workgroup per CU --
+//   half the LDS bytes per MFMA; used when the grid fills the chip.
 constexpr int kTK = 64;
 constexpr int kTSlots = kTK / 8 + 1;   // 16-byte slots per LDS row (one pad)
 constexpr int kTPitch = kTSlots * 16;  // 144 B: 16 consecutive rows hit disjoint banks
@@ -270,36 +279,68 @@ __device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rsrc, unsigned 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t *)lds, 16, voff, soff, 0, 0);
 }
 
-template <int kTile>
+__device__ __forceinline__ uint32_t lds_u32(const unsigned char *p) {
+  return uint32_t(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) unsigned char *)(p)));
+}
+// ds_read_b128 as asm: the compiler does not track it, the caller awaits it
+// with lgkm_wait_all, whose "+v" operands keep later uses after the wait.
+template <int kOff>
+__device__ __forceinline__ u32x4_t ds_read16(uint32_t addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
+}
+template <int kFM, int kFN>
+__device__ __forceinline__ void lgkm_wait_all(u32x4_t (&a)[kFM], u32x4_t (&b)[kFN]) {
+  if constexpr (kFM == 2 && kFN == 2)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+  else if constexpr (kFM == 4 && kFN == 2)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]));
+  else
+    static_assert(kFM < 0, "fragment counts without a wait");
+}
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <int BM, int BN, int WM, int WN>
 struct TileCfg {
-  static constexpr int kOpTile = kTile * kTPitch;       // one operand's LDS tile
-  static constexpr int kStage = 2 * kOpTile;            // x tile + W tile
-  static constexpr int kOpDma = kOpTile / 1024;         // DMA blocks per operand tile
-  static constexpr int kPerWave = 2 * kOpDma / 4;       // DMA blocks per wave per stage
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kATile = BM * kTPitch, kBTile = BN * kTPitch;
+  static constexpr int kStage = kATile + kBTile;
+  static constexpr int kABlk = kATile / 1024;           // DMA blocks of the x tile
+  static constexpr int kBlk = kABlk + kBTile / 1024;     // DMA blocks per stage
+  static constexpr int kPerWave = (kBlk + kWaves - 1) / kWaves;
   static constexpr int kLds = 2 * kStage;
-  static constexpr int kFrag = kTile / 64;              // MFMA tiles per wave per dim
-  static_assert(kOpTile % 1024 == 0 && (2 * kOpDma) % 4 == 0, "whole DMA blocks per wave");
+  static constexpr int kFM = BM / WM / 32, kFN = BN / WN / 32;  // MFMA tiles per wave
+  static_assert(kATile % 1024 == 0 && kBTile % 1024 == 0, "whole DMA blocks");
 };
 
-template <int kTile>
-__global__ __launch_bounds__(256) void gemm_tiled_kernel(
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K) {
-  using C = TileCfg<kTile>;
-  constexpr int kF = C::kFrag;
+  using C = TileCfg<BM, BN, WM, WN>;
+  constexpr int kFM = C::kFM, kFN = C::kFN;
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int g = lane >> 5, r32 = lane & 31;
-  const int m0 = blockIdx.y * kTile, n0 = blockIdx.x * kTile;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-  // DMA block b (= wave + 4i) of a stage: b < kOpDma fills the x tile, the
-  // rest the W tile; lane j of a block fills 16-byte slot 64 (b mod kOpDma) + j;
-  // slot c of row r holds k-chunk c (the pad slot repeats chunk 0, never read).
-  // Lane offsets are tile-invariant, the k offset is scalar, and the buffer
-  // ranges end at the last valid row, so rows past M / N read zero.
-  const int a_rows = min(kTile, M - m0), b_rows = min(kTile, N - n0);
+  // DMA block b (= wave + kWaves*i) of a stage: b < kABlk fills the x tile,
+  // the rest the W tile; lane j of a block fills 16-byte slot 64 (b mod
+  // tile) + j; slot c of row r holds k-chunk c (the pad slot repeats chunk
+  // 0, never read).  Lane offsets are tile-invariant, the k offset is scalar,
+  // and the buffer ranges end at the last valid row.
+  const int a_rows = min(BM, M - m0), b_rows = min(BN, N - n0);
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16_t *>(x + int64_t(m0) * xs0), 0,
       int(uint32_t(a_rows - 1) * uint32_t(xs0) * 2u + uint32_t(K) * 2u), 0x00020000);
@@ -309,89 +350,113 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(
   uint32_t voff[C::kPerWave];
 #pragma unroll
   for (int i = 0; i < C::kPerWave; ++i) {
-    const int blk = wave + 4 * i;
-    const int sl = 64 * (blk % C::kOpDma) + lane;
+    const int blk = wave + C::kWaves * i;
+    const bool is_a = blk < C::kABlk;
+    const int sl = 64 * (is_a ? blk : blk - C::kABlk) + lane;
     const int row = sl / kTSlots, c = sl - (sl / kTSlots) * kTSlots;
     const uint32_t cb = uint32_t(c < kTK / 8 ? c : 0) * 16u;
-    voff[i] = uint32_t(row) * uint32_t(blk < C::kOpDma ? xs0 : ws0) * 2u + cb;
+    voff[i] = uint32_t(row) * uint32_t(is_a ? xs0 : ws0) * 2u + cb;
   }
   auto issue = [&](int kt) {
     unsigned char *st = smem + (kt & 1) * C::kStage;
     const uint32_t soff = uint32_t(kt * kTK) * 2u;
 #pragma unroll
     for (int i = 0; i < C::kPerWave; ++i) {
-      const int blk = wave + 4 * i;  // wave-uniform
-      if (blk < C::kOpDma) dma_block(a_rsrc, st + blk * 1024, voff[i], soff);
-      else dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
+      const int blk = wave + C::kWaves * i;  // wave-uniform
+      if (blk < C::kABlk) dma_block(a_rsrc, st + blk * 1024, voff[i], soff);
+      else if (blk < C::kBlk) dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
     }
   };
 
-  f32x16_t acc[kF][kF];
+  f32x16_t acc[kFM][kFN];
 #pragma unroll
-  for (int i = 0; i < kF; ++i)
+  for (int i = 0; i < kFM; ++i)
 #pragma unroll
-    for (int j = 0; j < kF; ++j)
+    for (int j = 0; j < kFN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int kt_n = K / kTK;
   issue(0);
-  const uint32_t a_lane = uint32_t((kTile / 2 * wm + r32) * kTPitch + 16 * g);
-  const uint32_t b_lane = uint32_t(C::kOpTile + (kTile / 2 * wn + r32) * kTPitch + 16 * g);
+  const uint32_t a_lane = uint32_t((BM / WM * wm + r32) * kTPitch + 16 * g);
+  const uint32_t b_lane = uint32_t(C::kATile + (BN / WN * wn + r32) * kTPitch + 16 * g);
   for (int kt = 0; kt < kt_n; ++kt) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this stage has landed
     __syncthreads();                                   // and every wave is done with the other
     if (kt + 1 < kt_n) issue(kt + 1);
-    const unsigned char *st = smem + (kt & 1) * C::kStage;
+    const uint32_t st = lds_u32(smem + (kt & 1) * C::kStage);
+    const uint32_t abase = st + a_lane, bbase = st + b_lane;
+    u32x4_t av[2][kFM], bv[2][kFN];
+    auto load = [&](auto bufc, auto ksc) {
+      constexpr int buf = decltype(bufc)::value, ks = decltype(ksc)::value;
+      static_for<0, kFM>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        av[buf][t] = ds_read16<t * 32 * kTPitch + ks * 32>(abase);
+      });
+      static_for<0, kFN>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        bv[buf][t] = ds_read16<t * 32 * kTPitch + ks * 32>(bbase);
+      });
+    };
+    load(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    lgkm_wait_all<kFM, kFN>(av[0], bv[0]);
+    static_for<0, kTK / 16>([&](auto ksc) {
+      constexpr int ks = decltype(ksc)::value, cur = ks & 1;
+      if constexpr (ks + 1 < kTK / 16)
+        load(std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, ks + 1>{});
 #pragma unroll
-    for (int ks = 0; ks < kTK / 16; ++ks) {
-      u32x4_t av[kF], bv[kF];
+      for (int i = 0; i < kFM; ++i)
 #pragma unroll
-      for (int t = 0; t < kF; ++t) {
-        av[t] = ld16(st + a_lane + t * 32 * kTPitch + ks * 32);
-        bv[t] = ld16(st + b_lane + t * 32 * kTPitch + ks * 32);
-      }
-#pragma unroll
-      for (int i = 0; i < kF; ++i)
-#pragma unroll
-        for (int j = 0; j < kF; ++j)
+        for (int j = 0; j < kFN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, av[i]), __builtin_bit_cast(bf16x8_t, bv[j]),
+              __builtin_bit_cast(bf16x8_t, av[cur][i]), __builtin_bit_cast(bf16x8_t, bv[cur][j]),
               acc[i][j], 0, 0, 0);
-    }
+      if constexpr (ks + 1 < kTK / 16) lgkm_wait_all<kFM, kFN>(av[cur ^ 1], bv[cur ^ 1]);
+    });
   }
 
   // acc[i][j] register r of lane l: row (r&3) + 8(r>>2) + 4(l/32) of m-tile i,
   // column l%32 of n-tile j.
 #pragma unroll
-  for (int i = 0; i < kF; ++i)
+  for (int i = 0; i < kFM; ++i)
 #pragma unroll
-    for (int j = 0; j < kF; ++j) {
-      const int col = n0 + kTile / 2 * wn + 32 * j + r32;
+    for (int j = 0; j < kFN; ++j) {
+      const int col = n0 + BN / WN * wn + 32 * j + r32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + kTile / 2 * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
+        const int row = m0 + BM / WM * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
         if (row < M && col < N)
           y[int64_t(row) * ys0 + col] = bf16_t(f32_to_bf16_bits(acc[i][j][r]));
       }
     }
 }
 
-template <int kTile>
-int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
-                 int64_t ys0, int M, int N, int K, hipStream_t st) {
-  auto *fn = gemm_tiled_kernel<kTile>;
+template <int BM, int BN, int WM, int WN>
+int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
+                     int64_t ys0, int M, int N, int K, hipStream_t st) {
+  using C = TileCfg<BM, BN, WM, WN>;
+  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN>;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(fn),
-        hipFuncAttributeMaxDynamicSharedMemorySize, TileCfg<kTile>::kLds);
+        reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
     if (e != hipSuccess) return int(e);
     attr_set = true;
   }
-  const dim3 grid(unsigned((N + kTile - 1) / kTile), unsigned((M + kTile - 1) / kTile));
-  fn<<<grid, 256, TileCfg<kTile>::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K);
+  const dim3 grid(unsigned((N + BN - 1) / BN), unsigned((M + BM - 1) / BM));
+  fn<<<grid, 64 * C::kWaves, C::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K);
   return wyh::launch_status();
+}
+
+// The 256 x 256 tile when its grid fills whole rounds of the 256 CUs (one
+// workgroup each) or runs for 4+ rounds, else 128 x 128 (two workgroups per
+// CU, four times the workgroups, so a partial last round costs less).
+int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
+                 int64_t ys0, int M, int N, int K, hipStream_t st) {
+  const int64_t big = int64_t((M + 255) / 256) * ((N + 255) / 256);
+  if (big >= 256 && (big % 256 == 0 || big >= 1024))
+    return launch_tiled_cfg<256, 256, 2, 4>(x, xs0, w, ws0, y, ys0, M, N, K, st);
+  return launch_tiled_cfg<128, 128, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
 }
 
 struct SkinnyArgs {
@@ -537,10 +602,10 @@ extern "C" int wy_gemm_2d(const void *x, const int64_t *x_strides, const void *w
                  nullptr, ProArgs{}};
     return run_skinny(a, 0, workspace, workspace_bytes, st);
   }
-  // 32-bit buffer offsets within one 128-row band
-  if (int64_t(128) * x_strides[0] * 2 >= INT32_MAX || int64_t(128) * w_strides[0] * 2 >= INT32_MAX)
+  // 32-bit buffer offsets within one 256-row band
+  if (int64_t(256) * x_strides[0] * 2 >= INT32_MAX || int64_t(256) * w_strides[0] * 2 >= INT32_MAX)
     return WY_E_SHAPE;
-  return launch_tiled<128>(xb, x_strides[0], wb, w_strides[0], yb, y_strides[0], M, N, K, st);
+  return launch_tiled(xb, x_strides[0], wb, w_strides[0], yb, y_strides[0], M, N, K, st);
 }
 
 extern "C" int wy_gemm_2d_rmsnorm(const void *x, int64_t x_stride0, const void *residual,
