@@ -396,6 +396,50 @@ int wy_gdn_recurrent_decode(const void *q, const int64_t *q_strides, const void 
                             int num_heads, int key_dim, int value_dim, void *stream);
 
 /*
+ * Gated DeltaNet chunk-64 (WY) prefill of one prompt, stage 1 of 3: per chunk
+ * of 64 tokens and head, G = cumsum(g) (g_cumsum [N, H, 64]), and the
+ * solutions of (I + L) X = B with L[t, i] = beta_t exp(G_t - G_i) <k_t, k_i>
+ * (i < t): u_base = X for B = beta v ([N, H, 64, value_dim]), w = X for
+ * B = beta exp(G) k ([N, H, 64, key_dim]); all fp32, contiguous, N =
+ * ceil(T/64), rows past T zero.  k, v [T, H, 128] bf16 (unit inner stride,
+ * 16-byte aligned rows), beta, g [T, H] fp32.  key_dim = value_dim = 128.
+ * Replaces wy_lib::gdn_chunk_prepare_wy
+ *   (triton_kernels/gdn_recurrent_prefill.py:823-876, kernel :249-411).
+ */
+int wy_gdn_chunk_prepare_wy(const void *k, const int64_t *k_strides, const void *v,
+                            const int64_t *v_strides, const float *beta,
+                            const int64_t *beta_strides, const float *g,
+                            const int64_t *g_strides, float *w, float *u_base, float *g_cumsum,
+                            int token_num, int num_heads, int key_dim, int value_dim,
+                            void *stream);
+
+/*
+ * Stage 2: the chunk recurrence.  chunk_state[c] = the state entering chunk
+ * c ([N, H, key_dim, value_dim]), delta = u_base - w S ([N, H, 64, value_dim]),
+ * S = exp(G_last) S + k^T (delta exp(G_last - G_t)) with tokens past T
+ * masked; final_state [H, key_dim, value_dim].  All fp32 contiguous.
+ * Replaces wy_lib::gdn_chunk_state
+ *   (triton_kernels/gdn_recurrent_prefill.py:885-960, kernel :417-538).
+ */
+int wy_gdn_chunk_state(const void *k, const int64_t *k_strides, const float *w,
+                       const float *u_base, const float *g_cumsum, float *delta,
+                       float *chunk_state, float *final_state, int token_num, int num_heads,
+                       int key_dim, int value_dim, void *stream);
+
+/*
+ * Stage 3: out_t = exp(G_t) q_t S_c + sum_{i <= t in the chunk}
+ * exp(G_t - G_i) <q_t, k_i> delta_i, stored bf16 [T, H, value_dim] with
+ * out_strides (unit inner stride).  q, k as stage 1.
+ * Replaces wy_lib::gdn_chunk_output
+ *   (triton_kernels/gdn_recurrent_prefill.py:969-1011, kernel :570-697).
+ */
+int wy_gdn_chunk_output(const void *q, const int64_t *q_strides, const void *k,
+                        const int64_t *k_strides, const float *delta, const float *g_cumsum,
+                        const float *chunk_state, void *out, const int64_t *out_strides,
+                        int token_num, int num_heads, int key_dim, int value_dim,
+                        void *stream);
+
+/*
  * Gated DeltaNet sequential prefill over a packed varlen batch: sequence b
  * owns tokens [cu_seqlens[b], cu_seqlens[b+1]) of q, k [T, H, key_dim],
  * v, out [T, H, value_dim] (bf16), beta, g [T, H] fp32, and starts from a

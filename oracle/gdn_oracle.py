@@ -30,6 +30,10 @@ PINNED = {
     "gdn_gated_rmsnorm": "pure-Python brute force; z=0 -> 0; scale invariance of x",
     "conv4_prefill": "torch conv1d (padding 3) per sequence of a packed batch",
     "conv_state_from_packed": "direct row selection by index (last 4 rows, zero on top)",
+    "gdn_chunk_prepare_wy / gdn_chunk_state / gdn_chunk_output": "the three stages chained "
+        "(fp64) == gdn_sequential for T in {1, 63, 64, 65, 200, 300} (out and final state); "
+        "u_base / w solve (I + L) X = B (residual ~1e-15 against the explicit matrix); "
+        "chunk_state[0] == 0 and chunk_state[c] == the sequential state after 64 c tokens",
 }
 
 
@@ -151,3 +155,87 @@ def make_gdn_inputs(T, H, DK, DV, gen):
     beta = torch.sigmoid(torch.randn(T, H, generator=gen))
     g = -torch.nn.functional.softplus(torch.randn(T, H, generator=gen))
     return q, k, v, beta, g
+
+
+# ------------------------------------------------------------ chunked (WY) prefill
+CHUNK = 64
+
+
+def gdn_chunk_prepare_wy(k, v, beta, g):
+    """Per 64-token chunk and head (gdn_recurrent_prefill.py:249-411):
+    G = cumsum(g) in the chunk; L[t, i] = beta_t exp(G_t - G_i) <k_t, k_i> for
+    i < t; P = (I + L)^-1; u_base = P (beta v), w = P (beta exp(G) k).
+    Tokens past T count as beta = g = 0 and k = v = 0.  fp64.  Returns
+    ``(w [N, H, 64, DK], u_base [N, H, 64, DV], g_cumsum [N, H, 64])``."""
+    T, H, DK = k.shape
+    DV = v.shape[-1]
+    N = -(-T // CHUNK)
+    pad = N * CHUNK - T
+    kf = torch.nn.functional.pad(k.double(), (0, 0, 0, 0, 0, pad))
+    vf = torch.nn.functional.pad(v.double(), (0, 0, 0, 0, 0, pad))
+    bf = torch.nn.functional.pad(beta.double(), (0, 0, 0, pad))
+    gf = torch.nn.functional.pad(g.double(), (0, 0, 0, pad))
+    kc = kf.view(N, CHUNK, H, DK).permute(0, 2, 1, 3)     # [N, H, 64, DK]
+    vc = vf.view(N, CHUNK, H, DV).permute(0, 2, 1, 3)
+    bc = bf.view(N, CHUNK, H).permute(0, 2, 1)            # [N, H, 64]
+    G = gf.view(N, CHUNK, H).permute(0, 2, 1).cumsum(-1)
+    kkt = kc @ kc.transpose(-1, -2)
+    strict = torch.tril(torch.ones(CHUNK, CHUNK, dtype=torch.bool), -1)
+    decay = torch.exp(torch.where(strict, G[..., :, None] - G[..., None, :],
+                                  torch.full((), -float("inf"), dtype=torch.float64)))
+    L = bc[..., :, None] * decay * kkt
+    eye = torch.eye(CHUNK, dtype=torch.float64)
+    rhs = torch.cat([bc[..., None] * vc, (bc * torch.exp(G))[..., None] * kc], dim=-1)
+    X = torch.linalg.solve_triangular(eye + L, rhs, upper=False, unitriangular=True)
+    return X[..., DV:].contiguous(), X[..., :DV].contiguous(), G
+
+
+def gdn_chunk_state(k, w, u_base, g_cumsum):
+    """Chunk recurrence (gdn_recurrent_prefill.py:417-538): chunk_state[c] =
+    the state entering chunk c; delta = u_base - w S; S = exp(G_last) S +
+    k^T (delta * exp(G_last - G_t)), tokens past T masked.  fp64.
+    Returns ``(delta [N, H, 64, DV], chunk_state [N, H, DK, DV], final [H, DK, DV])``."""
+    T, H, DK = k.shape
+    N, _, _, DV = u_base.shape
+    pad = N * CHUNK - T
+    kc = torch.nn.functional.pad(k.double(), (0, 0, 0, 0, 0, pad)).view(
+        N, CHUNK, H, DK).permute(0, 2, 1, 3)
+    valid = (torch.arange(N * CHUNK) < T).view(N, CHUNK).double()
+    S = torch.zeros(H, DK, DV, dtype=torch.float64)
+    delta = torch.empty(N, H, CHUNK, DV, dtype=torch.float64)
+    chunk_state = torch.empty(N, H, DK, DV, dtype=torch.float64)
+    for c in range(N):
+        chunk_state[c] = S
+        d = u_base[c].double() - w[c].double() @ S
+        delta[c] = d
+        G = g_cumsum[c].double()
+        to_end = torch.exp(G[:, -1:] - G) * valid[c][None, :]
+        S = torch.exp(G[:, -1])[:, None, None] * S + kc[c].transpose(-1, -2) @ (d * to_end[..., None])
+    return delta, chunk_state, S
+
+
+def gdn_chunk_output(q, k, delta, g_cumsum, chunk_state):
+    """Chunk outputs (gdn_recurrent_prefill.py:570-697): out_t = exp(G_t) q_t S_c
+    + sum_{i <= t} exp(G_t - G_i) <q_t, k_i> delta_i.  fp64 ``[T, H, DV]``."""
+    T, H, DK = q.shape
+    N, _, _, DV = delta.shape
+    pad = N * CHUNK - T
+    qc = torch.nn.functional.pad(q.double(), (0, 0, 0, 0, 0, pad)).view(
+        N, CHUNK, H, DK).permute(0, 2, 1, 3)
+    kc = torch.nn.functional.pad(k.double(), (0, 0, 0, 0, 0, pad)).view(
+        N, CHUNK, H, DK).permute(0, 2, 1, 3)
+    G = g_cumsum.double()
+    causal = torch.tril(torch.ones(CHUNK, CHUNK, dtype=torch.bool))
+    decay = torch.exp(torch.where(causal, G[..., :, None] - G[..., None, :],
+                                  torch.full((), -float("inf"), dtype=torch.float64)))
+    att = (qc @ kc.transpose(-1, -2)) * decay
+    out = torch.exp(G)[..., None] * (qc @ chunk_state.double()) + att @ delta.double()
+    return out.permute(0, 2, 1, 3).reshape(N * CHUNK, H, DV)[:T]
+
+
+def gdn_chunked(q, k, v, beta, g):
+    """The three stages chained (call_gdn_recurrent_prefill_chunked_triton,
+    gdn_recurrent_prefill.py:1026-1046): ``(out fp64 [T, H, DV], state [H, DK, DV])``."""
+    w, u, G = gdn_chunk_prepare_wy(k, v, beta, g)
+    delta, cs, final = gdn_chunk_state(k, w, u, G)
+    return gdn_chunk_output(q, k, delta, G, cs), final

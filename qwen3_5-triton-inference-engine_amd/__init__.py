@@ -57,8 +57,15 @@ from .gdn_gated_rmsnorm import call_gdn_gated_rmsnorm_triton, gdn_gated_rmsnorm
 from .gdn_mixer import gdn_decode_block, gdn_decode_ops
 from .gdn_qk_norm_gates import call_gdn_qk_norm_gates_triton, gdn_qk_norm_gates
 from .gdn_recurrent_prefill import (
+    call_gdn_chunk_output_triton,
+    call_gdn_chunk_prepare_wy_triton,
+    call_gdn_chunk_state_triton,
     call_gdn_recurrent_decode_triton,
+    call_gdn_recurrent_prefill_chunked_triton,
     call_gdn_recurrent_prefill_sequential_triton,
+    gdn_chunk_output,
+    gdn_chunk_prepare_wy,
+    gdn_chunk_state,
     gdn_recurrent_decode,
     gdn_recurrent_prefill_sequential,
 )

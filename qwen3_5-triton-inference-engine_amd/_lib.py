@@ -39,6 +39,11 @@ _SIGNATURES = {
                                      _c_i64p, _c_i64p, _vp, _i64, _vp, _vp, _c_i64p, _vp,
                                      _c_i64p, _i, _i, _i, _i, _i, _i, _vp],
     "wy_page_stream_read": [_vp, _vp, _c_i64p, _c_i64p, _vp, _i64, _vp, _i, _i, _i, _vp, _vp],
+    "wy_gdn_chunk_prepare_wy": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp,
+                                _vp, _vp, _i, _i, _i, _i, _vp],
+    "wy_gdn_chunk_state": [_vp, _c_i64p, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp],
+    "wy_gdn_chunk_output": [_vp, _c_i64p, _vp, _c_i64p, _vp, _vp, _vp, _vp, _c_i64p, _i, _i,
+                            _i, _i, _vp],
     "wy_varlen_causal_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p,
                                  _vp, _i, _i, _i, _i, _i, _i64, _vp, _i64, _vp],
     "wy_partial_rope": [_vp, _c_i64p, _vp, _c_i64p, _vp, _c_i64p, _i, _vp, _i, _i, _i, _i,

@@ -21,7 +21,7 @@ OBJ_DIR = PKG_DIR / "_build"
 ARCH = os.environ.get("WY_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["capi.hip", "kv_cache.hip", "rope_gate.hip", "rmsnorm.hip", "decode.hip", "prefill.hip",
-           "gemm.hip", "gdn.hip", "gdn_block.hip", "model_ops.hip"]
+           "gemm.hip", "gdn.hip", "gdn_block.hip", "gdn_chunk.hip", "model_ops.hip"]
 
 # Packed fp32 VALU ops are disabled: their occasional silent miscompares on
 # this hardware pool are not worth the few percent they might buy.

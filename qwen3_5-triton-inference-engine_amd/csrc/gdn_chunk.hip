@@ -1,0 +1,433 @@
+// Gated DeltaNet chunk-64 (WY) prefill on gfx950: the delta-rule recurrence of
+// one long prompt in three launches instead of a token-by-token walk.
+// Reference: gdn_recurrent_prefill.py:249-411 (prepare), :417-538 (state),
+// :570-697 (output), ops :1050-1046 chain at :1026-1046.
+//
+// Per chunk of 64 tokens and head, with G = cumsum(g) inside the chunk:
+//   L[t, i] = beta_t exp(G_t - G_i) <k_t, k_i>   (i < t)
+//   u_base  = (I + L)^-1 (beta v),   w = (I + L)^-1 (beta exp(G) k)
+//   delta   = u_base - w S_c                       (S_c: state entering chunk c)
+//   S_c+1   = exp(G_last) S_c + k^T (delta exp(G_last - G_t))
+//   out_t   = exp(G_t) q_t S_c + sum_{i <= t} exp(G_t - G_i) <q_t, k_i> delta_i
+// Tokens past T count as beta = g = 0, k = v = q = 0 (their rows are zero).
+//
+// Precision: <k_t, k_i> and <q_t, k_i> are bf16 x bf16 products summed in
+// fp32 on v_mfma_f32_32x32x16_bf16 (exact products).  In the chunk recurrence
+// every fp32 operand x is split as hi = bf16(x), lo = bf16(x - hi) (16 bits
+// of mantissa) and a product of two fp32 operands is hi*hi + hi*lo + lo*hi on
+// v_mfma_f32_16x16x32_bf16 (relative error ~2^-16; the reference uses
+// three-pass tf32 for the same products); a bf16 x fp32 product is two such
+// MFMAs.  The output kernel's products run on v_mfma_f32_16x16x4_f32.  (I + L)^-1 is applied by forward substitution on
+// the right-hand sides, one column per thread, in fp32.
+#include "wy_common.h"
+
+using namespace wy;
+
+namespace {
+
+constexpr int kC = 64;    // chunk tokens
+constexpr int kDK = 128;  // key dim
+constexpr int kDV = 128;  // value dim
+constexpr int kBV = 16;   // value columns per state workgroup
+constexpr int kKPad = kDK + 8;
+
+typedef float f32x4_t_ __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t_ mfma16x4(float a, float b, f32x4_t_ c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t_ mfma16x32(u32x4_t a, u32x4_t b, f32x4_t_ c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+// fp32 x = hi + lo + O(2^-17 |x|) with hi = bf16(x), lo = bf16(x - hi): eight
+// values split into two bf16 MFMA operands
+__device__ __forceinline__ void split8(const float (&x)[8], u32x4_t &hi, u32x4_t &lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float h0 = round_bf16(x[2 * e]), h1 = round_bf16(x[2 * e + 1]);
+    hi[e] = pack_bf16x2(h0, h1);
+    lo[e] = pack_bf16x2(x[2 * e] - h0, x[2 * e + 1] - h1);
+  }
+}
+
+// kk^T-type 64 x 64 product of two bf16 [64][kKPad] LDS tiles on 32x32x16
+// MFMAs: wave w computes output tile (w / 2, w % 2); register r of lane l is
+// row 32 (w/2) + (r&3) + 8 (r>>2) + 4 (l/32), column 32 (w%2) + l%32.
+__device__ __forceinline__ f32x16_t gram64(const bf16_t (*a)[kKPad], const bf16_t (*b)[kKPad],
+                                           int wave, int lane) {
+  const int r0 = 32 * (wave >> 1), c0 = 32 * (wave & 1);
+  f32x16_t acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < kDK / 16; ++ks) {
+    const u32x4_t av = ld16(&a[r0 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
+    const u32x4_t bv = ld16(&b[c0 + (lane & 31)][ks * 16 + 8 * (lane >> 5)]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, av),
+                                                  __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Rows [t0, t0 + nval) of a [T, H, 128] bf16 tensor (head h) into LDS; rows
+// past nval are zero.  Inner stride 1, rows 16-byte aligned (host-checked).
+__device__ __forceinline__ void load_rows(bf16_t (*dst)[kKPad], const bf16_t *src, int64_t st,
+                                          int nval) {
+  for (int i = threadIdx.x; i < kC * 16; i += 256) {
+    const int r = i >> 4, c = (i & 15) * 8;
+    u32x4_t x = {0u, 0u, 0u, 0u};
+    if (r < nval) x = ld16(src + r * st + c);
+    st16(&dst[r][c], x);
+  }
+}
+
+// ---- 1. prepare: G, w, u_base per (chunk, head) ----------------------------------
+__global__ __launch_bounds__(256) void gdn_chunk_prepare_kernel(
+    const bf16_t *__restrict__ k, int64_t k_t, int64_t k_h, const bf16_t *__restrict__ v,
+    int64_t v_t, int64_t v_h, const float *__restrict__ beta, int64_t b_t, int64_t b_h,
+    const float *__restrict__ g, int64_t g_t, int64_t g_h, float *__restrict__ w,
+    float *__restrict__ u, float *__restrict__ gcs, int T, int H) {
+  __shared__ __align__(16) bf16_t ks[kC][kKPad];
+  __shared__ __align__(16) bf16_t vs[kC][kKPad];
+  __shared__ __align__(16) float L[kC][kC + 4];
+  __shared__ float sb[kC], sG[kC], seG[kC];
+  const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int t0 = n * kC;
+  const int nval = min(kC, T - t0);
+  load_rows(ks, k + int64_t(t0) * k_t + h * k_h, k_t, nval);
+  load_rows(vs, v + int64_t(t0) * v_t + h * v_h, v_t, nval);
+  if (tid < kC) {
+    const bool ok = tid < nval;
+    const float bt = ok ? beta[int64_t(t0 + tid) * b_t + h * b_h] : 0.f;
+    float G = ok ? g[int64_t(t0 + tid) * g_t + h * g_h] : 0.f;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {  // inclusive prefix sum over the chunk
+      const float y = __shfl_up(G, o);
+      if (tid >= o) G += y;
+    }
+    sb[tid] = bt;
+    sG[tid] = G;
+    seG[tid] = expf(G);
+    gcs[(int64_t(n) * H + h) * kC + tid] = G;
+  }
+  __syncthreads();
+
+  // L = beta_t exp(G_t - G_i) <k_t, k_i>, strictly lower, in LDS
+  if (wave != 1) {  // output tile (0, 1) lies above the diagonal
+    const f32x16_t kk = gram64(ks, ks, wave, lane);
+    const int i = 32 * (wave & 1) + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * (wave >> 1) + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+      L[t][i] = (i < t && t < nval) ? sb[t] * expf(sG[t] - sG[i]) * kk[r] : 0.f;
+    }
+  } else {
+    for (int e = lane; e < 32 * 32; e += 64) L[e >> 5][32 + (e & 31)] = 0.f;
+  }
+  __syncthreads();
+
+  // forward substitution X = (I + L)^-1 B, thread c owning column c of
+  // B = [beta v | beta exp(G) k]: X_t = B_t - sum_{i<t} L[t][i] X_i
+  const int c = tid;
+  float x[kC];
+#pragma unroll
+  for (int t = 0; t < kC; ++t) {
+    float acc = c < kDV ? sb[t] * bf16_to_f32(vs[t][c]) : sb[t] * seG[t] * bf16_to_f32(ks[t][c - kDV]);
+#pragma unroll
+    for (int i4 = 0; i4 < t; i4 += 4) {
+      const float4 l4 = *reinterpret_cast<const float4 *>(&L[t][i4]);
+      acc -= l4.x * x[i4];
+      if (i4 + 1 < t) acc -= l4.y * x[i4 + 1];
+      if (i4 + 2 < t) acc -= l4.z * x[i4 + 2];
+      if (i4 + 3 < t) acc -= l4.w * x[i4 + 3];
+    }
+    x[t] = acc;
+  }
+  float *dst = (c < kDV ? u : w) + (int64_t(n) * H + h) * kC * 128 + (c & 127);
+#pragma unroll
+  for (int t = 0; t < kC; ++t) dst[t * 128] = x[t];
+}
+
+// ---- 2. state: the chunk recurrence per (head, 16 value columns) ----------------
+//
+// S (128 x 16 fp32) lives in registers in the 16x16 MFMA output layout: wave
+// wv holds key rows 32 wv .. 32 wv + 31 as two 16-row tiles; lane l has rows
+// 16 dt + 4 (l/16) + j, column l%16.  Per chunk:
+//   delta (64 x 16) = u_base - w S     wave wv: token rows 16 wv .. +15
+//   dd = delta * exp(G_last - G_t)     (zero past T), via LDS
+//   S = exp(G_last) S + k^T dd
+// The k index of an MFMA may be any permutation shared by its A and B
+// operands: in w S lane (row r, group qd) takes keys 32 qd .. 32 qd + 31, so
+// its w operand is 32 consecutive floats of row r (one contiguous load,
+// fetched a chunk ahead); in k^T dd it takes tokens 16 qd .. 16 qd + 15.
+// Every operand of a product is read before its first MFMA.
+__global__ __launch_bounds__(256) void gdn_chunk_state_kernel(
+    const bf16_t *__restrict__ k, int64_t k_t, int64_t k_h, const float *__restrict__ w,
+    const float *__restrict__ u, const float *__restrict__ gcs, float *__restrict__ delta,
+    float *__restrict__ chunk_state, float *__restrict__ final_state, int T, int H, int N) {
+  // S as the B operand of w S: key row d holds its 16 columns at offset
+  // 16 ((d / 32) & 1) of a 32-float row, so the four lane groups (reading rows
+  // 32 qd + kq) meet in pairs on a bank, not all four
+  __shared__ __align__(16) float sS[kDK][2 * kBV];
+  __shared__ __align__(16) float sdd[kC][kBV + 1];   // dd as the B operand of k^T dd
+  __shared__ __align__(16) float sdl[kC][kBV];       // delta rows for the coalesced store
+  __shared__ __align__(16) bf16_t sk[kC][kKPad];     // k of the chunk (A operand of k^T dd)
+  __shared__ float sG[kC];
+  const int h = blockIdx.x, v0 = blockIdx.y * kBV, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, quad = lane >> 4;
+
+  f32x4_t_ S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
+  // the chunk's operands in registers: w row 16 wave + col, keys 32 quad ..
+  // +31 (8 x 16 bytes); k rows for LDS (4 x 16 bytes per thread); u_base of
+  // the lane's delta outputs; G
+  f32x4_t_ cw[8], nw[8];
+  u32x4_t nk[4];
+  float nu[4], cu[4];
+  float nG = 0.f;
+  auto fetch = [&](int c) {
+    const float *wr = w + ((int64_t(c) * H + h) * kC + 16 * wave + col) * kDK + 32 * quad;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nw[i] = *reinterpret_cast<const f32x4_t_ *>(wr + 4 * i);
+    const int t0 = c * kC, nval = min(kC, T - t0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, r = e >> 4, cc = (e & 15) * 8;
+      nk[i] = r < nval ? ld16(k + int64_t(t0 + r) * k_t + h * k_h + cc) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    const float *uc = u + (int64_t(c) * H + h) * kC * kDV + v0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) nu[j] = uc[(16 * wave + 4 * quad + j) * kDV + col];
+    if (tid < kC) nG = gcs[(int64_t(c) * H + h) * kC + tid];
+  };
+  fetch(0);
+  for (int c = 0; c < N; ++c) {
+    // the fetched chunk becomes current; publish S (B operand) and k
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cw[i] = nw[i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      cu[j] = nu[j];
+      asm volatile("" : "+v"(cu[j]));  // copy now, before the next fetch reuses nu
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i;
+      st16(&sk[e >> 4][(e & 15) * 8], nk[i]);
+    }
+    if (tid < kC) sG[tid] = nG;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = 32 * wave + 4 * quad + j;
+      sS[d][col + 16 * (wave & 1)] = S0[j];
+      sS[d + 16][col + 16 * (wave & 1)] = S1[j];
+    }
+    __syncthreads();
+    // this chunk's entering state, coalesced: 16-byte pieces of the rows of S
+    // (LDS offset 16 ((d / 32) & 1) within the 32-float row)
+    float *cs = chunk_state + (int64_t(c) * H + h) * kDK * kDV + v0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i, d = e >> 2, p4 = (e & 3) * 4;
+      *reinterpret_cast<f32x4_t_ *>(cs + d * kDV + p4) =
+          *reinterpret_cast<const f32x4_t_ *>(&sS[d][p4 + 16 * ((d >> 5) & 1)]);
+    }
+    if (c + 1 < N) fetch(c + 1);
+
+    // delta rows 16 wave .. +15 = u_base - w S on bf16 MFMAs with both fp32
+    // operands split (hi hi + hi lo + lo hi); step ks covers keys
+    // 32 qd + 8 ks .. +7 of lane group qd
+    f32x4_t_ acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float bx[8], ax[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bx[e] = sS[32 * quad + 8 * ks + e][col + 16 * (quad & 1)];
+        ax[e] = cw[2 * ks + (e >> 2)][e & 3];
+      }
+      u32x4_t ah, al, bh, bl;
+      split8(ax, ah, al);
+      split8(bx, bh, bl);
+      acc = mfma16x32(ah, bh, acc);
+      acc = mfma16x32(ah, bl, acc);
+      acc = mfma16x32(al, bh, acc);
+    }
+    const int t0 = c * kC, nval = min(kC, T - t0);
+    const float G_last = sG[kC - 1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * wave + 4 * quad + j;
+      const float d = cu[j] - acc[j];
+      sdl[t][col] = d;
+      sdd[t][col] = t < nval ? d * expf(G_last - sG[t]) : 0.f;
+    }
+    __syncthreads();
+    {  // delta rows, coalesced: one 16-byte piece per thread
+      float *dl = delta + (int64_t(c) * H + h) * kC * kDV + v0;
+      const int t = tid >> 2, p4 = (tid & 3) * 4;
+      *reinterpret_cast<f32x4_t_ *>(dl + t * kDV + p4) =
+          *reinterpret_cast<const f32x4_t_ *>(&sdl[t][p4]);
+    }
+
+    // S = exp(G_last) S + k^T dd: A[d][t] = k[t][d] (bf16, exact), dd split;
+    // step ks covers tokens 16 qd + 8 ks .. +7 of lane group qd
+    const int d0 = 32 * wave + col;
+    const float eg = expf(G_last);
+    S0 *= eg;
+    S1 *= eg;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float bx[8];
+      u32x4_t a0, a1;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int t = 16 * quad + 8 * ks + e;
+        bx[e] = sdd[t][col];
+        bx[e + 1] = sdd[t + 1][col];
+        a0[e / 2] = uint32_t(sk[t][d0]) | (uint32_t(sk[t + 1][d0]) << 16);
+        a1[e / 2] = uint32_t(sk[t][d0 + 16]) | (uint32_t(sk[t + 1][d0 + 16]) << 16);
+      }
+      u32x4_t bh, bl;
+      split8(bx, bh, bl);
+      S0 = mfma16x32(a0, bh, S0);
+      S0 = mfma16x32(a0, bl, S0);
+      S1 = mfma16x32(a1, bh, S1);
+      S1 = mfma16x32(a1, bl, S1);
+    }
+    __syncthreads();  // sS / sdd / sk are rewritten by the next chunk
+  }
+  float *fs = final_state + int64_t(h) * kDK * kDV + v0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = 32 * wave + 4 * quad + j;
+    fs[d * kDV + col] = S0[j];
+    fs[(d + 16) * kDV + col] = S1[j];
+  }
+}
+
+// ---- 3. output per (chunk, head) -------------------------------------------------
+//
+// out (64 x 128) = exp(G_t) q S_c + A delta with A[t][i] = <q_t, k_i>
+// exp(G_t - G_i) (i <= t).  Wave wv owns token rows 16 wv .. +15 and all 128
+// value columns (8 tiles of 16 x 16); both products run on 16x16x4 fp32 MFMAs
+// with the B operands (S_c, delta) streamed from global memory.
+__global__ __launch_bounds__(256) void gdn_chunk_output_kernel(
+    const bf16_t *__restrict__ q, int64_t q_t, int64_t q_h, const bf16_t *__restrict__ k,
+    int64_t k_t, int64_t k_h, const float *__restrict__ delta, const float *__restrict__ gcs,
+    const float *__restrict__ chunk_state, bf16_t *__restrict__ out, int64_t o_t, int64_t o_h,
+    int T, int H) {
+  __shared__ __align__(16) bf16_t qs[kC][kKPad];
+  __shared__ __align__(16) bf16_t ks[kC][kKPad];
+  __shared__ __align__(16) float A[kC][kC + 4];
+  __shared__ float sG[kC];
+  const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, quad = lane >> 4;
+  const int t0 = n * kC;
+  const int nval = min(kC, T - t0);
+  load_rows(qs, q + int64_t(t0) * q_t + h * q_h, q_t, nval);
+  load_rows(ks, k + int64_t(t0) * k_t + h * k_h, k_t, nval);
+  if (tid < kC) sG[tid] = gcs[(int64_t(n) * H + h) * kC + tid];
+  __syncthreads();
+  if (wave != 1) {
+    const f32x16_t qk = gram64(qs, ks, wave, lane);
+    const int i = 32 * (wave & 1) + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = 32 * (wave >> 1) + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+      A[t][i] = (i <= t && t < nval) ? qk[r] * expf(sG[t] - sG[i]) : 0.f;
+    }
+  } else {
+    for (int e = lane; e < 32 * 32; e += 64) A[e >> 5][32 + (e & 31)] = 0.f;
+  }
+  __syncthreads();
+
+  const float *Sc = chunk_state + (int64_t(n) * H + h) * kDK * kDV;
+  const float *dl = delta + (int64_t(n) * H + h) * kC * kDV;
+  const int trow = 16 * wave + col;  // A-operand row of this lane
+  f32x4_t_ o[8];
+#pragma unroll
+  for (int vt = 0; vt < 8; ++vt) {
+    f32x4_t_ a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int kq = 0; kq < kDK / 4; ++kq)
+      a1 = mfma16x4(bf16_to_f32(qs[trow][4 * kq + quad]), Sc[(4 * kq + quad) * kDV + 16 * vt + col],
+                    a1);
+#pragma unroll 8
+    for (int kq = 0; kq < kC / 4; ++kq)
+      a2 = mfma16x4(A[trow][4 * kq + quad], dl[(4 * kq + quad) * kDV + 16 * vt + col], a2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * wave + 4 * quad + j;
+      o[vt][j] = expf(sG[t]) * a1[j] + a2[j];
+    }
+  }
+#pragma unroll
+  for (int vt = 0; vt < 8; ++vt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = 16 * wave + 4 * quad + j;
+      if (t < nval)
+        out[int64_t(t0 + t) * o_t + h * o_h + 16 * vt + col] = bf16_t(f32_to_bf16_bits(o[vt][j]));
+    }
+}
+
+bool rows_ok(const void *p, const int64_t *s) {
+  return s[2] == 1 && s[0] % 8 == 0 && s[1] % 8 == 0 && wyh::aligned16(p);
+}
+
+}  // namespace
+
+extern "C" int wy_gdn_chunk_prepare_wy(const void *k, const int64_t *ks, const void *v,
+                                       const int64_t *vs, const float *beta, const int64_t *bs,
+                                       const float *g, const int64_t *gs, float *w,
+                                       float *u_base, float *g_cumsum, int token_num,
+                                       int num_heads, int key_dim, int value_dim, void *stream) {
+  if (!k || !ks || !v || !vs || !beta || !bs || !g || !gs || !w || !u_base || !g_cumsum)
+    return WY_E_NULL;
+  if (token_num <= 0 || num_heads <= 0) return WY_E_SHAPE;
+  if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
+  if (!rows_ok(k, ks) || !rows_ok(v, vs)) return WY_E_LAYOUT;
+  const int N = (token_num + kC - 1) / kC;
+  gdn_chunk_prepare_kernel<<<dim3(N, num_heads), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(k), ks[0], ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1],
+      beta, bs[0], bs[1], g, gs[0], gs[1], w, u_base, g_cumsum, token_num, num_heads);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_gdn_chunk_state(const void *k, const int64_t *ks, const float *w,
+                                  const float *u_base, const float *g_cumsum, float *delta,
+                                  float *chunk_state, float *final_state, int token_num,
+                                  int num_heads, int key_dim, int value_dim, void *stream) {
+  if (!k || !ks || !w || !u_base || !g_cumsum || !delta || !chunk_state || !final_state)
+    return WY_E_NULL;
+  if (token_num <= 0 || num_heads <= 0) return WY_E_SHAPE;
+  if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
+  if (!rows_ok(k, ks) || !wyh::aligned16(w)) return WY_E_LAYOUT;
+  const int N = (token_num + kC - 1) / kC;
+  gdn_chunk_state_kernel<<<dim3(num_heads, kDV / kBV), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(k), ks[0], ks[1], w, u_base, g_cumsum, delta, chunk_state,
+      final_state, token_num, num_heads, N);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_gdn_chunk_output(const void *q, const int64_t *qs, const void *k,
+                                   const int64_t *ks, const float *delta, const float *g_cumsum,
+                                   const float *chunk_state, void *out, const int64_t *os,
+                                   int token_num, int num_heads, int key_dim, int value_dim,
+                                   void *stream) {
+  if (!q || !qs || !k || !ks || !delta || !g_cumsum || !chunk_state || !out || !os)
+    return WY_E_NULL;
+  if (token_num <= 0 || num_heads <= 0) return WY_E_SHAPE;
+  if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
+  if (!rows_ok(q, qs) || !rows_ok(k, ks) || os[2] != 1) return WY_E_LAYOUT;
+  const int N = (token_num + kC - 1) / kC;
+  gdn_chunk_output_kernel<<<dim3(N, num_heads), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0], ks[1],
+      delta, g_cumsum, chunk_state, static_cast<bf16_t *>(out), os[0], os[1], token_num,
+      num_heads);
+  return wyh::launch_status();
+}

@@ -34,7 +34,15 @@ from .depthwise_causal_conv4_decode import conv_state_from_packed_prefill
 from .depthwise_causal_conv4_prefill import depthwise_causal_conv4_prefill
 from .gdn_gated_rmsnorm import gdn_gated_rmsnorm
 from .gdn_qk_norm_gates import gdn_qk_norm_gates
-from .gdn_recurrent_prefill import gdn_recurrent_prefill_sequential
+from .gdn_recurrent_prefill import (
+    call_gdn_recurrent_prefill_chunked_triton,
+    gdn_recurrent_prefill_sequential,
+)
+
+# A single prompt at least this long takes the chunk-64 GDN prefill (the
+# reference's routing threshold, engine/runner.py:151-153); packed batches and
+# shorter prompts take the sequential kernel.
+GDN_CHUNKED_PREFILL_MIN_TOKENS = 2048
 from .cache import allocate_attn_caches
 from .embedding_gather import embedding_gather
 from .gemm_2d import gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
@@ -331,7 +339,13 @@ class DecodeModel:
         qn, kn, beta, g = gdn_qk_norm_gates(q, k, fused[:, 4 * HD:4 * HD + H],
                                             fused[:, 4 * HD + H:], w.extra["a_log"],
                                             w.extra["dt_bias"])
-        core, state = gdn_recurrent_prefill_sequential(qn, kn, v, beta, g, packed.cu_seqlens)
+        if packed.batch == 1 and T >= GDN_CHUNKED_PREFILL_MIN_TOKENS:
+            # one long prompt: the chunk-64 WY path (engine/runner.py:272-273)
+            core, state = call_gdn_recurrent_prefill_chunked_triton(qn, kn, v, beta, g)
+            state = state.unsqueeze(0)
+        else:
+            core, state = gdn_recurrent_prefill_sequential(qn, kn, v, beta, g,
+                                                           packed.cu_seqlens)
         self.rec_states[i].copy_(state)
         conv_state_from_packed_prefill(self.conv_states[i], qkv, packed.cu_seqlens)
         normed = gdn_gated_rmsnorm(core, fused[:, 3 * HD:4 * HD].view(T, H, D), w.extra["norm"])

@@ -4,6 +4,7 @@ rule, closed-form special cases and torch's own conv1d.  CPU only."""
 
 import math
 
+import pytest
 import torch
 
 from oracle import gdn_oracle as go
@@ -204,3 +205,44 @@ def test_conv_state_from_packed_selects_rows():
     assert torch.equal(st[0, :2], torch.zeros(2, 3, dtype=torch.bfloat16))
     assert torch.equal(st[0, 2:], x[0:2])
     assert torch.equal(st[1], x[6:10])
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 200, 300])
+def test_chunked_stages_equal_sequential(T):
+    """The chunk-64 WY form (three stages) equals the sequential recurrence,
+    which the brute-force tests above pin: any wrong term of L, w, u_base, the
+    chunk state or the intra-chunk output shows here."""
+    gen = torch.Generator().manual_seed(T)
+    q, k, v, beta, g = go.make_gdn_inputs(T, 3, 16, 8, gen)
+    out, st = go.gdn_chunked(q, k, v, beta, g)
+    ref_o, ref_s = go.gdn_sequential(q, k, v, beta, g)
+    torch.testing.assert_close(out.float(), ref_o, atol=2e-5, rtol=2e-5)
+    torch.testing.assert_close(st.float(), ref_s[0], atol=2e-5, rtol=2e-5)
+
+
+def test_chunk_prepare_solves_the_triangular_system_and_states_chain():
+    gen = torch.Generator().manual_seed(11)
+    T, H, DK, DV = 150, 2, 16, 8
+    q, k, v, beta, g = go.make_gdn_inputs(T, H, DK, DV, gen)
+    w, u, G = go.gdn_chunk_prepare_wy(k, v, beta, g)
+    # (I + L) [u | w] = [beta v | beta exp(G) k] row by row, L built explicitly
+    for c in range(w.shape[0]):
+        for h in range(H):
+            n = min(64, T - 64 * c)
+            kk = k[64 * c:64 * c + n, h].double()
+            b = beta[64 * c:64 * c + n, h].double()
+            Gc = G[c, h, :n]
+            L = torch.zeros(n, n, dtype=torch.float64)
+            for t in range(n):
+                for i in range(t):
+                    L[t, i] = b[t] * math.exp(Gc[t] - Gc[i]) * float(kk[t] @ kk[i])
+            A = torch.eye(n, dtype=torch.float64) + L
+            assert torch.allclose(A @ u[c, h, :n], b[:, None] * v[64 * c:64 * c + n, h].double(),
+                                  atol=1e-12)
+            assert torch.allclose(A @ w[c, h, :n], (b * torch.exp(Gc))[:, None] * kk, atol=1e-12)
+    delta, cs, final = go.gdn_chunk_state(k, w, u, G)
+    assert not cs[0].any()
+    for c in (1, 2):
+        _, s_ref = go.gdn_sequential(q[:64 * c], k[:64 * c], v[:64 * c], beta[:64 * c],
+                                     g[:64 * c])
+        torch.testing.assert_close(cs[c].float(), s_ref[0], atol=2e-5, rtol=2e-5)
