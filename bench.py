@@ -791,6 +791,22 @@ def gdn_bench(pkg, dev):
         name = f"gdn_recurrent_prefill_sequential {len(lengths)} x {lengths[0]}"
         out[name] = {"us": round(ms * 1e3, 2), "tokens/s": round(T / ms * 1e3, 1),
                      "us_per_token_step": round(ms * 1e3 / max(lengths), 4)}
+    # one long prompt through the chunk-64 WY form (the runner's route for a
+    # single sequence of >= 2048 tokens), stage by stage and as the chain
+    for T in (4096, 16384):
+        q, k, v, beta, g = qkv(T)
+        ms = time_events(lambda: pkg.call_gdn_recurrent_prefill_chunked_triton(q, k, v, beta, g), 5)
+        w, u, G = pkg.gdn_chunk_prepare_wy(k, v, beta, g)
+        delta, cs, _ = pkg.gdn_chunk_state(k, w, u, G)
+        st = {"prepare_wy": time_events(lambda: pkg.gdn_chunk_prepare_wy(k, v, beta, g), 5),
+              "state": time_events(lambda: pkg.gdn_chunk_state(k, w, u, G), 5),
+              "output": time_events(lambda: pkg.gdn_chunk_output(q, k, delta, G, cs), 5)}
+        r = {"us": round(ms * 1e3, 2), "tokens/s": round(T / ms * 1e3, 1),
+             "stage_us": {n: round(x * 1e3, 2) for n, x in st.items()}}
+        if T == 4096:
+            r["vs_sequential"] = round(out["gdn_recurrent_prefill_sequential 1 x 4096"]["us"]
+                                       / r["us"], 2)
+        out[f"gdn_recurrent_prefill_chunked 1 x {T}"] = r
     for name, r in out.items():
         log(f"gdn {name}: {r}")
     return out
