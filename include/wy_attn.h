@@ -404,7 +404,7 @@ int wy_gdn_recurrent_decode(const void *q, const int64_t *q_strides, const void 
  * ceil(T/64), rows past T zero.  k, v [T, H, 128] bf16 (unit inner stride,
  * 16-byte aligned rows), beta, g [T, H] fp32.  key_dim = value_dim = 128.
  * Replaces wy_lib::gdn_chunk_prepare_wy
- *   (triton_kernels/gdn_recurrent_prefill.py:823-876, kernel :249-411).
+ *   (triton_kernels/gdn_recurrent_prefill.py:703-826, kernel :249-402).
  */
 int wy_gdn_chunk_prepare_wy(const void *k, const int64_t *k_strides, const void *v,
                             const int64_t *v_strides, const float *beta,
@@ -419,7 +419,7 @@ int wy_gdn_chunk_prepare_wy(const void *k, const int64_t *k_strides, const void 
  * S = exp(G_last) S + k^T (delta exp(G_last - G_t)) with tokens past T
  * masked; final_state [H, key_dim, value_dim].  All fp32 contiguous.
  * Replaces wy_lib::gdn_chunk_state
- *   (triton_kernels/gdn_recurrent_prefill.py:885-960, kernel :417-538).
+ *   (triton_kernels/gdn_recurrent_prefill.py:829-936, kernel :405-562).
  */
 int wy_gdn_chunk_state(const void *k, const int64_t *k_strides, const float *w,
                        const float *u_base, const float *g_cumsum, float *delta,
@@ -431,7 +431,7 @@ int wy_gdn_chunk_state(const void *k, const int64_t *k_strides, const float *w,
  * exp(G_t - G_i) <q_t, k_i> delta_i, stored bf16 [T, H, value_dim] with
  * out_strides (unit inner stride).  q, k as stage 1.
  * Replaces wy_lib::gdn_chunk_output
- *   (triton_kernels/gdn_recurrent_prefill.py:969-1011, kernel :570-697).
+ *   (triton_kernels/gdn_recurrent_prefill.py:939-1023, kernel :565-690).
  */
 int wy_gdn_chunk_output(const void *q, const int64_t *q_strides, const void *k,
                         const int64_t *k_strides, const float *delta, const float *g_cumsum,

@@ -162,7 +162,7 @@ CHUNK = 64
 
 
 def gdn_chunk_prepare_wy(k, v, beta, g):
-    """Per 64-token chunk and head (gdn_recurrent_prefill.py:249-411):
+    """Per 64-token chunk and head (gdn_recurrent_prefill.py:249-402):
     G = cumsum(g) in the chunk; L[t, i] = beta_t exp(G_t - G_i) <k_t, k_i> for
     i < t; P = (I + L)^-1; u_base = P (beta v), w = P (beta exp(G) k).
     Tokens past T count as beta = g = 0 and k = v = 0.  fp64.  Returns
@@ -191,7 +191,7 @@ def gdn_chunk_prepare_wy(k, v, beta, g):
 
 
 def gdn_chunk_state(k, w, u_base, g_cumsum):
-    """Chunk recurrence (gdn_recurrent_prefill.py:417-538): chunk_state[c] =
+    """Chunk recurrence (gdn_recurrent_prefill.py:405-562): chunk_state[c] =
     the state entering chunk c; delta = u_base - w S; S = exp(G_last) S +
     k^T (delta * exp(G_last - G_t)), tokens past T masked.  fp64.
     Returns ``(delta [N, H, 64, DV], chunk_state [N, H, DK, DV], final [H, DK, DV])``."""
@@ -215,7 +215,7 @@ def gdn_chunk_state(k, w, u_base, g_cumsum):
 
 
 def gdn_chunk_output(q, k, delta, g_cumsum, chunk_state):
-    """Chunk outputs (gdn_recurrent_prefill.py:570-697): out_t = exp(G_t) q_t S_c
+    """Chunk outputs (gdn_recurrent_prefill.py:565-690): out_t = exp(G_t) q_t S_c
     + sum_{i <= t} exp(G_t - G_i) <q_t, k_i> delta_i.  fp64 ``[T, H, DV]``."""
     T, H, DK = q.shape
     N, _, _, DV = delta.shape
@@ -235,7 +235,7 @@ def gdn_chunk_output(q, k, delta, g_cumsum, chunk_state):
 
 def gdn_chunked(q, k, v, beta, g):
     """The three stages chained (call_gdn_recurrent_prefill_chunked_triton,
-    gdn_recurrent_prefill.py:1026-1046): ``(out fp64 [T, H, DV], state [H, DK, DV])``."""
+    gdn_recurrent_prefill.py:1026-1048): ``(out fp64 [T, H, DV], state [H, DK, DV])``."""
     w, u, G = gdn_chunk_prepare_wy(k, v, beta, g)
     delta, cs, final = gdn_chunk_state(k, w, u, G)
     return gdn_chunk_output(q, k, delta, G, cs), final

@@ -1,7 +1,7 @@
 // Gated DeltaNet chunk-64 (WY) prefill on gfx950: the delta-rule recurrence of
 // one long prompt in three launches instead of a token-by-token walk.
-// Reference: gdn_recurrent_prefill.py:249-411 (prepare), :417-538 (state),
-// :570-697 (output), ops :1050-1046 chain at :1026-1046.
+// Reference: gdn_recurrent_prefill.py:249-402 (prepare kernel), :405-562 (state),
+// :565-690 (output); ops :707-1023, the chain :1026-1051.
 //
 // Per chunk of 64 tokens and head, with G = cumsum(g) inside the chunk:
 //   L[t, i] = beta_t exp(G_t - G_i) <k_t, k_i>   (i < t)

@@ -150,7 +150,7 @@ def gdn_chunk_prepare_wy(
     k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor, g: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Per 64-token chunk and head: ``(w [N, H, 64, DK], u_base [N, H, 64, DV],
-    g_cumsum [N, H, 64])`` fp32 (reference gdn_recurrent_prefill.py:823-876)."""
+    g_cumsum [N, H, 64])`` fp32 (reference gdn_recurrent_prefill.py:703-826)."""
     assert k.ndim == 3 and v.ndim == 3
     assert k.shape[:2] == v.shape[:2]
     assert beta.ndim == 2 and g.ndim == 2
@@ -196,7 +196,7 @@ def gdn_chunk_state(
     k: torch.Tensor, w: torch.Tensor, u_base: torch.Tensor, g_cumsum: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """The chunk recurrence: ``(delta [N, H, 64, DV], chunk_state [N, H, DK, DV],
-    final_state [H, DK, DV])`` fp32 (reference gdn_recurrent_prefill.py:885-960)."""
+    final_state [H, DK, DV])`` fp32 (reference gdn_recurrent_prefill.py:829-936)."""
     assert k.ndim == 3 and k.dtype == torch.bfloat16
     assert w.ndim == 4 and u_base.ndim == 4 and g_cumsum.ndim == 3
     assert w.dtype == u_base.dtype == g_cumsum.dtype == torch.float32
@@ -241,7 +241,7 @@ def gdn_chunk_output(
     q: torch.Tensor, k: torch.Tensor, delta: torch.Tensor, g_cumsum: torch.Tensor,
     chunk_state: torch.Tensor,
 ) -> torch.Tensor:
-    """``out [T, H, DV]`` bf16 of every chunk (reference gdn_recurrent_prefill.py:969-1011)."""
+    """``out [T, H, DV]`` bf16 of every chunk (reference gdn_recurrent_prefill.py:939-1023)."""
     assert q.ndim == 3 and k.ndim == 3 and q.shape == k.shape
     assert q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16
     assert delta.ndim == 4 and delta.dtype == torch.float32
@@ -275,7 +275,7 @@ def call_gdn_chunk_output_triton(q, k, delta, g_cumsum, chunk_state):
 
 def call_gdn_recurrent_prefill_chunked_triton(q, k, v, beta, g):
     """One prompt through the three chunk launches: ``(out [T, H, DV] bf16,
-    final_state [H, DK, DV] fp32)`` (reference gdn_recurrent_prefill.py:1026-1046)."""
+    final_state [H, DK, DV] fp32)`` (reference gdn_recurrent_prefill.py:1026-1048)."""
     w, u_base, g_cumsum = gdn_chunk_prepare_wy(k, v, beta, g)
     delta, chunk_state, final_state = gdn_chunk_state(k, w, u_base, g_cumsum)
     return gdn_chunk_output(q, k, delta, g_cumsum, chunk_state), final_state
