@@ -156,155 +156,234 @@ __global__ __launch_bounds__(256) void gdn_chunk_prepare_kernel(
 // wv holds key rows 32 wv .. 32 wv + 31 as two 16-row tiles; lane l has rows
 // 16 dt + 4 (l/16) + j, column l%16.  Per chunk:
 //   delta (64 x 16) = u_base - w S     wave wv: token rows 16 wv .. +15
-//   dd = delta * exp(G_last - G_t)     (zero past T), via LDS
+//   dd = delta * exp(G_last - G_t)     (zero past T)
 //   S = exp(G_last) S + k^T dd
-// The k index of an MFMA may be any permutation shared by its A and B
-// operands: in w S lane (row r, group qd) takes keys 32 qd .. 32 qd + 31, so
-// its w operand is 32 consecutive floats of row r (one contiguous load,
-// fetched a chunk ahead); in k^T dd it takes tokens 16 qd .. 16 qd + 15.
-// Every operand of a product is read before its first MFMA.
-__global__ __launch_bounds__(256) void gdn_chunk_state_kernel(
+// The shared B operands (S of w S, dd of k^T dd) are split into bf16 hi/lo
+// once, by the lanes that own them, and published to LDS transposed
+// ([column][k index]) so that each lane's 8 consecutive k indices are one
+// 16-byte read.  The k index of an MFMA may be any permutation shared by its
+// A and B operands: in w S lane (row r, group qd) takes keys 32 qd .. 32 qd +
+// 31, so its w operand is 32 consecutive floats of row r (one contiguous
+// load, fetched a chunk ahead); in k^T dd it takes tokens 16 qd .. 16 qd + 15
+// and reads its k operand (8 tokens of one key row) from the row-major k
+// tile with two transposing reads.
+constexpr int kSPad = kDK + 8;   // bf16 row pitch of the transposed S
+constexpr int kDPad = kC + 8;    // bf16 row pitch of the transposed dd
+
+__device__ __forceinline__ u32x2_t lds_read_tr16(const bf16_t *p) {
+  typedef short i16x4_t __attribute__((ext_vector_type(4)));
+  const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4_t *)(p));
+  return __builtin_bit_cast(u32x2_t, r);
+}
+
+// four fp32 values -> (hi, lo) bf16 quads, x = hi + lo + O(2^-17 |x|)
+__device__ __forceinline__ void split4(const f32x4_t_ x, u32x2_t &hi, u32x2_t &lo) {
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const uint32_t hp = pack_bf16x2(x[2 * e], x[2 * e + 1]);
+    hi[e] = hp;
+    lo[e] = pack_bf16x2(x[2 * e] - __uint_as_float(hp << 16),
+                        x[2 * e + 1] - __uint_as_float(hp & 0xffff0000u));
+  }
+}
+
+// Two wave roles.  Waves 0-3 compute, as above, from LDS only.  Waves 4-7
+// move the data: they issue the global loads of chunk c + 2 at the start of
+// chunk c (two register sets), store chunk c's entering state and delta rows from LDS, and write
+// the loaded chunk into the other half of a double buffer before the chunk's
+// last barrier, with the decay factors exp(G_last - G_t) (zero past T) and
+// exp(G_last) computed once.  A CU streams only ~50 GB/s from L2, so the 56 KB a chunk
+// moves per workgroup takes about as long as the chunk's arithmetic; with
+// the roles split the two overlap instead of adding up.
+constexpr int kWPad = kDK + 4;   // fp32 row pitch of the w tile
+constexpr int kFPad = kDK + 4;   // fp32 row pitch of the transposed S (state store)
+struct StateLds {
+  float w[2][kC][kWPad];         // w of the chunk (A operand rows)
+  bf16_t k[2][kC][kKPad];        // k of the chunk, row-major
+  float u[2][kC][kBV];           // u_base columns v0 .. v0 + 15
+  float E[2][kC];                // exp(G_last - G_t), zero past T
+  float eg[4];                   // exp(G_last) (4: keeps the members after it 16-byte aligned)
+  bf16_t Sh[kBV][kSPad], Sl[kBV][kSPad];   // S^T hi / lo: B operand of w S
+  bf16_t Dh[kBV][kDPad], Dl[kBV][kDPad];   // dd^T hi / lo: B operand of k^T dd
+  float dl[kC][kBV];             // delta rows for the store
+  float Sf[kBV][kFPad];          // S^T fp32 for the state store
+};
+constexpr int kStateLds = int(sizeof(StateLds));
+static_assert(offsetof(StateLds, Sh) % 16 == 0 && offsetof(StateLds, Dh) % 16 == 0 &&
+                  offsetof(StateLds, dl) % 16 == 0 && offsetof(StateLds, Sf) % 16 == 0,
+              "16-byte LDS accesses");
+static_assert(kStateLds <= 160 * 1024, "state kernel LDS");
+
+__global__ __launch_bounds__(512) void gdn_chunk_state_kernel(
     const bf16_t *__restrict__ k, int64_t k_t, int64_t k_h, const float *__restrict__ w,
     const float *__restrict__ u, const float *__restrict__ gcs, float *__restrict__ delta,
     float *__restrict__ chunk_state, float *__restrict__ final_state, int T, int H, int N) {
-  // S as the B operand of w S: key row d holds its 16 columns at offset
-  // 16 ((d / 32) & 1) of a 32-float row, so the four lane groups (reading rows
-  // 32 qd + kq) meet in pairs on a bank, not all four
-  __shared__ __align__(16) float sS[kDK][2 * kBV];
-  __shared__ __align__(16) float sdd[kC][kBV + 1];   // dd as the B operand of k^T dd
-  __shared__ __align__(16) float sdl[kC][kBV];       // delta rows for the coalesced store
-  __shared__ __align__(16) bf16_t sk[kC][kKPad];     // k of the chunk (A operand of k^T dd)
-  __shared__ float sG[kC];
+  extern __shared__ __align__(16) unsigned char state_smem[];
+  StateLds &L = *reinterpret_cast<StateLds *>(state_smem);
   const int h = blockIdx.x, v0 = blockIdx.y * kBV, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, quad = lane >> 4;
+  const bool mover = wave >= 4;
+  const int ptid = tid - 256;   // mover thread index
 
-  f32x4_t_ S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
-  // the chunk's operands in registers: w row 16 wave + col, keys 32 quad ..
-  // +31 (8 x 16 bytes); k rows for LDS (4 x 16 bytes per thread); u_base of
-  // the lane's delta outputs; G
-  f32x4_t_ cw[8], nw[8];
-  u32x4_t nk[4];
-  float nu[4], cu[4];
-  float nG = 0.f;
-  auto fetch = [&](int c) {
-    const float *wr = w + ((int64_t(c) * H + h) * kC + 16 * wave + col) * kDK + 32 * quad;
+  // mover: chunk c's global loads into register set sl / into LDS buffer b
+  f32x4_t_ rw[2][8];
+  u32x4_t rk[2][4];
+  f32x4_t_ ru[2];
+  float rG[2] = {0.f, 0.f};
+  auto load = [&](int c, int sl) {
+    const float *wc = w + (int64_t(c) * H + h) * kC * kDK;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) nw[i] = *reinterpret_cast<const f32x4_t_ *>(wr + 4 * i);
-    const int t0 = c * kC, nval = min(kC, T - t0);
+    for (int i = 0; i < 8; ++i) {
+      const int e = ptid + 256 * i;
+      rw[sl][i] = *reinterpret_cast<const f32x4_t_ *>(wc + (e >> 5) * kDK + (e & 31) * 4);
+    }
+    const int t0 = c * kC, last = min(kC, T - t0) - 1;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i, r = e >> 4, cc = (e & 15) * 8;
-      nk[i] = r < nval ? ld16(k + int64_t(t0 + r) * k_t + h * k_h + cc) : u32x4_t{0u, 0u, 0u, 0u};
+      const int e = ptid + 256 * i, r = min(e >> 4, last);   // rows past T: zeroed at the write
+      rk[sl][i] = ld16(k + int64_t(t0 + r) * k_t + h * k_h + (e & 15) * 8);
     }
-    const float *uc = u + (int64_t(c) * H + h) * kC * kDV + v0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) nu[j] = uc[(16 * wave + 4 * quad + j) * kDV + col];
-    if (tid < kC) nG = gcs[(int64_t(c) * H + h) * kC + tid];
+    ru[sl] = *reinterpret_cast<const f32x4_t_ *>(u + ((int64_t(c) * H + h) * kC + (ptid >> 2)) * kDV +
+                                             v0 + (ptid & 3) * 4);
+    if (ptid < kC) rG[sl] = gcs[(int64_t(c) * H + h) * kC + ptid];
   };
-  fetch(0);
-  for (int c = 0; c < N; ++c) {
-    // the fetched chunk becomes current; publish S (B operand) and k
+  auto put = [&](int c, int b, int sl) {
+    const int nval = min(kC, T - c * kC);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) cw[i] = nw[i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      cu[j] = nu[j];
-      asm volatile("" : "+v"(cu[j]));  // copy now, before the next fetch reuses nu
+    for (int i = 0; i < 8; ++i) {
+      const int e = ptid + 256 * i;
+      *reinterpret_cast<f32x4_t_ *>(&L.w[b][e >> 5][(e & 31) * 4]) = rw[sl][i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i;
-      st16(&sk[e >> 4][(e & 15) * 8], nk[i]);
+      const int e = ptid + 256 * i;
+      st16(&L.k[b][e >> 4][(e & 15) * 8], (e >> 4) < nval ? rk[sl][i] : u32x4_t{0u, 0u, 0u, 0u});
     }
-    if (tid < kC) sG[tid] = nG;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = 32 * wave + 4 * quad + j;
-      sS[d][col + 16 * (wave & 1)] = S0[j];
-      sS[d + 16][col + 16 * (wave & 1)] = S1[j];
-    }
-    __syncthreads();
-    // this chunk's entering state, coalesced: 16-byte pieces of the rows of S
-    // (LDS offset 16 ((d / 32) & 1) within the 32-float row)
-    float *cs = chunk_state + (int64_t(c) * H + h) * kDK * kDV + v0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + 256 * i, d = e >> 2, p4 = (e & 3) * 4;
-      *reinterpret_cast<f32x4_t_ *>(cs + d * kDV + p4) =
-          *reinterpret_cast<const f32x4_t_ *>(&sS[d][p4 + 16 * ((d >> 5) & 1)]);
-    }
-    if (c + 1 < N) fetch(c + 1);
+    *reinterpret_cast<f32x4_t_ *>(&L.u[b][ptid >> 2][(ptid & 3) * 4]) = ru[sl];
+    const float G_last = __shfl(rG[sl], kC - 1);   // mover threads 0..63 are one wave
+    if (ptid < kC) L.E[b][ptid] = ptid < nval ? expf(G_last - rG[sl]) : 0.f;
+    if (ptid == 0) L.eg[b] = expf(G_last);
+  };
 
-    // delta rows 16 wave .. +15 = u_base - w S on bf16 MFMAs with both fp32
-    // operands split (hi hi + hi lo + lo hi); step ks covers keys
-    // 32 qd + 8 ks .. +7 of lane group qd
-    f32x4_t_ acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      float bx[8], ax[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bx[e] = sS[32 * quad + 8 * ks + e][col + 16 * (quad & 1)];
-        ax[e] = cw[2 * ks + (e >> 2)][e & 3];
-      }
-      u32x4_t ah, al, bh, bl;
-      split8(ax, ah, al);
-      split8(bx, bh, bl);
-      acc = mfma16x32(ah, bh, acc);
-      acc = mfma16x32(ah, bl, acc);
-      acc = mfma16x32(al, bh, acc);
-    }
-    const int t0 = c * kC, nval = min(kC, T - t0);
-    const float G_last = sG[kC - 1];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 16 * wave + 4 * quad + j;
-      const float d = cu[j] - acc[j];
-      sdl[t][col] = d;
-      sdd[t][col] = t < nval ? d * expf(G_last - sG[t]) : 0.f;
-    }
-    __syncthreads();
-    {  // delta rows, coalesced: one 16-byte piece per thread
-      float *dl = delta + (int64_t(c) * H + h) * kC * kDV + v0;
-      const int t = tid >> 2, p4 = (tid & 3) * 4;
-      *reinterpret_cast<f32x4_t_ *>(dl + t * kDV + p4) =
-          *reinterpret_cast<const f32x4_t_ *>(&sdl[t][p4]);
-    }
+  // compute waves: S rows 32 wave + 4 quad + j (S0) and + 16 (S1), column col
+  const int col = lane & 15, quad = lane >> 4;
+  const int dS = 32 * wave + 4 * quad;
+  f32x4_t_ S0 = {0.f, 0.f, 0.f, 0.f}, S1 = {0.f, 0.f, 0.f, 0.f};
 
-    // S = exp(G_last) S + k^T dd: A[d][t] = k[t][d] (bf16, exact), dd split;
-    // step ks covers tokens 16 qd + 8 ks .. +7 of lane group qd
-    const int d0 = 32 * wave + col;
-    const float eg = expf(G_last);
-    S0 *= eg;
-    S1 *= eg;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float bx[8];
-      u32x4_t a0, a1;
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const int t = 16 * quad + 8 * ks + e;
-        bx[e] = sdd[t][col];
-        bx[e + 1] = sdd[t + 1][col];
-        a0[e / 2] = uint32_t(sk[t][d0]) | (uint32_t(sk[t + 1][d0]) << 16);
-        a1[e / 2] = uint32_t(sk[t][d0 + 16]) | (uint32_t(sk[t + 1][d0 + 16]) << 16);
-      }
-      u32x4_t bh, bl;
-      split8(bx, bh, bl);
-      S0 = mfma16x32(a0, bh, S0);
-      S0 = mfma16x32(a0, bl, S0);
-      S1 = mfma16x32(a1, bh, S1);
-      S1 = mfma16x32(a1, bl, S1);
-    }
-    __syncthreads();  // sS / sdd / sk are rewritten by the next chunk
+  if (mover) {
+    load(0, 0);
+    put(0, 0, 0);
+    if (N > 1) load(1, 1);
   }
-  float *fs = final_state + int64_t(h) * kDK * kDV + v0;
+  __syncthreads();
+  for (int c0 = 0; c0 < N; c0 += 2)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int d = 32 * wave + 4 * quad + j;
-    fs[d * kDV + col] = S0[j];
-    fs[(d + 16) * kDV + col] = S1[j];
+  for (int b = 0; b < 2; ++b) {   // chunk c uses LDS buffer and register set c & 1
+    const int c = c0 + b;
+    if (c >= N) break;   // uniform over the workgroup
+    // ---- phase 1: publish S; the mover requests chunk c + 2
+    if (mover) {
+      if (c + 2 < N) load(c + 2, b);
+    } else {
+      u32x2_t h0, l0, h1, l1;
+      split4(S0, h0, l0);
+      split4(S1, h1, l1);
+      *reinterpret_cast<u32x2_t *>(&L.Sh[col][dS]) = h0;
+      *reinterpret_cast<u32x2_t *>(&L.Sl[col][dS]) = l0;
+      *reinterpret_cast<u32x2_t *>(&L.Sh[col][dS + 16]) = h1;
+      *reinterpret_cast<u32x2_t *>(&L.Sl[col][dS + 16]) = l1;
+      *reinterpret_cast<f32x4_t_ *>(&L.Sf[col][dS]) = S0;
+      *reinterpret_cast<f32x4_t_ *>(&L.Sf[col][dS + 16]) = S1;
+    }
+    __syncthreads();
+    // ---- phase 2: delta = u_base - w S and dd; the mover stores the entering state
+    if (mover) {
+      float *cs = chunk_state + (int64_t(c) * H + h) * kDK * kDV + v0;
+      const int cc = ptid & 15;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int d = 4 * ((ptid >> 4) + 16 * i);
+        const f32x4_t_ x = *reinterpret_cast<const f32x4_t_ *>(&L.Sf[cc][d]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cs[(d + e) * kDV + cc] = x[e];
+      }
+    } else {
+      // w S on bf16 MFMAs with both fp32 operands split (hi hi + hi lo + lo hi);
+      // step ks covers keys 32 qd + 8 ks .. +7 of lane group qd
+      f32x4_t_ acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float *wr = &L.w[b][16 * wave + col][32 * quad + 8 * ks];
+        const f32x4_t_ x0 = *reinterpret_cast<const f32x4_t_ *>(wr);
+        const f32x4_t_ x1 = *reinterpret_cast<const f32x4_t_ *>(wr + 4);
+        const u32x4_t bh = ld16(&L.Sh[col][32 * quad + 8 * ks]);
+        const u32x4_t bl = ld16(&L.Sl[col][32 * quad + 8 * ks]);
+        u32x2_t ah0, al0, ah1, al1;
+        split4(x0, ah0, al0);
+        split4(x1, ah1, al1);
+        const u32x4_t ah = {ah0[0], ah0[1], ah1[0], ah1[1]};
+        const u32x4_t al = {al0[0], al0[1], al1[0], al1[1]};
+        acc = mfma16x32(ah, bh, acc);
+        acc = mfma16x32(ah, bl, acc);
+        acc = mfma16x32(al, bh, acc);
+      }
+      const f32x4_t_ ex = *reinterpret_cast<const f32x4_t_ *>(&L.E[b][16 * wave + 4 * quad]);
+      f32x4_t_ dd;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int t = 16 * wave + 4 * quad + j;
+        const float d = L.u[b][t][col] - acc[j];
+        L.dl[t][col] = d;
+        dd[j] = d * ex[j];
+      }
+      u32x2_t dh, dl;
+      split4(dd, dh, dl);
+      *reinterpret_cast<u32x2_t *>(&L.Dh[col][16 * wave + 4 * quad]) = dh;
+      *reinterpret_cast<u32x2_t *>(&L.Dl[col][16 * wave + 4 * quad]) = dl;
+    }
+    __syncthreads();
+    // ---- phase 3: S = exp(G_last) S + k^T dd; the mover stores delta and
+    // fills the other buffer with chunk c + 1
+    if (mover) {
+      float *dlt = delta + (int64_t(c) * H + h) * kC * kDV + v0;
+      const int t = ptid >> 2, p4 = (ptid & 3) * 4;
+      *reinterpret_cast<f32x4_t_ *>(dlt + t * kDV + p4) =
+          *reinterpret_cast<const f32x4_t_ *>(&L.dl[t][p4]);
+      if (c + 1 < N) put(c + 1, b ^ 1, b ^ 1);
+    } else {
+      // A[d][t] = k[t][d] (bf16, exact), dd split; step ks covers tokens
+      // 16 qd + 8 ks .. +7 of lane group qd.  Transposing read: lane i of a
+      // 16-lane group receives element i%4 of the 4-token pieces addressed by
+      // lanes 4j + i/4, so lane L addresses token row t0 + L/4 at key 4 (L%4)
+      // of the tile's 16 keys.
+      const float eg = L.eg[b];
+      S0 *= eg;
+      S1 *= eg;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int tr = 16 * quad + 8 * ks + (col >> 2), dk = 32 * wave + 4 * (col & 3);
+        const u32x2_t p0 = lds_read_tr16(&L.k[b][tr][dk]), q0 = lds_read_tr16(&L.k[b][tr + 4][dk]);
+        const u32x2_t p1 = lds_read_tr16(&L.k[b][tr][dk + 16]);
+        const u32x2_t q1 = lds_read_tr16(&L.k[b][tr + 4][dk + 16]);
+        const u32x4_t a0 = {p0[0], p0[1], q0[0], q0[1]}, a1 = {p1[0], p1[1], q1[0], q1[1]};
+        const u32x4_t bh = ld16(&L.Dh[col][16 * quad + 8 * ks]);
+        const u32x4_t bl = ld16(&L.Dl[col][16 * quad + 8 * ks]);
+        S0 = mfma16x32(a0, bh, S0);
+        S0 = mfma16x32(a0, bl, S0);
+        S1 = mfma16x32(a1, bh, S1);
+        S1 = mfma16x32(a1, bl, S1);
+      }
+    }
+    __syncthreads();  // the next chunk rewrites Sh/Sl/Sf/Dh/Dl/dl and reads buffer b ^ 1
+  }
+  if (!mover) {
+    float *fs = final_state + int64_t(h) * kDK * kDV + v0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      fs[(dS + j) * kDV + col] = S0[j];
+      fs[(dS + 16 + j) * kDV + col] = S1[j];
+    }
   }
 }
 
@@ -408,7 +487,15 @@ extern "C" int wy_gdn_chunk_state(const void *k, const int64_t *ks, const float 
   if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
   if (!rows_ok(k, ks) || !wyh::aligned16(w)) return WY_E_LAYOUT;
   const int N = (token_num + kC - 1) / kC;
-  gdn_chunk_state_kernel<<<dim3(num_heads, kDV / kBV), 256, 0, static_cast<hipStream_t>(stream)>>>(
+  static bool lds_set = false;   // the attribute is per function, set once
+  if (!lds_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gdn_chunk_state_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kStateLds);
+    if (e != hipSuccess) return int(e);
+    lds_set = true;
+  }
+  gdn_chunk_state_kernel<<<dim3(num_heads, kDV / kBV), 512, kStateLds,
+                           static_cast<hipStream_t>(stream)>>>(
       static_cast<const bf16_t *>(k), ks[0], ks[1], w, u_base, g_cumsum, delta, chunk_state,
       final_state, token_num, num_heads, N);
   return wyh::launch_status();
