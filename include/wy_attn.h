@@ -236,7 +236,7 @@ int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_kv_heads, in
  *   attention_gate_pack                (triton_kernels/attention_gate_pack.py:77-126)
  *   paged_kv_fill_varlen               (triton_kernels/gqa_attention_decode_paged.py:492-561)
  * q [T, H_q, D], k / v [T, H_kv, D] (after q/k norm; unit inner stride, rows
- * 16-byte aligned), gate [T, H_q, D] view (unit inner stride, 8-byte aligned
+ * 16-byte aligned), gate [T, H_q, D] view (unit inner stride, 16-byte aligned
  * rows), position_ids [T] (element stride pos_stride; int32, or int64 with
  * pos_is_int64 = 1), inv_freq [rotary_dim / 2] fp32, rotary_dim 64.
  * Launch 1 rotates K, writes K and V into the pages (block_table /

@@ -57,6 +57,10 @@ constexpr int kKDma = kTileK / 1024 + (kTileK % 1024 != 0);  // 1 KiB DMA blocks
 constexpr int kVDma = kTileV / 1024;                          // 36
 static_assert(kTileV % 1024 == 0, "V tile is a whole number of DMA blocks");
 constexpr int kLdsBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 KiB
+// Output staging in the epilogue (reuses the rings): 32 rows of 4 heads x
+// 256 dims, rows padded by 16 bytes against bank conflicts of the lane writes.
+constexpr int kStagePitch = 4 * 256 + 8;   // bf16
+static_assert(32 * kStagePitch * 2 <= kLdsBytes, "output stage fits the rings");
 // Exponentials are taken against a per-row reference fixed by the first KV
 // tile; a later score may exceed it by a factor up to 2^64 (P stays finite in
 // bf16 and fp32).  Beyond that the block is recomputed exactly.
@@ -341,10 +345,13 @@ void varlen_causal_prefill_kernel(
   // The q loads are issued before the first tiles' DMA, so they do not queue
   // behind it; the conversion waits for q only.
   bf16x8_t qb_op[16];
-  // Attention block: the row's gate values, requested with q so that their
-  // latency is hidden behind the block (one 8-byte chunk per output chunk of
-  // the epilogue; the loads are all issued before any is used).
-  u32x2_t gate_v[8][4];
+  // Attention block: the gate values of the pieces this thread stores in the
+  // epilogue (rows r0, r0 + 2, ..., 16 bytes at column c8 of the 4 heads'
+  // 2 KiB row), requested with q so that their latency is hidden behind the
+  // block; whole rows per load instruction.
+  static_assert(kG * kD == 1024, "two output rows per workgroup step");
+  const int r0 = tid >> 7, c8 = (tid & 127) * 8;
+  u32x4_t gate_c[kRot > 0 ? kBQ / 2 : 1];
   {
     const int qc = qrow < n ? qrow : n - 1;
     const bf16_t *qp = q + (int64_t(start) + qc) * qs_t + hq * qs_h + g * 8;
@@ -365,12 +372,12 @@ void varlen_causal_prefill_kernel(
     }
     issue_first();
     if constexpr (kRot > 0) {
-      const bf16_t *gp = blk.gate + (int64_t(start) + qc) * blk.gs_t + hq * blk.gs_h + 4 * g;
+      const int last = n - 1 - q0;   // rows past the sequence re-read its last row
+      const bf16_t *gp = blk.gate + (int64_t(start) + q0) * blk.gs_t +
+                         (h * kG + c8 / kD) * blk.gs_h + c8 % kD;
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          gate_v[dt][j] = *reinterpret_cast<const u32x2_t *>(gp + dt * 32 + 8 * j);
+      for (int i = 0; i < kBQ / 2; ++i)
+        gate_c[i] = ld16(gp + int64_t(min(r0 + 2 * i, last)) * blk.gs_t);
     }
     if constexpr (kRot > 0) {
       // Partial RoPE of the raw row, the standalone kernel's device math and
@@ -599,26 +606,42 @@ void varlen_causal_prefill_kernel(
   }
 
   // ---- normalise and store: lane holds row qrow, dims dt*32 + 8j + 4g + i -------
+  // The block's output is 32 rows of 4 heads x 256 dims, each row one 2 KiB
+  // run in memory.  The lanes' 8-byte pieces (16 bytes of each row per store
+  // instruction) are staged in LDS and written back as whole rows: each store
+  // instruction then covers 1 KiB of one row instead of 32 rows.
   const float inv_l = 1.0f / l;
-  if (qrow < n) {
-    bf16_t *op = out + (int64_t(start) + qrow) * os_t + hq * os_h;
+  __syncthreads();   // every wave is past its last K/V read of the rings
+  bf16_t *const stage = reinterpret_cast<bf16_t *>(smem);
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
-                     pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
-        if constexpr (kRot > 0) {
-          // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
-          // gate pack computes it
-          const u32x2_t gv = gate_v[dt][j];
+    for (int j = 0; j < 4; ++j) {
+      const u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
+                         pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
+      *reinterpret_cast<u32x2_t *>(stage + col * kStagePitch + wave * kD + dt * 32 + 8 * j + 4 * g) = w;
+    }
+  __syncthreads();
+  {
+    // 256 threads x 16 bytes = two rows per step; thread tid keeps its column
+    const int rows = min(kBQ, n - q0);
+    bf16_t *ob = out + (int64_t(start) + q0 + r0) * os_t + (h * kG + c8 / kD) * os_h + c8 % kD;
+    const bf16_t *sp = stage + r0 * kStagePitch + c8;
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
-            w[e] = pack_bf16x2(bf16_lo(w[e]) * gate_sigmoid(bf16_lo(gv[e])),
-                               bf16_hi(w[e]) * gate_sigmoid(bf16_hi(gv[e])));
-        }
-        *reinterpret_cast<u32x2_t *>(op + dt * 32 + 8 * j + 4 * g) = w;
+    for (int i = 0; i < kBQ / 2; ++i) {
+      u32x4_t w = ld16(sp);
+      if constexpr (kRot > 0) {
+        // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
+        // gate pack computes it
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack_bf16x2(bf16_lo(w[e]) * gate_sigmoid(bf16_lo(gate_c[i][e])),
+                             bf16_hi(w[e]) * gate_sigmoid(bf16_hi(gate_c[i][e])));
       }
+      if (r0 + 2 * i < rows) st16(ob, w);
+      ob += 2 * os_t;
+      sp += 2 * kStagePitch;
+    }
   }
   if constexpr (!kList) return;
   // Every wave is past its last LDS read of this block before the next
@@ -685,9 +708,9 @@ int set_prefill_lds() {
 bool prefill_layout_ok(const void *q, const int64_t *qs, const void *k, const int64_t *ks,
                        const void *v, const int64_t *vs, const void *out, const int64_t *os) {
   return !(qs[2] != 1 || ks[2] != 1 || vs[2] != 1 || os[2] != 1 || qs[0] % 8 || qs[1] % 8 ||
-           ks[0] % 8 || ks[1] % 8 || vs[0] % 8 || vs[1] % 8 || os[0] % 4 || os[1] % 4 ||
+           ks[0] % 8 || ks[1] % 8 || vs[0] % 8 || vs[1] % 8 || os[0] % 8 || os[1] % 8 ||
            !wyh::aligned16(q) || !wyh::aligned16(k) || !wyh::aligned16(v) ||
-           (reinterpret_cast<uintptr_t>(out) & 7u));
+           !wyh::aligned16(out));
 }
 
 // Validated arguments -> one launch (direct or queue).
@@ -771,7 +794,7 @@ extern "C" int wy_prefill_attention_block(
   const int64_t krs[3] = {int64_t(num_kv_heads) * head_dim, head_dim, 1};
   const int64_t os[3] = {int64_t(num_q_heads) * head_dim, head_dim, 1};
   if (!prefill_layout_ok(q, qs, k_roped, krs, v, vs, out, os) || ks[2] != 1 || gs[2] != 1 ||
-      gs[0] % 4 || gs[1] % 4 || (reinterpret_cast<uintptr_t>(gate) & 7u))
+      gs[0] % 8 || gs[1] % 8 || !wyh::aligned16(gate))
     return WY_E_LAYOUT;
   if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
       (reinterpret_cast<uintptr_t>(workspace) & 3u))

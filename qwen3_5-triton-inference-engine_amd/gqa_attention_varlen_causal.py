@@ -93,6 +93,8 @@ def prefill_attention_block(
     total_tokens, num_q_head, d_model = q.shape
     num_kv_head = k.shape[1]
     assert k.shape == v.shape and k.shape[0] == total_tokens and k.shape[2] == d_model
+    if gate.stride(2) != 1 or gate.stride(0) % 8 or gate.stride(1) % 8 or gate.data_ptr() % 16:
+        gate = gate.contiguous()   # the epilogue reads 16-byte pieces of gate rows
     assert cu_seqlens.dtype == torch.int32 and cu_seqlens.is_contiguous()
     assert position_ids.dtype in (torch.int32, torch.int64)
     assert position_ids.numel() == total_tokens

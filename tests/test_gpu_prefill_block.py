@@ -93,3 +93,23 @@ def test_block_vs_oracle(pkg, dev):
             torch.testing.assert_close(row[:, :64].float(), kr[s0 + t][:, :64].float(),
                                        atol=2e-2, rtol=1e-2)
             assert torch.equal(vc[phys, :, t % 16].cpu(), vcpu[s0 + t])
+
+
+def test_block_gate_view_offsets(pkg, dev):
+    """The gate as a view of a wider projection output, at a 16-byte-aligned
+    offset (read in place) and at an 8-byte offset (copied first): the same
+    bytes as with a contiguous gate."""
+    say("prefill block gate views")
+    lengths = [40, 130, 7]
+    q, k, v, gate, bt, kc, vc, packed = make(pkg, dev, lengths, 12)
+    inv = pkg.rope_inv_freq(64, 1e7, device=dev)
+    T = sum(lengths)
+    ref = pkg.prefill_attention_block(q, k, v, gate, inv, 64, packed, kc.clone(), vc.clone(), bt)
+    for off in (8, 4):
+        wide = torch.zeros(T, HQ * D + 16, dtype=torch.bfloat16, device=dev)
+        wide[:, off:off + HQ * D] = gate
+        view = wide[:, off:off + HQ * D]
+        got = pkg.prefill_attention_block(q, k, v, view, inv, 64, packed, kc.clone(), vc.clone(),
+                                          bt)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), off
