@@ -50,9 +50,11 @@ constexpr int kBN = 64;                  // kv tokens per tile
 constexpr int kKSlots = kD / 8 + 1;      // 33 slots per K row
 constexpr int kVSlots = kD / 8 + 4;      // 36 slots per V row
 constexpr int kKPitch = kKSlots * 16;    // 528 B
+constexpr int kQPitch = 528;             // q staging rows (512 B + 16 against bank conflicts)
 constexpr int kVPitch = kVSlots * 16;    // 576 B
 constexpr int kTileK = kBN * kKPitch;    // 33792 B
 constexpr int kTileV = kBN * kVPitch;    // 36864 B
+static_assert(2 * 32 * kQPitch <= kTileV, "two waves' q rows fit one V slot");
 constexpr int kKDma = kTileK / 1024 + (kTileK % 1024 != 0);  // 1 KiB DMA blocks: 33
 constexpr int kVDma = kTileV / 1024;                          // 36
 static_assert(kTileV % 1024 == 0, "V tile is a whole number of DMA blocks");
@@ -343,7 +345,10 @@ void varlen_causal_prefill_kernel(
   // pre-multiplied by scale*log2(e) and rounded to bf16 as the reference does
   // (gqa_attention_varlen_causal.py:146,158): scores come out in log2 units.
   // The q loads are issued before the first tiles' DMA, so they do not queue
-  // behind it; the conversion waits for q only.
+  // behind it; the conversion waits for q only.  Each wave loads its head's
+  // 32 rows whole (two 512-byte rows per load instruction) and regroups them
+  // through LDS into the lanes' 16-byte slices: the V slot of tile 1, not
+  // written before the first tile loop, holds two waves' rows at a time.
   bf16x8_t qb_op[16];
   // Attention block: the gate values of the pieces this thread stores in the
   // epilogue (rows r0, r0 + 2, ..., 16 bytes at column c8 of the 4 heads'
@@ -354,10 +359,15 @@ void varlen_causal_prefill_kernel(
   u32x4_t gate_c[kRot > 0 ? kBQ / 2 : 1];
   {
     const int qc = qrow < n ? qrow : n - 1;
-    const bf16_t *qp = q + (int64_t(start) + qc) * qs_t + hq * qs_h + g * 8;
     u32x4_t xr[16];
+    {
+      // rows past the sequence re-read its last row (zeroed below)
+      const int last = n - 1 - q0;
+      const bf16_t *qp = q + (int64_t(start) + q0) * qs_t + hq * qs_h + (lane & 31) * 8;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) xr[kk] = ld16(qp + 16 * kk);
+      for (int i = 0; i < 16; ++i)
+        xr[i] = ld16(qp + int64_t(min(2 * i + (lane >> 5), last)) * qs_t);
+    }
     // the row's sin / cos for its rotary dims (written by the K/V launch)
     f32x4_t tsn[kRot > 0 ? kRot / 16 : 1], tcs[kRot > 0 ? kRot / 16 : 1];
     if constexpr (kRot > 0) {
@@ -378,6 +388,27 @@ void varlen_causal_prefill_kernel(
 #pragma unroll
       for (int i = 0; i < kBQ / 2; ++i)
         gate_c[i] = ld16(gp + int64_t(min(r0 + 2 * i, last)) * blk.gs_t);
+    }
+    {
+      unsigned char *const qst = v_ring + kTileV + (wave & 1) * (kBQ * kQPitch);
+#pragma unroll
+      for (int round = 0; round < 2; ++round) {
+        if ((wave >> 1) == round) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            st16(qst + (2 * i + (lane >> 5)) * kQPitch + (lane & 31) * 16, xr[i]);
+#pragma unroll
+          for (int kk = 0; kk < 16; ++kk) xr[kk] = ld16(qst + col * kQPitch + kk * 32 + g * 16);
+          if (round == 1 && n < n_tiles * kBN) {
+            // the slot must hold finite values past the sequence (see above)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              st16(qst + (2 * i + (lane >> 5)) * kQPitch + (lane & 31) * 16,
+                   u32x4_t{0u, 0u, 0u, 0u});
+          }
+        }
+        if (round == 0) __syncthreads();
+      }
     }
     if constexpr (kRot > 0) {
       // Partial RoPE of the raw row, the standalone kernel's device math and
