@@ -81,9 +81,9 @@ __global__ __launch_bounds__(256) void paged_kv_fill_varlen_kernel(
       const int j = is_v ? i - total : i;
       const int r = j / cpr, c = (j - r * cpr) * 8;
       if (!is_v)
-        st16(kdst + r * kc_s + c, ld16(ksrc + r * k_t + c));
+        st16_nt(kdst + r * kc_s + c, ld16(ksrc + r * k_t + c));
       else
-        st16(vdst + r * vc_s + c, ld16(vsrc + r * v_t + c));
+        st16_nt(vdst + r * vc_s + c, ld16(vsrc + r * v_t + c));
     }
   } else {
     const int total = rows * D;
@@ -191,19 +191,19 @@ __global__ __launch_bounds__(256) void prefill_kv_rope_fill_kernel(
         }
         bf16_t *dst = kc + phys * kc_p + h * kc_h + r * kc_s + c * 8;
         bf16_t *kdup = kr + h * kr_h + (tok0 + r) * kr_t + c * 8;
-        st16(dst, oa);
-        st16(dst + half, ob);
-        st16(kdup, oa);
-        st16(kdup + half, ob);
+        st16_nt(dst, oa);
+        st16_nt(dst + half, ob);
+        st16_nt(kdup, oa);
+        st16_nt(kdup + half, ob);
       } else if (i < n_rot + n_kcopy) {
         const int j = i - n_rot;
         const int r = j / kcopy, c = 2 * hr + (j - r * kcopy);
-        st16(kc + phys * kc_p + h * kc_h + r * kc_s + c * 8, x0[u]);
-        st16(kr + h * kr_h + (tok0 + r) * kr_t + c * 8, x0[u]);
+        st16_nt(kc + phys * kc_p + h * kc_h + r * kc_s + c * 8, x0[u]);
+        st16_nt(kr + h * kr_h + (tok0 + r) * kr_t + c * 8, x0[u]);
       } else if (i < total) {
         const int j = i - n_rot - n_kcopy;
         const int r = j / cpr, c = j - r * cpr;
-        st16(vc + phys * vc_p + h * vc_h + r * vc_s + c * 8, x0[u]);
+        st16_nt(vc + phys * vc_p + h * vc_h + r * vc_s + c * 8, x0[u]);
       }
     }
   }

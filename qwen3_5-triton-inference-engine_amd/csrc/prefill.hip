@@ -669,7 +669,7 @@ void varlen_causal_prefill_kernel(
           w[e] = pack_bf16x2(bf16_lo(w[e]) * gate_sigmoid(bf16_lo(gate_c[i][e])),
                              bf16_hi(w[e]) * gate_sigmoid(bf16_hi(gate_c[i][e])));
       }
-      if (r0 + 2 * i < rows) __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t *>(ob));
+      if (r0 + 2 * i < rows) st16_nt(ob, w);
       ob += 2 * os_t;
       sp += 2 * kStagePitch;
     }

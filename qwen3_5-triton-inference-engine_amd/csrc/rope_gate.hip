@@ -63,8 +63,8 @@ __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
         oa[w] = pack_bf16x2(o1l, o1h);
         ob[w] = pack_bf16x2(o2l, o2h);
       }
-      st16(orow + (h0 + i) * os_h + c * 8, oa);
-      st16(orow + (h0 + i) * os_h + R / 2 + c * 8, ob);
+      st16_nt(orow + (h0 + i) * os_h + c * 8, oa);
+      st16_nt(orow + (h0 + i) * os_h + R / 2 + c * 8, ob);
     }
     return;
   }
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
     h = int(bh % uint32_t(H));
     b = int(bh / uint32_t(H));
   }
-  st16(out + b * os_b + h * os_h + t * os_t + c * 8, ld16(x + b * xs_b + h * xs_h + t * xs_t + c * 8));
+  st16_nt(out + b * os_b + h * os_h + t * os_t + c * 8, ld16(x + b * xs_b + h * xs_h + t * xs_t + c * 8));
 }
 
 // Generic path: one lane per output element, any strides, any even R <= D.
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void gate_pack_vec_kernel(
     const float sh = gate_sigmoid(bf16_hi(gv[w]));
     o[w] = pack_bf16x2(bf16_lo(xv[w]) * sl, bf16_hi(xv[w]) * sh);
   }
-  st16(out + gid * 8, o);
+  st16_nt(out + gid * 8, o);
 }
 
 __global__ __launch_bounds__(256) void gate_pack_generic_kernel(

@@ -50,6 +50,12 @@ __device__ __forceinline__ u32x4_t ld16(const void *p) {
 __device__ __forceinline__ void st16(void *p, u32x4_t v) {
   *reinterpret_cast<u32x4_t *>(p) = v;
 }
+// Non-temporal 16-byte store (global_store ... nt): for bulk outputs that
+// this launch does not read back, so they stream out while the kernel runs
+// rather than sit dirty in L2 until the end-of-kernel writeback.
+__device__ __forceinline__ void st16_nt(void *p, u32x4_t v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(p));
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
