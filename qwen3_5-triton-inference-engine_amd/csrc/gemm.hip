@@ -416,7 +416,39 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   }
 
   // acc[i][j] register r of lane l: row (r&3) + 8(r>>2) + 4(l/32) of m-tile i,
-  // column l%32 of n-tile j.
+  // column l%32 of n-tile j.  With 16-byte-aligned output rows each wave
+  // stages its sub-tile in LDS (the ring is free once every wave is past its
+  // last operand read) and writes whole 16-byte pieces of its rows with
+  // non-temporal stores; otherwise element by element.
+  constexpr int kRW = BM / WM, kCW = BN / WN;   // the wave's sub-tile
+  constexpr int kSP = kCW * 2 + 16;             // staged row pitch, bytes
+  static_assert(C::kWaves * kRW * kSP <= C::kLds, "output stage fits the ring");
+  const bool vec_out = ((N | ys0) & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  if (vec_out) {
+    __syncthreads();
+    unsigned char *const stg = smem + wave * (kRW * kSP);
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
+          *reinterpret_cast<bf16_t *>(stg + row * kSP + (32 * j + r32) * 2) =
+              bf16_t(f32_to_bf16_bits(acc[i][j][r]));
+        }
+    // one wave writes and reads its own region: its LDS operations complete
+    // in issue order
+    constexpr int kCPR = kCW / 8;   // 16-byte pieces per row
+#pragma unroll 4
+    for (int e = lane; e < kRW * kCPR; e += 64) {
+      const int row = e / kCPR, c = e - row * kCPR;
+      const int grow = m0 + kRW * wm + row, gcol = n0 + kCW * wn + 8 * c;
+      if (grow < M && gcol < N)
+        st16_nt(y + int64_t(grow) * ys0 + gcol, ld16(stg + row * kSP + 16 * c));
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kFM; ++i)
 #pragma unroll
