@@ -295,6 +295,8 @@ template <int kFM, int kFN>
 __device__ __forceinline__ void lgkm_wait_all(u32x4_t (&a)[kFM], u32x4_t (&b)[kFN]) {
   if constexpr (kFM == 2 && kFN == 2)
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
+  else if constexpr (kFM == 2 && kFN == 1)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]));
   else if constexpr (kFM == 4 && kFN == 2)
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]));
@@ -488,6 +490,10 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
   const int64_t big = int64_t((M + 255) / 256) * ((N + 255) / 256);
   if (big >= 256 && (big % 256 == 0 || big >= 1024))
     return launch_tiled_cfg<256, 256, 2, 4>(x, xs0, w, ws0, y, ys0, M, N, K, st);
+  // fewer 128 x 128 tiles than CUs (e.g. a narrow k_proj): 128 x 64 tiles
+  // put twice as many workgroups on the chip
+  const int64_t mid = int64_t((M + 127) / 128) * ((N + 127) / 128);
+  if (mid < 256) return launch_tiled_cfg<128, 64, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
   return launch_tiled_cfg<128, 128, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
 }
 
