@@ -490,10 +490,10 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
   const int64_t big = int64_t((M + 255) / 256) * ((N + 255) / 256);
   if (big >= 256 && (big % 256 == 0 || big >= 1024))
     return launch_tiled_cfg<256, 256, 2, 4>(x, xs0, w, ws0, y, ys0, M, N, K, st);
-  // fewer 128 x 128 tiles than CUs (e.g. a narrow k_proj): 128 x 64 tiles
-  // put twice as many workgroups on the chip
+  // fewer 128 x 128 tiles than two per CU (e.g. k_proj and o_proj at 4096
+  // tokens): 128 x 64 tiles put twice as many workgroups on the chip
   const int64_t mid = int64_t((M + 127) / 128) * ((N + 127) / 128);
-  if (mid < 256) return launch_tiled_cfg<128, 64, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
+  if (mid < 512) return launch_tiled_cfg<128, 64, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
   return launch_tiled_cfg<128, 128, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
 }
 
