@@ -17,8 +17,9 @@
 // of mantissa) and a product of two fp32 operands is hi*hi + hi*lo + lo*hi on
 // v_mfma_f32_16x16x32_bf16 (relative error ~2^-16; the reference uses
 // three-pass tf32 for the same products); a bf16 x fp32 product is two such
-// MFMAs.  The output kernel's products run on v_mfma_f32_16x16x4_f32.  (I + L)^-1 is applied by forward substitution on
-// the right-hand sides, one column per thread, in fp32.
+// MFMAs; the output kernel's fp32 operands are split the same way.
+// (I + L)^-1 is applied by forward substitution on the right-hand sides, one
+// column per thread, in fp32.
 #include "wy_common.h"
 
 using namespace wy;
@@ -33,9 +34,6 @@ constexpr int kKPad = kDK + 8;
 
 typedef float f32x4_t_ __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f32x4_t_ mfma16x4(float a, float b, f32x4_t_ c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x4_t_ mfma16x32(u32x4_t a, u32x4_t b, f32x4_t_ c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -391,58 +389,130 @@ __global__ __launch_bounds__(512) void gdn_chunk_state_kernel(
 //
 // out (64 x 128) = exp(G_t) q S_c + A delta with A[t][i] = <q_t, k_i>
 // exp(G_t - G_i) (i <= t).  Wave wv owns token rows 16 wv .. +15 and all 128
-// value columns (8 tiles of 16 x 16); both products run on 16x16x4 fp32 MFMAs
-// with the B operands (S_c, delta) streamed from global memory.
+// value columns (8 tiles of 16 x 16) on v_mfma_f32_16x16x32_bf16: q is bf16
+// (exact), S_c and delta are split once into bf16 hi / lo planes in LDS
+// (row-major; their k index runs down the rows, so each lane's 8 consecutive
+// k values come from two transposing reads), A is split in registers; q S_c
+// takes 2 products per step (q S_hi + q S_lo), A delta 3 (hi hi + hi lo + lo hi).
+constexpr int kOPad = kDV + 8;   // bf16 row pitch of the S_c / delta planes
+struct OutLds {
+  bf16_t qs[kC][kKPad];
+  bf16_t ks[kC][kKPad];
+  float A[kC][kC + 4];
+  bf16_t Sh[kDK][kOPad], Sl[kDK][kOPad];   // S_c split (rows = keys)
+  bf16_t Dh[kC][kOPad], Dl[kC][kOPad];     // delta split (rows = chunk tokens)
+  float sG[kC];
+};
+constexpr int kOutLds = int(sizeof(OutLds));
+static_assert(kOutLds <= 160 * 1024, "output kernel LDS");
+static_assert(offsetof(OutLds, Sh) % 16 == 0 && offsetof(OutLds, Dh) % 16 == 0 &&
+                  offsetof(OutLds, A) % 16 == 0 && offsetof(OutLds, ks) % 16 == 0,
+              "16-byte LDS accesses");
+
 __global__ __launch_bounds__(256) void gdn_chunk_output_kernel(
     const bf16_t *__restrict__ q, int64_t q_t, int64_t q_h, const bf16_t *__restrict__ k,
     int64_t k_t, int64_t k_h, const float *__restrict__ delta, const float *__restrict__ gcs,
     const float *__restrict__ chunk_state, bf16_t *__restrict__ out, int64_t o_t, int64_t o_h,
     int T, int H) {
-  __shared__ __align__(16) bf16_t qs[kC][kKPad];
-  __shared__ __align__(16) bf16_t ks[kC][kKPad];
-  __shared__ __align__(16) float A[kC][kC + 4];
-  __shared__ float sG[kC];
+  extern __shared__ __align__(16) unsigned char out_smem[];
+  OutLds &L = *reinterpret_cast<OutLds *>(out_smem);
   const int n = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, quad = lane >> 4;
   const int t0 = n * kC;
   const int nval = min(kC, T - t0);
-  load_rows(qs, q + int64_t(t0) * q_t + h * q_h, q_t, nval);
-  load_rows(ks, k + int64_t(t0) * k_t + h * k_h, k_t, nval);
-  if (tid < kC) sG[tid] = gcs[(int64_t(n) * H + h) * kC + tid];
+  // S_c and delta: 16-byte loads, split into the hi / lo planes
+  const float *Sc = chunk_state + (int64_t(n) * H + h) * kDK * kDV;
+  const float *dl = delta + (int64_t(n) * H + h) * kC * kDV;
+  f32x4_t_ sv[16], dv[8];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = tid + 256 * i;
+    sv[i] = *reinterpret_cast<const f32x4_t_ *>(Sc + (e >> 5) * kDV + (e & 31) * 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tid + 256 * i;
+    dv[i] = *reinterpret_cast<const f32x4_t_ *>(dl + (e >> 5) * kDV + (e & 31) * 4);
+  }
+  load_rows(L.qs, q + int64_t(t0) * q_t + h * q_h, q_t, nval);
+  load_rows(L.ks, k + int64_t(t0) * k_t + h * k_h, k_t, nval);
+  if (tid < kC) L.sG[tid] = gcs[(int64_t(n) * H + h) * kC + tid];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = tid + 256 * i;
+    u32x2_t hi, lo;
+    split4(sv[i], hi, lo);
+    *reinterpret_cast<u32x2_t *>(&L.Sh[e >> 5][(e & 31) * 4]) = hi;
+    *reinterpret_cast<u32x2_t *>(&L.Sl[e >> 5][(e & 31) * 4]) = lo;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int e = tid + 256 * i;
+    u32x2_t hi, lo;
+    split4(dv[i], hi, lo);
+    *reinterpret_cast<u32x2_t *>(&L.Dh[e >> 5][(e & 31) * 4]) = hi;
+    *reinterpret_cast<u32x2_t *>(&L.Dl[e >> 5][(e & 31) * 4]) = lo;
+  }
   __syncthreads();
   if (wave != 1) {
-    const f32x16_t qk = gram64(qs, ks, wave, lane);
+    const f32x16_t qk = gram64(L.qs, L.ks, wave, lane);
     const int i = 32 * (wave & 1) + (lane & 31);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = 32 * (wave >> 1) + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
-      A[t][i] = (i <= t && t < nval) ? qk[r] * expf(sG[t] - sG[i]) : 0.f;
+      L.A[t][i] = (i <= t && t < nval) ? qk[r] * expf(L.sG[t] - L.sG[i]) : 0.f;
     }
   } else {
-    for (int e = lane; e < 32 * 32; e += 64) A[e >> 5][32 + (e & 31)] = 0.f;
+    for (int e = lane; e < 32 * 32; e += 64) L.A[e >> 5][32 + (e & 31)] = 0.f;
   }
   __syncthreads();
 
-  const float *Sc = chunk_state + (int64_t(n) * H + h) * kDK * kDV;
-  const float *dl = delta + (int64_t(n) * H + h) * kC * kDV;
-  const int trow = 16 * wave + col;  // A-operand row of this lane
+  // B operand of k-step rows r0 .. r0 + 31 (lane group quad: rows r0 + 8 quad
+  // .. +7) and value columns 16 vt .. +15 of a plane: lane L of the 16-lane
+  // group addresses row r0 + 8 quad + L/4 (+4) at column 16 vt + 4 (L%4)
+  const int trow = 8 * quad + (col >> 2), tcol = 4 * (col & 3);
+  auto bop = [&](const bf16_t (*P)[kOPad], int r0, int vt) {
+    const u32x2_t p = lds_read_tr16(&P[r0 + trow][16 * vt + tcol]);
+    const u32x2_t q2 = lds_read_tr16(&P[r0 + trow + 4][16 * vt + tcol]);
+    return u32x4_t{p[0], p[1], q2[0], q2[1]};
+  };
+  const int arow = 16 * wave + col;   // A-operand row of this lane
+  // q rows (bf16) for the 4 key steps; A rows split for the 2 token steps
+  u32x4_t qa[4], ah[2], al[2];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qa[ks] = ld16(&L.qs[arow][32 * ks + 8 * quad]);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const f32x4_t_ x0 = *reinterpret_cast<const f32x4_t_ *>(&L.A[arow][32 * ks + 8 * quad]);
+    const f32x4_t_ x1 = *reinterpret_cast<const f32x4_t_ *>(&L.A[arow][32 * ks + 8 * quad + 4]);
+    u32x2_t h0, l0, h1, l1;
+    split4(x0, h0, l0);
+    split4(x1, h1, l1);
+    ah[ks] = u32x4_t{h0[0], h0[1], h1[0], h1[1]};
+    al[ks] = u32x4_t{l0[0], l0[1], l1[0], l1[1]};
+  }
+  float eg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) eg[j] = expf(L.sG[16 * wave + 4 * quad + j]);
   f32x4_t_ o[8];
 #pragma unroll
   for (int vt = 0; vt < 8; ++vt) {
     f32x4_t_ a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int kq = 0; kq < kDK / 4; ++kq)
-      a1 = mfma16x4(bf16_to_f32(qs[trow][4 * kq + quad]), Sc[(4 * kq + quad) * kDV + 16 * vt + col],
-                    a1);
-#pragma unroll 8
-    for (int kq = 0; kq < kC / 4; ++kq)
-      a2 = mfma16x4(A[trow][4 * kq + quad], dl[(4 * kq + quad) * kDV + 16 * vt + col], a2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = 16 * wave + 4 * quad + j;
-      o[vt][j] = expf(sG[t]) * a1[j] + a2[j];
+    for (int ks = 0; ks < 4; ++ks) {
+      a1 = mfma16x32(qa[ks], bop(L.Sh, 32 * ks, vt), a1);
+      a1 = mfma16x32(qa[ks], bop(L.Sl, 32 * ks, vt), a1);
     }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4_t dh = bop(L.Dh, 32 * ks, vt), dlo = bop(L.Dl, 32 * ks, vt);
+      a2 = mfma16x32(ah[ks], dh, a2);
+      a2 = mfma16x32(ah[ks], dlo, a2);
+      a2 = mfma16x32(al[ks], dh, a2);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[vt][j] = eg[j] * a1[j] + a2[j];
   }
 #pragma unroll
   for (int vt = 0; vt < 8; ++vt)
@@ -512,7 +582,14 @@ extern "C" int wy_gdn_chunk_output(const void *q, const int64_t *qs, const void 
   if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
   if (!rows_ok(q, qs) || !rows_ok(k, ks) || os[2] != 1) return WY_E_LAYOUT;
   const int N = (token_num + kC - 1) / kC;
-  gdn_chunk_output_kernel<<<dim3(N, num_heads), 256, 0, static_cast<hipStream_t>(stream)>>>(
+  static bool lds_set = false;   // the attribute is per function, set once
+  if (!lds_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gdn_chunk_output_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kOutLds);
+    if (e != hipSuccess) return int(e);
+    lds_set = true;
+  }
+  gdn_chunk_output_kernel<<<dim3(N, num_heads), 256, kOutLds, static_cast<hipStream_t>(stream)>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0], ks[1],
       delta, g_cumsum, chunk_state, static_cast<bf16_t *>(out), os[0], os[1], token_num,
       num_heads);
