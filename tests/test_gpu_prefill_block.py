@@ -113,3 +113,22 @@ def test_block_gate_view_offsets(pkg, dev):
                                           bt)
         torch.cuda.synchronize()
         assert torch.equal(got, ref), off
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_equals_op_sequence_random_lengths(pkg, dev, seed):
+    """Random packed batches (2..24 sequences, lengths log-uniform in
+    [1, 4096]; most take the queue launch): the block and the op sequence
+    agree bit for bit, pages included."""
+    import random
+    rng = random.Random(1000 + seed)
+    lengths = [max(1, int(2 ** rng.uniform(0, 12))) for _ in range(rng.randint(2, 24))]
+    say(f"prefill block vs op sequence, random lengths seed={seed}: {lengths}")
+    q, k, v, gate, bt, kc, vc, packed = make(pkg, dev, lengths, 50 + seed)
+    inv = pkg.rope_inv_freq(64, 1e7, device=dev)
+    kc1, vc1, kc2, vc2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    ref = pkg.prefill_attention_packed(q, k, v, gate, inv, 64, packed, kc1, vc1, bt)
+    got = pkg.prefill_attention_block(q, k, v, gate, inv, 64, packed, kc2, vc2, bt)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
