@@ -141,6 +141,9 @@ __global__ __launch_bounds__(128) void gdn_gated_rmsnorm_kernel(
 // arithmetic as the decode step (conv4_silu), so prefill and decode agree bit
 // for bit on the same window.
 constexpr int kConvRun = 16;
+// Row counts from which the norm ops take the row-vectorised kernels (the
+// decode sizes keep one block per row, the same reduction either way).
+constexpr int kVecRows = 256;
 
 __global__ __launch_bounds__(256) void conv4_prefill_kernel(
     const bf16_t *__restrict__ x, int64_t x_t, int64_t x_c, const bf16_t *__restrict__ w,
@@ -168,6 +171,141 @@ __global__ __launch_bounds__(256) void conv4_prefill_kernel(
     const float a1 = t - 2 >= lo ? win[i + 1] : 0.f;
     const float a2 = t - 1 >= lo ? win[i + 2] : 0.f;
     out[int64_t(t) * o_t + c * o_c] = bf16_t(conv4_silu(a0, a1, a2, win[i + 3], w0, w1, w2, w3));
+  }
+}
+
+// ---- row-vectorised forms for many tokens (prefill) -----------------------
+//
+// A 16-lane group holds one 128-element row, lane l elements 8l .. 8l + 7
+// (one 16-byte load).  row_sum128 adds the 128 values with exactly the
+// pairings of sum128 (xor butterfly over element index within each 64-element
+// half, offsets 32, 16, 8, 4, 2, 1, then the two halves): offsets 32 / 16 / 8
+// are lanes l ^ 4 / 2 / 1, offsets 4 / 2 / 1 are registers j ^ 4 / 2 / 1, the
+// halves are lanes l ^ 8.  fp addition is commutative, so every partial sum
+// is bit-identical to sum128's and the results match the one-thread-per-
+// element kernels (and the fused decode block) bit for bit.
+__device__ __forceinline__ float row_sum128(float (&v)[8]) {
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] += __shfl_xor(v[j], o);
+  const float a0 = v[0] + v[4], a1 = v[1] + v[5], a2 = v[2] + v[6], a3 = v[3] + v[7];
+  const float b0 = a0 + a2, b1 = a1 + a3;
+  const float h = b0 + b1;
+  return h + __shfl_xor(h, 8);
+}
+
+__device__ __forceinline__ void unpack8(const u32x4_t x, float (&f)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = bf16_lo(x[e]);
+    f[2 * e + 1] = bf16_hi(x[e]);
+  }
+}
+
+// q/k norms and gates: 16 rows per 256-thread block, rows 2i (q) and 2i + 1
+// (k) of (token, head) pair 8 blockIdx + i.
+__global__ __launch_bounds__(256) void gdn_qk_norm_gates_vec_kernel(const QkNormArgs p,
+                                                                    int pairs) {
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int th = blockIdx.x * 8 + (grp >> 1);
+  const bool is_k = grp & 1;
+  if (th >= pairs) return;   // uniform over the 16-lane group
+  const int t = th / p.heads, h = th - t * p.heads;
+  const u32x4_t raw = ld16(is_k ? p.k + t * p.k_t + h * p.k_h + 8 * l
+                                : p.q + t * p.q_t + h * p.q_h + 8 * l);
+  float x[8], sq[8];
+  unpack8(raw, x);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sq[j] = x[j] * x[j];
+  const float r = rsqrtf(row_sum128(sq) + 1e-6f);
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = is_k ? (f32_to_bf16_bits(x[2 * e] * r) | (f32_to_bf16_bits(x[2 * e + 1] * r) << 16))
+                : (f32_to_bf16_bits((x[2 * e] * r) * p.q_scale) |
+                   (f32_to_bf16_bits((x[2 * e + 1] * r) * p.q_scale) << 16));
+  st16(is_k ? p.kn + t * p.kn_t + h * p.kn_h + 8 * l : p.qn + t * p.qn_t + h * p.qn_h + 8 * l, o);
+  if (!is_k && l == 0) {
+    float beta, g;
+    gdn_gates(bf16_to_f32(p.a[t * p.a_t + h * p.a_h]), bf16_to_f32(p.b[t * p.b_t + h * p.b_h]),
+              p.a_log[h], bf16_to_f32(p.dt_bias[h]), beta, g);
+    p.beta[th] = beta;
+    p.g[th] = g;
+  }
+}
+
+// Gated RMSNorm: 16 (token, head) rows per 256-thread block.
+__global__ __launch_bounds__(256) void gdn_gated_rmsnorm_vec_kernel(
+    const bf16_t *__restrict__ x, int64_t x_t, int64_t x_h, const bf16_t *__restrict__ z,
+    int64_t z_t, int64_t z_h, const float *__restrict__ w, bf16_t *__restrict__ out, int heads,
+    int rows) {
+  const int l = threadIdx.x & 15;
+  const int th = blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (th >= rows) return;
+  const int t = th / heads, h = th - t * heads;
+  float xv[8], zv[8], sq[8];
+  unpack8(ld16(x + t * x_t + h * x_h + 8 * l), xv);
+  unpack8(ld16(z + t * z_t + h * z_h + 8 * l), zv);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sq[j] = xv[j] * xv[j];
+  const float inv = rsqrtf(row_sum128(sq) / float(kDK) + 1e-6f);
+  const f32x4_t w0 = *reinterpret_cast<const f32x4_t *>(w + 8 * l);
+  const f32x4_t w1 = *reinterpret_cast<const f32x4_t *>(w + 8 * l + 4);
+  u32x4_t o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float wa = e < 2 ? w0[2 * e] : w1[2 * e - 4], wb = e < 2 ? w0[2 * e + 1] : w1[2 * e - 3];
+    o[e] = f32_to_bf16_bits(((xv[2 * e] * inv) * wa) * silu_gate(zv[2 * e])) |
+           (f32_to_bf16_bits(((xv[2 * e + 1] * inv) * wb) * silu_gate(zv[2 * e + 1])) << 16);
+  }
+  st16(out + int64_t(th) * kDK + 8 * l, o);
+}
+
+// conv4 prefill with 8 consecutive channels per thread (16-byte loads and
+// stores); per channel the same window and arithmetic as conv4_prefill_kernel.
+__global__ __launch_bounds__(256) void conv4_prefill_vec_kernel(
+    const bf16_t *__restrict__ x, int64_t x_t, const bf16_t *__restrict__ w, int64_t w_c,
+    int64_t w_k, bf16_t *__restrict__ out, int64_t o_t, const int32_t *__restrict__ seq_start,
+    int T, int C) {
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const int t0 = blockIdx.y * kConvRun;
+  if (c0 >= C) return;
+  float wt[4][8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wt[k][j] = bf16_to_f32(w[(c0 + j) * w_c + k * w_k]);
+  u32x4_t win[kConvRun + 3];   // win[j] = x[t0 - 3 + j, c0 .. c0 + 7] (zero outside [0, T))
+#pragma unroll
+  for (int j = 0; j < kConvRun + 3; ++j) {
+    const int t = t0 - 3 + j;
+    win[j] = (t >= 0 && t < T) ? ld16(x + int64_t(t) * x_t + c0) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < kConvRun; ++i) {
+    const int t = t0 + i;
+    if (t >= T) break;
+    const int lo = seq_start ? seq_start[t] : 0;
+    float a0[8], a1[8], a2[8], a3[8];
+    unpack8(win[i], a0);
+    unpack8(win[i + 1], a1);
+    unpack8(win[i + 2], a2);
+    unpack8(win[i + 3], a3);
+    u32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t y[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = 2 * e + u;
+        y[u] = conv4_silu(t - 3 >= lo ? a0[j] : 0.f, t - 2 >= lo ? a1[j] : 0.f,
+                          t - 1 >= lo ? a2[j] : 0.f, a3[j], wt[0][j], wt[1][j], wt[2][j],
+                          wt[3][j]);
+      }
+      o[e] = y[0] | (y[1] << 16);
+    }
+    st16(out + int64_t(t) * o_t + c0, o);
   }
 }
 
@@ -364,8 +502,15 @@ extern "C" int wy_gdn_qk_norm_gates(const void *q, const int64_t *q_strides, con
   p.g = g;
   p.heads = num_heads;
   p.q_scale = float(1.0 / sqrt(double(head_dim)));
-  gdn_qk_norm_gates_kernel<<<unsigned(tokens * num_heads), 256, 0,
-                             static_cast<hipStream_t>(stream)>>>(p);
+  const int pairs = tokens * num_heads;
+  const bool vec = p.q_d == 1 && p.k_d == 1 && ((p.q_t | p.q_h | p.k_t | p.k_h) & 7) == 0 &&
+                   wyh::aligned16(q) && wyh::aligned16(k) && wyh::aligned16(q_norm) &&
+                   wyh::aligned16(k_norm);
+  if (vec && pairs >= kVecRows)
+    gdn_qk_norm_gates_vec_kernel<<<unsigned((pairs + 7) / 8), 256, 0,
+                                   static_cast<hipStream_t>(stream)>>>(p, pairs);
+  else
+    gdn_qk_norm_gates_kernel<<<unsigned(pairs), 256, 0, static_cast<hipStream_t>(stream)>>>(p);
   return wyh::launch_status();
 }
 
@@ -377,11 +522,22 @@ extern "C" int wy_gdn_gated_rmsnorm(const void *x, const int64_t *x_strides, con
   if (head_dim != kDK) return WY_E_UNSUPPORTED;
   if (tokens == 0) return WY_OK;
   if (int64_t(tokens) * num_heads > 0x7fffffff) return WY_E_SHAPE;
-  gdn_gated_rmsnorm_kernel<<<unsigned(tokens * num_heads), 128, 0,
-                             static_cast<hipStream_t>(stream)>>>(
-      static_cast<const bf16_t *>(x), x_strides[0], x_strides[1], x_strides[2],
-      static_cast<const bf16_t *>(z), z_strides[0], z_strides[1], z_strides[2], weight,
-      static_cast<bf16_t *>(out), num_heads);
+  const int rows = tokens * num_heads;
+  const bool vec = x_strides[2] == 1 && z_strides[2] == 1 &&
+                   ((x_strides[0] | x_strides[1] | z_strides[0] | z_strides[1]) & 7) == 0 &&
+                   wyh::aligned16(x) && wyh::aligned16(z) && wyh::aligned16(weight) &&
+                   wyh::aligned16(out);
+  if (vec && rows >= kVecRows)
+    gdn_gated_rmsnorm_vec_kernel<<<unsigned((rows + 15) / 16), 256, 0,
+                                   static_cast<hipStream_t>(stream)>>>(
+        static_cast<const bf16_t *>(x), x_strides[0], x_strides[1],
+        static_cast<const bf16_t *>(z), z_strides[0], z_strides[1], weight,
+        static_cast<bf16_t *>(out), num_heads, rows);
+  else
+    gdn_gated_rmsnorm_kernel<<<unsigned(rows), 128, 0, static_cast<hipStream_t>(stream)>>>(
+        static_cast<const bf16_t *>(x), x_strides[0], x_strides[1], x_strides[2],
+        static_cast<const bf16_t *>(z), z_strides[0], z_strides[1], z_strides[2], weight,
+        static_cast<bf16_t *>(out), num_heads);
   return wyh::launch_status();
 }
 
@@ -433,7 +589,17 @@ extern "C" int wy_depthwise_causal_conv4_prefill(const void *x, const int64_t *x
   if (!x || !x_strides || !weight || !out || !out_strides) return WY_E_NULL;
   if (tokens < 0 || channels < 0) return WY_E_SHAPE;
   if (tokens == 0 || channels == 0) return WY_OK;
-  const dim3 grid(unsigned((channels + 255) / 256), unsigned((tokens + kConvRun - 1) / kConvRun));
+  const unsigned runs = unsigned((tokens + kConvRun - 1) / kConvRun);
+  if (x_strides[1] == 1 && out_strides[1] == 1 && channels % 8 == 0 &&
+      ((x_strides[0] | out_strides[0]) & 7) == 0 && wyh::aligned16(x) && wyh::aligned16(out)) {
+    conv4_prefill_vec_kernel<<<dim3(unsigned((channels / 8 + 255) / 256), runs), 256, 0,
+                               static_cast<hipStream_t>(stream)>>>(
+        static_cast<const bf16_t *>(x), x_strides[0], static_cast<const bf16_t *>(weight),
+        w_stride_c, w_stride_k, static_cast<bf16_t *>(out), out_strides[0], seq_start, tokens,
+        channels);
+    return wyh::launch_status();
+  }
+  const dim3 grid(unsigned((channels + 255) / 256), runs);
   conv4_prefill_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const bf16_t *>(x), x_strides[0], x_strides[1],
       static_cast<const bf16_t *>(weight), w_stride_c, w_stride_k, static_cast<bf16_t *>(out),

@@ -188,3 +188,31 @@ def test_conv4_prefill_vs_oracle_and_decode_chain(pkg, dev, lengths):
     pkg.conv_state_from_packed_prefill(state, xd, cu.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(state.cpu(), go.conv_state_from_packed(x, cu))
+
+
+def test_row_vectorised_norms_equal_per_row_kernels(pkg, dev):
+    """From 256 (token, head) rows the q/k norm + gates and the gated RMSNorm
+    take the 16-lanes-per-row kernels; token by token (16 rows) they take one
+    block per row.  Same pairing of the sum of squares either way: the results
+    agree bit for bit."""
+    say("gdn row-vectorised norms == per-row kernels")
+    T = 40
+    gen = torch.Generator().manual_seed(77)
+    qk = torch.randn(T, 2 * H * D, generator=gen).to(torch.bfloat16).to(dev)
+    a = torch.randn(T, H, generator=gen).to(torch.bfloat16).to(dev)
+    b = torch.randn(T, H, generator=gen).to(torch.bfloat16).to(dev)
+    a_log = torch.log(torch.rand(H, generator=gen) * 15 + 1).to(dev)
+    dt = torch.randn(H, generator=gen).to(torch.bfloat16).to(dev)
+    q, k = qk[:, :H * D].view(T, H, D), qk[:, H * D:].view(T, H, D)
+    assert T * H >= 256
+    big = pkg.gdn_qk_norm_gates(q, k, a, b, a_log, dt)
+    rows = [pkg.gdn_qk_norm_gates(q[t:t + 1], k[t:t + 1], a[t:t + 1], b[t:t + 1], a_log, dt)
+            for t in range(T)]
+    x = torch.randn(T, H, D, generator=gen).to(torch.bfloat16).to(dev)
+    w = (1 + 0.1 * torch.randn(D, generator=gen)).to(dev)
+    nbig = pkg.gdn_gated_rmsnorm(x, k, w)
+    nrows = [pkg.gdn_gated_rmsnorm(x[t:t + 1], k[t:t + 1], w) for t in range(T)]
+    torch.cuda.synchronize()
+    for i in range(4):
+        assert torch.equal(big[i], torch.cat([r[i] for r in rows])), i
+    assert torch.equal(nbig, torch.cat(nrows))
