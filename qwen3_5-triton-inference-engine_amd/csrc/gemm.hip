@@ -482,13 +482,15 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
   return wyh::launch_status();
 }
 
-// The 256 x 256 tile when its grid fills whole rounds of the 256 CUs (one
-// workgroup each) or runs for 4+ rounds, else 128 x 128 (two workgroups per
-// CU, four times the workgroups, so a partial last round costs less).
+// The 256 x 256 tile from 384 of its tiles (a round and a half of the 256 CUs,
+// one workgroup each: the 4096-token in_proj / gate_up shapes 115 -> 102 and
+// 73 -> 68 us; at 320 tiles, [4096, 5120], it lost 54 -> 65 us), else 128 x
+// 128 (two workgroups per CU, four times the workgroups, so a partial last
+// round costs less), or 128 x 64 below two 128 x 128 tiles per CU.
 int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                  int64_t ys0, int M, int N, int K, hipStream_t st) {
   const int64_t big = int64_t((M + 255) / 256) * ((N + 255) / 256);
-  if (big >= 256 && (big % 256 == 0 || big >= 1024))
+  if (big >= 384)
     return launch_tiled_cfg<256, 256, 2, 4>(x, xs0, w, ws0, y, ys0, M, N, K, st);
   // fewer 128 x 128 tiles than two per CU (e.g. k_proj and o_proj at 4096
   // tokens): 128 x 64 tiles put twice as many workgroups on the chip

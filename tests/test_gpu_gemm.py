@@ -38,8 +38,9 @@ SHAPES = [
     (65, 2048, 1024), (300, 512, 1024), (1000, 1024, 2048), (129, 100, 256), (4096, 2048, 1024),
     # fewer 128 x 128 tiles than CUs take 128 x 64 tiles (k_proj at 4096 tokens; ragged N)
     (4096, 512, 1024), (2000, 900, 256),
-    # grids of >= 256 256x256 tiles take the 8-wave 256 x 256 kernel; ragged edges
+    # grids of >= 384 256x256 tiles take the 8-wave 256 x 256 kernel; ragged edges
     (8292, 8132, 128), (8192, 8192, 128), (8192 + 255, 8192 + 129, 384),
+    (4096, 8224, 256),  # the GDN in_proj width at 4096 tokens (528 tiles, last column tile 32 wide)
 ]
 
 
