@@ -568,6 +568,18 @@ int wy_embedding_gather(const void *input_ids, int ids_is_int64, const void *wei
 int wy_residual_add(const void *x, const void *residual, void *out, int64_t n, void *stream);
 
 /*
+ * Residual add fused with the following RMSNorm: sum = bf16(h + x) and
+ * out = bf16(sum * rsqrt(mean(sum^2) + eps) * (1 + weight)), fp32 math, over
+ * [rows, d_model] contiguous bf16 rows (16-byte aligned, d_model % 256 == 0).
+ * Equals wy_residual_add -> wy_qwen_rmsnorm bit for bit.  sum and out must not
+ * alias h, x or each other.  No single counterpart in the reference: it fuses
+ * the residual_add and qwen_rmsnorm calls of its decoder layer
+ * (engine/runner.py's layer loop) into one launch.
+ */
+int wy_add_rmsnorm(const void *h, const void *x, const void *weight, void *sum, void *out,
+                   int rows, int d_model, float eps, void *stream);
+
+/*
  * SwiGLU: out[m, n] = bf16(up * gate * sigmoid(gate)), fp32 math; gate, up
  * [rows, cols] bf16 (element strides), out [rows, cols] contiguous.
  * Replaces wy_lib::swiglu (triton_kernels/swiglu.py:72-111, kernel :22-60).

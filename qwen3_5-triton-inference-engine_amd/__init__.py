@@ -72,7 +72,7 @@ from .gdn_recurrent_prefill import (
 from .gqa_attention_varlen_causal import build_cu_seqlens, gqa_attention_varlen_causal
 from .paging import PagePool, SequencePages, allocate_block_table
 from .partial_rope import partial_rope, rope_inv_freq
-from .qwen_rmsnorm import call_qwen_rmsnorm_triton, qwen_rmsnorm
+from .qwen_rmsnorm import add_rmsnorm, call_qwen_rmsnorm_triton, qwen_rmsnorm
 from .residual_add import call_residual_add_triton, residual_add
 from .swiglu import call_swiglu_triton, swiglu
 from .vocab_argmax import call_lm_head_argmax_triton, lm_head_argmax

@@ -79,6 +79,7 @@ _SIGNATURES = {
     "wy_conv_state_from_packed_prefill": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _vp],
     "wy_embedding_gather": [_vp, _i, _vp, _i64, _i64, _vp, _i64, _i, _i, _vp],
     "wy_residual_add": [_vp, _vp, _vp, _i64, _vp],
+    "wy_add_rmsnorm": [_vp, _vp, _vp, _vp, _vp, _i, _i, _f, _vp],
     "wy_swiglu": [_vp, _c_i64p, _vp, _c_i64p, _vp, _i, _i, _vp],
     "wy_lm_head_argmax": [_vp, _i64, _vp, _i64, _vp, _i, _i, _i, _vp, _i64, _vp],
     "wy_gemm_2d_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _f, _vp, _i64, _vp, _i64, _vp, _i64, _i,

@@ -38,6 +38,44 @@ __global__ __launch_bounds__(256) void qwen_rmsnorm_kernel(
   }
 }
 
+// Residual add fused with the RMSNorm that follows it in a decoder layer:
+// sum = bf16(h + x) (the residual add, rounded as a separate add would round
+// it), normed = RMSNorm(sum).  The sum of squares runs over the rounded sum in
+// qwen_rmsnorm_kernel's order, so both outputs equal the two separate ops bit
+// for bit.  Rows contiguous, [rows, D].
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
+    const bf16_t *__restrict__ h, const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
+    bf16_t *__restrict__ sum, bf16_t *__restrict__ out, int rows, int D, float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 5);
+  if (row >= rows) return;  // uniform over the row's 32 lanes
+  const int l = threadIdx.x & 31;
+  const int64_t base = int64_t(row) * D;
+  const int nk = D / 256;
+  float ss = 0.f;
+  for (int k = 0; k < nk; ++k) {
+    const int c = (32 * k + l) * 8;
+    const u32x4_t a = ld16(h + base + c), b = ld16(x + base + c);
+    u32x4_t s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      s[e] = pack_bf16x2(bf16_lo(a[e]) + bf16_lo(b[e]), bf16_hi(a[e]) + bf16_hi(b[e]));
+    st16(sum + base + c, s);
+    ss = rms_acc8(s, ss);
+  }
+  const float rs = rms_rsigma(ss, D, eps);
+  for (int k = 0; k < nk; ++k) {
+    const int c = (32 * k + l) * 8;
+    const u32x4_t sw = ld16(sum + base + c);  // this lane's own store above
+    const u32x4_t ww = ld16(w + c);
+    u32x4_t y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      y[e] = pack_bf16x2(rms_apply(bf16_lo(sw[e]), rs, bf16_lo(ww[e])),
+                         rms_apply(bf16_hi(sw[e]), rs, bf16_hi(ww[e])));
+    st16(out + base + c, y);
+  }
+}
+
 }  // namespace
 
 extern "C" int wy_qwen_rmsnorm(const void *x, const int64_t *xs, const void *weight, void *out,
@@ -54,5 +92,22 @@ extern "C" int wy_qwen_rmsnorm(const void *x, const int64_t *xs, const void *wei
   qwen_rmsnorm_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const bf16_t *>(x), xs[0], xs[1], static_cast<const bf16_t *>(weight),
       static_cast<bf16_t *>(out), os[0], os[1], rows, d_model, eps);
+  return wyh::launch_status();
+}
+
+extern "C" int wy_add_rmsnorm(const void *h, const void *x, const void *weight, void *sum,
+                              void *out, int rows, int d_model, float eps, void *stream) {
+  if (!h || !x || !weight || !sum || !out) return WY_E_NULL;
+  if (rows < 0 || d_model <= 0) return WY_E_SHAPE;
+  if (d_model % 256 != 0) return WY_E_UNSUPPORTED;
+  if (!wyh::aligned16(h) || !wyh::aligned16(x) || !wyh::aligned16(weight) ||
+      !wyh::aligned16(sum) || !wyh::aligned16(out))
+    return WY_E_LAYOUT;
+  if (rows == 0) return WY_OK;
+  const dim3 grid(unsigned((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  add_rmsnorm_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bf16_t *>(h), static_cast<const bf16_t *>(x),
+      static_cast<const bf16_t *>(weight), static_cast<bf16_t *>(sum), static_cast<bf16_t *>(out),
+      rows, d_model, eps);
   return wyh::launch_status();
 }

@@ -48,7 +48,7 @@ from .embedding_gather import embedding_gather
 from .gemm_2d import gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
 from .gdn_mixer import gdn_decode_block, gdn_decode_ops
 from .partial_rope import rope_inv_freq
-from .qwen_rmsnorm import qwen_rmsnorm
+from .qwen_rmsnorm import add_rmsnorm, qwen_rmsnorm
 from .residual_add import residual_add
 from .swiglu import swiglu
 from .vocab_argmax import lm_head_argmax
@@ -243,19 +243,22 @@ class DecodeModel:
         """Mixer blocks, separate residual add / RMSNorm / SwiGLU launches."""
         cfg = self.cfg
         x = embedding_gather(token_ids, self.embed)
+        h = None  # the previous sub-block's output, not yet added to x
         for i, w in enumerate(self.layers):
-            h = qwen_rmsnorm(x, w.input_layernorm, cfg.eps)
-            fused = gemm_2d(h, w.in_proj)
+            if h is None:
+                normed = qwen_rmsnorm(x, w.input_layernorm, cfg.eps)
+            else:
+                x, normed = add_rmsnorm(h, x, w.input_layernorm, cfg.eps)
+            fused = gemm_2d(normed, w.in_proj)
             if cfg.is_attention(i):
                 h = self._attention_from(fused, w, self.attn_index[i])
             else:
                 h = self._gdn_from(fused, w, i)
-            x = residual_add(h, x)
-            h = qwen_rmsnorm(x, w.post_attention_layernorm, cfg.eps)
-            gate_up = gemm_2d(h, w.gate_up)
+            x, normed = add_rmsnorm(h, x, w.post_attention_layernorm, cfg.eps)
+            gate_up = gemm_2d(normed, w.gate_up)
             h = swiglu(gate_up[:, :cfg.intermediate], gate_up[:, cfg.intermediate:])
-            x = residual_add(gemm_2d(h, w.down_proj), x)
-        return qwen_rmsnorm(x, self.final_norm, cfg.eps)
+            h = gemm_2d(h, w.down_proj)
+        return add_rmsnorm(h, x, self.final_norm, cfg.eps)[1]
 
     def _decode_step_ops(self, token_ids: torch.Tensor) -> torch.Tensor:
         """The reference runner's op sequence, one op per launch."""
@@ -289,23 +292,25 @@ class DecodeModel:
         packed = build_packed_batch(list(lengths), device=self.device)
         T = packed.total_tokens
         x = embedding_gather(token_ids, self.embed)
+        h = None  # the previous sub-block's output, not yet added to x
         for i, w in enumerate(self.layers):
-            residual = x
-            h = qwen_rmsnorm(x, w.input_layernorm, cfg.eps)
-            fused = gemm_2d(h, w.in_proj)
+            if h is None:
+                normed = qwen_rmsnorm(x, w.input_layernorm, cfg.eps)
+            else:
+                x, normed = add_rmsnorm(h, x, w.input_layernorm, cfg.eps)
+            fused = gemm_2d(normed, w.in_proj)
             if cfg.is_attention(i):
                 h = self._attention_prefill(fused, w, self.attn_index[i], packed)
             else:
                 h = self._gdn_prefill(fused, w, i, packed)
-            x = residual_add(h, residual)
-            residual = x
-            h = qwen_rmsnorm(x, w.post_attention_layernorm, cfg.eps)
-            gate_up = gemm_2d(h, w.gate_up)
+            x, normed = add_rmsnorm(h, x, w.post_attention_layernorm, cfg.eps)
+            gate_up = gemm_2d(normed, w.gate_up)
             h = gemm_2d(swiglu(gate_up[:, :cfg.intermediate], gate_up[:, cfg.intermediate:]),
                         w.down_proj)
-            x = residual_add(h, residual)
+        # only each prompt's last row reaches the LM head
         last = packed.cu_seqlens[1:].long() - 1
-        hidden = qwen_rmsnorm(x[last].contiguous(), self.final_norm, cfg.eps)
+        hidden = add_rmsnorm(h[last].contiguous(), x[last].contiguous(), self.final_norm,
+                             cfg.eps)[1]
         self.attn.pos.copy_(torch.tensor(lengths, dtype=torch.int64, device=self.device))
         assert T == token_ids.shape[0]
         return lm_head_argmax(hidden, self.embed, False)

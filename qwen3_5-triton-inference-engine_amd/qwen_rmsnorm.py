@@ -46,6 +46,31 @@ def _qwen_rmsnorm_fake(x, weight, eps=1e-6) -> torch.Tensor:
     return torch.empty_like(x)
 
 
+@torch.library.custom_op("wy_lib::add_rmsnorm", mutates_args=(), device_types="cuda")
+def add_rmsnorm(h: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(s, qwen_rmsnorm(s))`` with ``s = bf16(h + x)``: a decoder layer's
+    residual add and the RMSNorm after it in one launch, equal bit for bit to
+    ``residual_add`` followed by ``qwen_rmsnorm``.  h, x contiguous
+    ``[..., D]`` bf16."""
+    assert h.shape == x.shape
+    assert h.dtype == torch.bfloat16 and x.dtype == torch.bfloat16
+    assert weight.dtype == torch.bfloat16 and weight.is_contiguous()
+    assert h.is_contiguous() and x.is_contiguous()
+    d_model = x.shape[-1]
+    assert d_model % 256 == 0 and weight.shape == (d_model,)
+    s = torch.empty_like(x)
+    out = torch.empty_like(x)
+    _lib.call("wy_add_rmsnorm", _lib.ptr(h), _lib.ptr(x), _lib.ptr(weight), _lib.ptr(s),
+              _lib.ptr(out), x.numel() // d_model, d_model, float(eps), _lib.stream(x.device))
+    return s, out
+
+
+@add_rmsnorm.register_fake
+def _add_rmsnorm_fake(h, x, weight, eps=1e-6):
+    return torch.empty_like(x), torch.empty_like(x)
+
+
 def call_qwen_rmsnorm_triton(x: torch.Tensor, weight: torch.Tensor,
                              eps: float = 1e-6) -> torch.Tensor:
     return qwen_rmsnorm(x, weight, eps)

@@ -38,6 +38,27 @@ def test_residual_add_exact(pkg, dev, n):
     assert torch.equal(out.cpu(), mo.residual_add(x, r))
 
 
+@pytest.mark.parametrize("rows,d", [(32, 1024), (1, 1024), (4099, 1024), (13, 256)])
+def test_add_rmsnorm_equals_add_then_norm(pkg, dev, rows, d):
+    """The fused residual add + RMSNorm equals residual_add -> qwen_rmsnorm bit
+    for bit (both outputs), and the oracle's add + norm within bf16 rounding."""
+    from oracle import attention_oracle as ao
+
+    say(f"add_rmsnorm rows={rows} d={d}")
+    gen = torch.Generator().manual_seed(rows + d)
+    h = (torch.randn(rows, d, generator=gen) * 3).to(torch.bfloat16)
+    x = torch.randn(rows, d, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(d, generator=gen) * 0.1).to(torch.bfloat16)
+    hd, xd, wd = h.to(dev), x.to(dev), w.to(dev)
+    s, normed = pkg.add_rmsnorm(hd, xd, wd, 1e-6)
+    s_ref = pkg.residual_add(hd, xd)
+    assert torch.equal(s, s_ref)
+    assert torch.equal(normed, pkg.qwen_rmsnorm(s_ref, wd, 1e-6))
+    assert torch.equal(s.cpu(), mo.residual_add(h, x))
+    ref = ao.qwen_rmsnorm(mo.residual_add(h, x).float(), w, 1e-6)
+    torch.testing.assert_close(normed.float().cpu(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("M", [1, 32])
 def test_swiglu_vs_oracle(pkg, dev, M):
     say(f"swiglu M={M}")
