@@ -570,11 +570,12 @@ int wy_residual_add(const void *x, const void *residual, void *out, int64_t n, v
 /*
  * Residual add fused with the following RMSNorm: sum = bf16(h + x) and
  * out = bf16(sum * rsqrt(mean(sum^2) + eps) * (1 + weight)), fp32 math, over
- * [rows, d_model] contiguous bf16 rows (16-byte aligned, d_model % 256 == 0).
- * Equals wy_residual_add -> wy_qwen_rmsnorm bit for bit.  sum and out must not
- * alias h, x or each other.  No single counterpart in the reference: it fuses
- * the residual_add and qwen_rmsnorm calls of its decoder layer
- * (engine/runner.py's layer loop) into one launch.
+ * [rows, d_model] contiguous bf16 rows (16-byte aligned, d_model a multiple
+ * of 256 up to 1024).  Equals wy_residual_add -> wy_qwen_rmsnorm bit for bit.
+ * sum and out must not alias h, x or each other.  No single counterpart in
+ * the reference: it fuses the residual_add -> qwen_rmsnorm pairs of its
+ * decoder layer loop (engine/runner.py:555-558, :566-571; prefill :650-663)
+ * into one launch.
  */
 int wy_add_rmsnorm(const void *h, const void *x, const void *weight, void *sum, void *out,
                    int rows, int d_model, float eps, void *stream);
@@ -635,6 +636,25 @@ int wy_gemm_2d_rmsnorm(const void *x, int64_t x_stride0, const void *residual,
 int wy_gemm_2d_swiglu(const void *gate_up, int64_t gate_up_stride0, int64_t up_offset,
                       const void *w, int64_t w_stride0, void *y, int64_t y_stride0, int M, int N,
                       int K, void *workspace, int64_t workspace_bytes, void *stream);
+
+/*
+ * The gate/up projection with SwiGLU in the epilogue: w [2N, K] holds the gate
+ * rows [0, N) and the up rows [N, 2N); y [M, N] = bf16(up * gate *
+ * sigmoid(gate)) with gate = bf16(x @ w[0:N]^T), up = bf16(x @ w[N:2N]^T).
+ * Equals wy_gemm_2d (x, w) -> wy_swiglu bit for bit when 2N >= 4096 (the
+ * same workgroup plan; smaller N differ by fp32 summation order only).
+ * M <= 64 (else WY_E_UNSUPPORTED), K % 128 == 0, rows 16-byte aligned;
+ * workspace as in wy_gemm_2d, sized by
+ * wy_gemm_2d_gate_up_swiglu_workspace_bytes.  No counterpart in the
+ * reference: it fuses the gate_up gemm_2d and swiglu of its MLP
+ * (engine/runner.py:560-565) into one launch.
+ */
+int wy_gemm_2d_gate_up_swiglu(const void *x, int64_t x_stride0, const void *w,
+                              int64_t w_stride0, void *y, int64_t y_stride0, int M, int N, int K,
+                              void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes wy_gemm_2d_gate_up_swiglu needs for split K (0: none). */
+int64_t wy_gemm_2d_gate_up_swiglu_workspace_bytes(int M, int N, int K);
 
 #ifdef __cplusplus
 }

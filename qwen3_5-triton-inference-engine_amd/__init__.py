@@ -23,7 +23,8 @@ from .attention_gate_pack import attention_gate_pack
 from .cache import AttnCaches, allocate_attn_caches
 from .decoder import DecodeModel, DecoderConfig, GraphedDecoder, random_weights
 from .embedding_gather import call_embedding_gather_triton, embedding_gather
-from .gemm_2d import call_gemm_2d_triton, gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
+from .gemm_2d import (call_gemm_2d_triton, gate_up_swiglu, gemm_2d, rmsnorm_gemm_2d,
+                      swiglu_gemm_2d)
 from .gqa_attention_decode_paged import (
     MAX_SPLITS,
     MIN_PAGES_PER_SPLIT,

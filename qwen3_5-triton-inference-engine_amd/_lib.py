@@ -85,10 +85,12 @@ _SIGNATURES = {
     "wy_gemm_2d_rmsnorm": [_vp, _i64, _vp, _i64, _vp, _f, _vp, _i64, _vp, _i64, _vp, _i64, _i,
                            _i, _i, _vp, _i64, _vp],
     "wy_gemm_2d_swiglu": [_vp, _i64, _i64, _vp, _i64, _vp, _i64, _i, _i, _i, _vp, _i64, _vp],
+    "wy_gemm_2d_gate_up_swiglu": [_vp, _i64, _vp, _i64, _vp, _i64, _i, _i, _i, _vp, _i64, _vp],
 }
 
 # entry points returning a size (int64) rather than a status
 _SIZE_QUERIES = ("wy_varlen_causal_prefill_workspace_bytes", "wy_gemm_2d_workspace_bytes",
+                 "wy_gemm_2d_gate_up_swiglu_workspace_bytes",
                  "wy_lm_head_argmax_workspace_bytes", "wy_paged_decode_step_noalloc_max_rows",
                  "wy_page_stream_read_waves")
 
@@ -117,6 +119,7 @@ def load() -> ctypes.CDLL:
     lib.wy_build_info.argtypes = []
     lib.wy_build_info.restype = ctypes.c_char_p
     for fn in (lib.wy_varlen_causal_prefill_workspace_bytes, lib.wy_gemm_2d_workspace_bytes,
+               lib.wy_gemm_2d_gate_up_swiglu_workspace_bytes,
                lib.wy_lm_head_argmax_workspace_bytes):
         fn.argtypes = [_i, _i, _i]
         fn.restype = ctypes.c_int64

@@ -76,7 +76,84 @@ __device__ __forceinline__ u32x4_t swiglu_bf16x8(u32x4_t g, u32x4_t u) {
   return o;
 }
 
-template <int kNW, int kMT, int kNT, int kPro = 0>
+// Gate/up-pair epilogue (kEpi 1): sums the waves' tiles of the gate and the
+// up column tile in wave order, as the plain epilogue does, and stores
+// bf16(swiglu(bf16(gate), bf16(up))).  With K split across workgroups the
+// fp32 partials go to part[split][M][2N] (gate at column c, up at N + c)
+// and the workgroup that completes cnt[blockIdx.x] sums them in split order.
+template <int kNW, int kMT>
+__device__ __forceinline__ void gate_up_epilogue(const f32x4v_t (&red)[kNW][kMT * 2][64],
+                                 bf16_t *__restrict__ y, int64_t ys0, int M, int N, int n0,
+                                 float *__restrict__ part, int32_t *__restrict__ cnt,
+                                 int &last_ws) {
+  const int n_split = int(gridDim.y);
+  const int64_t pw = 2 * int64_t(N), part_stride = int64_t(M) * pw;
+  for (int e = threadIdx.x; e < M * 16; e += 64 * kNW) {
+    const int row = e >> 4, col = e & 15;
+    const int mt = row >> 4, src = col + 16 * ((row & 15) >> 2), i = row & 3;
+    float sg = 0.f, su = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kNW; ++wv) {
+      sg += red[wv][mt * 2][src][i];
+      su += red[wv][mt * 2 + 1][src][i];
+    }
+    if (n0 + col < N) {
+      if (n_split == 1) {
+        y[int64_t(row) * ys0 + n0 + col] = bf16_t(f32_to_bf16_bits(
+            swiglu_f(bf16_round(sg), bf16_round(su))));
+      } else {
+        float *pp = part + blockIdx.y * part_stride + int64_t(row) * pw + n0 + col;
+        __hip_atomic_store(pp, sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + N, su, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (n_split == 1) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int done = __hip_atomic_fetch_add(cnt + blockIdx.x, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    const int last = done == n_split - 1;
+    if (last) __hip_atomic_store(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_ws = last;
+  }
+  __syncthreads();
+  if (!last_ws) return;
+  for (int e = threadIdx.x; e < M * 16; e += 64 * kNW) {
+    const int row = e >> 4, col = e & 15;
+    if (n0 + col >= N) continue;
+    const float *pp = part + int64_t(row) * pw + n0 + col;
+    float g[kMaxSplit], u[kMaxSplit];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp) {
+      const float *q = pp + (sp < n_split ? sp : 0) * part_stride;
+      g[sp] = __hip_atomic_load(const_cast<float *>(q), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+      u[sp] = __hip_atomic_load(const_cast<float *>(q + N), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+    }
+    float sg = 0.f, su = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp) {
+      sg += sp < n_split ? g[sp] : 0.f;
+      su += sp < n_split ? u[sp] : 0.f;
+    }
+    y[int64_t(row) * ys0 + n0 + col] =
+        bf16_t(f32_to_bf16_bits(swiglu_f(bf16_round(sg), bf16_round(su))));
+  }
+}
+
+// Epilogues of the skinny kernel (kEpi):
+//   0: y = bf16(acc);
+//   1 (kNT == 2, gate/up pairs): the weight holds 2N rows, gate rows [0, N)
+//      and up rows [N, 2N); a workgroup's column tile 0 covers gate rows
+//      n0..n0+15 and tile 1 the up rows N+n0..; y[:, n0 + c] =
+//      bf16(swiglu(bf16(gate acc), bf16(up acc))), the [M, N] SwiGLU output
+//      of the [M, 2N] projection, equal to the plain GEMM followed by
+//      swiglu_kernel whenever the plain GEMM's plan matches (same waves and
+//      K split; 2N >= 4096).
+template <int kNW, int kMT, int kNT, int kPro = 0, int kEpi = 0>
 __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, float *__restrict__ part,
@@ -94,7 +171,8 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
   __shared__ int last_ws;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * 16 * kNT;
+  static_assert(kEpi == 0 || kNT == 2, "gate/up pairs need two column tiles");
+  const int n0 = blockIdx.x * 16 * (kEpi == 1 ? 1 : kNT);
   const int n_split = int(gridDim.y);
   const int ks = K / n_split;  // a multiple of 32 * kNW (host)
   const int kc = ks / kNW;
@@ -103,7 +181,10 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
   const bf16_t *wp[kNT];
 #pragma unroll
   for (int nt = 0; nt < kNT; ++nt)
-    wp[nt] = w + int64_t(min(n0 + 16 * nt + (lane & 15), N - 1)) * ws0 + kb + 8 * g;
+    wp[nt] = w +
+             (kEpi == 1 ? int64_t(min(n0 + (lane & 15), N - 1)) + int64_t(nt) * N
+                        : int64_t(min(n0 + 16 * nt + (lane & 15), N - 1))) * ws0 +
+             kb + 8 * g;
   const bf16_t *xp[kMT];
   bool xok[kMT];
 #pragma unroll
@@ -199,6 +280,10 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) red[wave][mt * kNT + nt][lane] = acc[mt][nt];
   __syncthreads();
+  if constexpr (kEpi == 1) {
+    gate_up_epilogue<kNW, kMT>(red, y, ys0, M, N, n0, part, cnt, last_ws);
+    return;
+  }
   const int64_t part_stride = int64_t(M) * N;
   for (int e = threadIdx.x; e < M * 16 * kNT; e += 64 * kNW) {
     const int row = e / (16 * kNT), cc = e - row * (16 * kNT);
@@ -512,20 +597,21 @@ struct SkinnyArgs {
   ProArgs pro;
 };
 
-template <int kNW, int kMT, int kNT, int kPro>
+template <int kNW, int kMT, int kNT, int kPro, int kEpi = 0>
 void launch_skinny(const SkinnyArgs &a, hipStream_t st) {
-  const dim3 grid(unsigned((a.N + 16 * kNT - 1) / (16 * kNT)), unsigned(a.split));
-  gemm_skinny_kernel<kNW, kMT, kNT, kPro><<<grid, 64 * kNW, 0, st>>>(
+  const int cols = 16 * (kEpi == 1 ? 1 : kNT);
+  const dim3 grid(unsigned((a.N + cols - 1) / cols), unsigned(a.split));
+  gemm_skinny_kernel<kNW, kMT, kNT, kPro, kEpi><<<grid, 64 * kNW, 0, st>>>(
       a.x, a.xs0, a.w, a.ws0, a.y, a.ys0, a.M, a.N, a.K, a.part, a.cnt, a.pro);
 }
 
-template <int kNW, int kNT, int kPro>
+template <int kNW, int kNT, int kPro, int kEpi = 0>
 void launch_skinny_m(const SkinnyArgs &a, hipStream_t st) {
   switch ((a.M + 15) / 16) {
-    case 1: launch_skinny<kNW, 1, kNT, kPro>(a, st); break;
-    case 2: launch_skinny<kNW, 2, kNT, kPro>(a, st); break;
-    case 3: launch_skinny<kNW, 3, kNT, kPro>(a, st); break;
-    default: launch_skinny<kNW, 4, kNT, kPro>(a, st); break;
+    case 1: launch_skinny<kNW, 1, kNT, kPro, kEpi>(a, st); break;
+    case 2: launch_skinny<kNW, 2, kNT, kPro, kEpi>(a, st); break;
+    case 3: launch_skinny<kNW, 3, kNT, kPro, kEpi>(a, st); break;
+    default: launch_skinny<kNW, 4, kNT, kPro, kEpi>(a, st); break;
   }
 }
 
@@ -565,12 +651,14 @@ int skinny_waves(int groups, int ks) {
   return nw;
 }
 
-SkinnyPlan skinny_plan(int N, int K) {
+SkinnyPlan skinny_plan(int N, int K, bool gate_up_pairs = false) {
   SkinnyPlan p;
   // 32 columns per workgroup when N is large (each x load then feeds two
-  // column tiles, halving the x bytes per column), else 16.
-  p.nt = N >= 4096 ? 2 : 1;
-  p.blocks = (N + 16 * p.nt - 1) / (16 * p.nt);
+  // column tiles, halving the x bytes per column), else 16.  Gate/up pairs
+  // (N output columns from 2N weight rows) always take two tiles, one of each
+  // half: the same workgroups as the plain plan of 2N columns when 2N >= 4096.
+  p.nt = gate_up_pairs || N >= 4096 ? 2 : 1;
+  p.blocks = gate_up_pairs ? (N + 15) / 16 : (N + 16 * p.nt - 1) / (16 * p.nt);
   // Split K across workgroups until the grid covers the CUs once, keeping
   // at least WY_GEMM_SPLIT_MIN_K of K per workgroup.
   p.split = 1;
@@ -696,4 +784,45 @@ extern "C" int wy_gemm_2d_swiglu(const void *gate_up, int64_t gate_up_stride0, i
                static_cast<const bf16_t *>(w), w_stride0, static_cast<bf16_t *>(y), y_stride0,
                M, N, K, 1, nullptr, nullptr, pro};
   return run_skinny(a, 2, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t wy_gemm_2d_gate_up_swiglu_workspace_bytes(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128 || M > kSkinnyMaxM) return 0;
+  const SkinnyPlan p = skinny_plan(N, K, true);
+  if (p.split == 1 || p.blocks > kSplitCounters) return 0;
+  return kSplitPartOffset + int64_t(p.split) * M * 2 * N * 4;
+}
+
+extern "C" int wy_gemm_2d_gate_up_swiglu(const void *x, int64_t x_stride0, const void *w,
+                                         int64_t w_stride0, void *y, int64_t y_stride0, int M,
+                                         int N, int K, void *workspace, int64_t workspace_bytes,
+                                         void *stream) {
+  if (!x || !w || !y) return WY_E_NULL;
+  if (M < 0 || N < 0 || K <= 0 || K % 128) return WY_E_SHAPE;
+  if (M > kSkinnyMaxM) return WY_E_UNSUPPORTED;
+  if (x_stride0 % 8 || w_stride0 % 8 || x_stride0 < K || w_stride0 < K || y_stride0 < N ||
+      !wyh::aligned16(x) || !wyh::aligned16(w) || (reinterpret_cast<uintptr_t>(y) & 1u))
+    return WY_E_LAYOUT;
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 3u))
+    return WY_E_LAYOUT;
+  if (M == 0 || N == 0) return WY_OK;
+  SkinnyArgs a{static_cast<const bf16_t *>(x), x_stride0, static_cast<const bf16_t *>(w),
+               w_stride0, static_cast<bf16_t *>(y), y_stride0, M, N, K, 1, nullptr, nullptr,
+               ProArgs{}};
+  SkinnyPlan p = skinny_plan(N, K, true);
+  const int64_t need = wy_gemm_2d_gate_up_swiglu_workspace_bytes(M, N, K);
+  if (p.split > 1 && need > 0 && workspace_bytes >= need) {
+    a.split = p.split;
+    a.cnt = static_cast<int32_t *>(workspace);
+    a.part = reinterpret_cast<float *>(static_cast<char *>(workspace) + kSplitPartOffset);
+  } else if (p.split > 1) {
+    p.split = 1;
+    p.nw = skinny_waves(p.blocks, K);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (p.nw == 4) launch_skinny_m<4, 2, 0, 1>(a, st);
+  else if (p.nw == 8) launch_skinny_m<8, 2, 0, 1>(a, st);
+  else launch_skinny_m<16, 2, 0, 1>(a, st);
+  return wyh::launch_status();
 }

@@ -45,7 +45,7 @@ from .gdn_recurrent_prefill import (
 GDN_CHUNKED_PREFILL_MIN_TOKENS = 2048
 from .cache import allocate_attn_caches
 from .embedding_gather import embedding_gather
-from .gemm_2d import gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
+from .gemm_2d import gate_up_swiglu, gemm_2d, rmsnorm_gemm_2d, swiglu_gemm_2d
 from .gdn_mixer import gdn_decode_block, gdn_decode_ops
 from .partial_rope import rope_inv_freq
 from .qwen_rmsnorm import add_rmsnorm, qwen_rmsnorm
@@ -240,7 +240,9 @@ class DecodeModel:
         return gemm_2d(normed, w.out_proj)
 
     def _decode_step_blocks(self, token_ids: torch.Tensor) -> torch.Tensor:
-        """Mixer blocks, separate residual add / RMSNorm / SwiGLU launches."""
+        """Mixer blocks with plain GEMMs: the residual add and the RMSNorm after
+        it share a launch, and SwiGLU runs in the gate/up GEMM's epilogue
+        (all bit-identical to the op sequence)."""
         cfg = self.cfg
         x = embedding_gather(token_ids, self.embed)
         h = None  # the previous sub-block's output, not yet added to x
@@ -255,9 +257,7 @@ class DecodeModel:
             else:
                 h = self._gdn_from(fused, w, i)
             x, normed = add_rmsnorm(h, x, w.post_attention_layernorm, cfg.eps)
-            gate_up = gemm_2d(normed, w.gate_up)
-            h = swiglu(gate_up[:, :cfg.intermediate], gate_up[:, cfg.intermediate:])
-            h = gemm_2d(h, w.down_proj)
+            h = gemm_2d(gate_up_swiglu(normed, w.gate_up), w.down_proj)
         return add_rmsnorm(h, x, self.final_norm, cfg.eps)[1]
 
     def _decode_step_ops(self, token_ids: torch.Tensor) -> torch.Tensor:

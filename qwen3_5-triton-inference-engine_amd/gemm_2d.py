@@ -117,3 +117,34 @@ def swiglu_gemm_2d(gate_up: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 @swiglu_gemm_2d.register_fake
 def _swiglu_gemm_2d_fake(gate_up, weight):
     return gate_up.new_empty((gate_up.shape[0], weight.shape[0]))
+
+
+@torch.library.custom_op("wy_lib::gate_up_swiglu", mutates_args=(), device_types="cuda")
+def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``swiglu(g, u)`` of ``[g | u] = x @ weight.T`` (weight ``[2I, K]``: gate
+    rows then up rows), ``[M, I]`` bf16.  Decode rows (M <= 64) take one
+    launch with SwiGLU in the GEMM epilogue; larger M run gemm_2d then swiglu.
+    Bit-identical to gemm_2d -> swiglu when 2I >= 4096 (engine/runner.py:560-565)."""
+    from .swiglu import swiglu
+
+    assert x.ndim == 2 and x.dtype == weight.dtype == torch.bfloat16
+    assert weight.is_contiguous() and weight.shape[0] % 2 == 0
+    M, K = x.shape
+    N = weight.shape[0] // 2
+    assert weight.shape[1] == K and K % 128 == 0
+    if M > 64:
+        gu = gemm_2d(x, weight)
+        return swiglu(gu[:, :N], gu[:, N:])
+    x = _rows16(x)
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    ws_bytes = _lib.load().wy_gemm_2d_gate_up_swiglu_workspace_bytes(M, N, K)
+    ws = _lib.stream_workspace(x.device, "gemm_split", ws_bytes) if ws_bytes > 0 else None
+    _lib.call("wy_gemm_2d_gate_up_swiglu", _lib.ptr(x), x.stride(0), _lib.ptr(weight),
+              weight.stride(0), _lib.ptr(y), y.stride(0), M, N, K, _lib.ptr(ws),
+              ws.numel() if ws is not None else 0, _lib.stream(x.device))
+    return y
+
+
+@gate_up_swiglu.register_fake
+def _gate_up_swiglu_fake(x, weight):
+    return x.new_empty((x.shape[0], weight.shape[0] // 2))

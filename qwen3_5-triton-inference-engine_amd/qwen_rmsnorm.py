@@ -58,7 +58,7 @@ def add_rmsnorm(h: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
     assert weight.dtype == torch.bfloat16 and weight.is_contiguous()
     assert h.is_contiguous() and x.is_contiguous()
     d_model = x.shape[-1]
-    assert d_model % 256 == 0 and weight.shape == (d_model,)
+    assert d_model % 256 == 0 and d_model <= 1024 and weight.shape == (d_model,)
     s = torch.empty_like(x)
     out = torch.empty_like(x)
     _lib.call("wy_add_rmsnorm", _lib.ptr(h), _lib.ptr(x), _lib.ptr(weight), _lib.ptr(s),

@@ -220,7 +220,7 @@ def test_op_schemas_match_reference():
                  "paged_gqa_attention_decode_combine", "partial_rope",
                  "prefill_attention_block", "gdn_decode_block", "rmsnorm_gemm_2d",
                  "swiglu_gemm_2d", "embedding_gather", "residual_add", "swiglu",
-                 "lm_head_argmax", "add_rmsnorm"):
+                 "lm_head_argmax", "add_rmsnorm", "gate_up_swiglu"):
         assert hasattr(torch.ops.wy_lib, name)
 
 

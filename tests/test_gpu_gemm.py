@@ -169,6 +169,40 @@ def test_swiglu_gemm_equals_separate_ops(pkg, dev, M):
     assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
 
 
+@pytest.mark.parametrize("M", [1, 17, 32, 64, 100])
+def test_gate_up_swiglu_equals_separate_ops(pkg, dev, M):
+    """wy_gemm_2d_gate_up_swiglu == gemm_2d -> swiglu bit for bit on the
+    model's gate/up projection ([7168, 1024]); M > 64 runs those two ops."""
+    say(f"gate_up_swiglu M={M}")
+    g = torch.Generator(device=dev).manual_seed(M)
+    I, K = 3584, 1024
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(2 * I, K, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    y = pkg.gate_up_swiglu(x, w)
+    gu = pkg.gemm_2d(x, w)
+    y_ref = pkg.swiglu(gu[:, :I], gu[:, I:])
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
+
+
+@pytest.mark.parametrize("M,I,K", [(32, 1024, 2048), (5, 1000, 512), (64, 256, 4096)])
+def test_gate_up_swiglu_small_and_split(pkg, dev, M, I, K):
+    """Pair plans unlike the plain GEMM's (2I < 4096; split K with fp32
+    partials for I <= 1024): against the fp64 projection rounded to bf16,
+    then SwiGLU in fp64 (atol/rtol 2e-2, bf16 rounding of gate and up)."""
+    say(f"gate_up_swiglu M={M} I={I} K={K}")
+    g = torch.Generator(device=dev).manual_seed(I + K)
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(2 * I, K, device=dev, generator=g) * 0.03).to(torch.bfloat16)
+    for rep in range(2):  # the split counters must be left zero for the next call
+        y = pkg.gate_up_swiglu(x, w)
+        torch.cuda.synchronize()
+        gu = (x.double() @ w.double().T).to(torch.bfloat16).double()
+        gate, up = gu[:, :I], gu[:, I:]
+        ref = up * gate * torch.sigmoid(gate)
+        torch.testing.assert_close(y.double(), ref, atol=2e-2, rtol=2e-2)
+
+
 @pytest.mark.parametrize("M", [1, 32, 64])
 @pytest.mark.parametrize("N,K", [(1024, 1152), (1024, 1408), (512, 2304), (5120, 1152)])
 def test_gemm_2d_skinny_odd_k(pkg, dev, M, N, K):
