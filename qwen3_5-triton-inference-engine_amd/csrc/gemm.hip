@@ -193,6 +193,18 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
     xok[mt] = row < M;
     xp[mt] = x + int64_t(xok[mt] ? row : 0) * xs0 + kb + 8 * g;
   }
+  // K runs in batches of four 32-wide steps (all loads of a batch issued
+  // before its first MFMA), then one batch of the remaining kc % 128 steps,
+  // loaded together as well.  The first full batch's W rows are requested
+  // before the A prologue, which does not need them.
+  const int nfull = kc >> 7, rem = (kc & 127) >> 5;
+  u32x4_t w_first[4][kNT];
+  if (nfull > 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) w_first[j][nt] = ld16(wp[nt] + 32 * j);
+  }
   float rsr[kMT];
   const bf16_t *rp[kMT];
   const bf16_t *nwp = nullptr;
@@ -249,29 +261,35 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
           __builtin_bit_cast(bf16x8_t, xv), __builtin_bit_cast(bf16x8_t, wv[nt]), acc[mt][nt], 0,
           0, 0);
   };
-  int k = 0;
-  for (; k + 128 <= kc; k += 128) {
-    u32x4_t wv[4][kNT], xv[kMT][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int nt = 0; nt < kNT; ++nt) wv[j][nt] = ld16(wp[nt] + k + 32 * j);
+  // R steps from k: x loads, then the MFMAs over the given W rows
+  auto batch = [&](auto steps, const u32x4_t (&wv)[decltype(steps)::value][kNT], int k) {
+    constexpr int R = decltype(steps)::value;
+    u32x4_t xv[kMT][R];
 #pragma unroll
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xv[mt][j] = load_a(mt, k + 32 * j);
+      for (int j = 0; j < R; ++j) xv[mt][j] = load_a(mt, k + 32 * j);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < R; ++j)
 #pragma unroll
       for (int mt = 0; mt < kMT; ++mt) step(wv[j], xv[mt][j], mt);
-  }
-  for (; k < kc; k += 32) {
-    u32x4_t wv[kNT];
+  };
+  auto load_batch = [&](auto steps, int k) {
+    constexpr int R = decltype(steps)::value;
+    u32x4_t wv[R][kNT];
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) wv[nt] = ld16(wp[nt] + k);
+    for (int j = 0; j < R; ++j)
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt) step(wv, load_a(mt, k), mt);
-  }
+      for (int nt = 0; nt < kNT; ++nt) wv[j][nt] = ld16(wp[nt] + k + 32 * j);
+    batch(steps, wv, k);
+  };
+  using S4 = std::integral_constant<int, 4>;
+  if (nfull > 0) batch(S4{}, w_first, 0);
+  for (int b = 1; b < nfull; ++b) load_batch(S4{}, 128 * b);
+  const int kt = 128 * nfull;
+  if (rem == 1) load_batch(std::integral_constant<int, 1>{}, kt);
+  else if (rem == 2) load_batch(std::integral_constant<int, 2>{}, kt);
+  else if (rem == 3) load_batch(std::integral_constant<int, 3>{}, kt);
 
   // lane l of tile (mt, nt) holds rows mt*16 + 4(l/16) + i (i = 0..3) of
   // column 16 nt + l%16
