@@ -22,8 +22,17 @@ namespace {
 
 // tokens whose inputs are in flight in the prefill: deep for the latency-
 // bound narrow layout, shallow for the wide one (registers set occupancy)
+#ifndef WY_GDN_PREFETCH_NARROW
+#define WY_GDN_PREFETCH_NARROW 4
+#endif
+#ifndef WY_GDN_PREFETCH_WIDE
+#define WY_GDN_PREFETCH_WIDE 2
+#endif
+#ifndef WY_GDN_NARROW_BELOW
+#define WY_GDN_NARROW_BELOW 2048
+#endif
 template <int NC>
-constexpr int prefetch_depth() { return NC == 1 ? 4 : 2; }
+constexpr int prefetch_depth() { return NC == 1 ? WY_GDN_PREFETCH_NARROW : WY_GDN_PREFETCH_WIDE; }
 
 __device__ __forceinline__ float *state_block(const GdnArgs &a, int b, int h, int kg, int col) {
   return a.state + b * a.s_b + h * a.s_h + int64_t(kg * kRows) * a.s_k + col;
@@ -82,30 +91,43 @@ __global__ __launch_bounds__(64) void gdn_prefill_sequential_kernel(const GdnArg
     for (int j = 0; j < NC; ++j) s[i][j] = 0.f;
   // kPrefetch tokens in flight: token t's inputs are requested while token
   // t - kPrefetch is processed, so the load latency hides behind several steps.
+  // Every load and store of the main loop is unconditional (a prefetch past
+  // the end re-reads the last token; all 16 lanes of a row store the same
+  // output values), so the compiler's memory counter waits name exactly the
+  // token a step needs: a load or store that only some paths issue makes it
+  // wait for everything in flight.
   constexpr int kPrefetch = prefetch_depth<NC>();
-  TokenInT<NC> buf[kPrefetch];
+  auto store_out = [&](int t, const float (&o)[NC]) {
+    bf16_t *op = a.out + (start + t) * a.o_t + h * a.o_h + col * a.o_d;
+    if constexpr (NC == kCols)
+      store4<kContig>(op, a.o_d, o);
+    else
 #pragma unroll
-  for (int u = 0; u < kPrefetch; ++u)
-    if (u < len) load_token<kContig, NC>(a, start + u, h, kg, col, buf[u]);
-  for (int t0 = 0; t0 < len; t0 += kPrefetch) {
+      for (int e = 0; e < NC; ++e) op[e * a.o_d] = bf16_t(f32_to_bf16_bits(o[e]));
+  };
+  if (len > 0) {
+    TokenRaw<NC> buf[kPrefetch];
 #pragma unroll
-    for (int u = 0; u < kPrefetch; ++u) {
-      const int t = t0 + u;
-      if (t < len) {
+    for (int u = 0; u < kPrefetch; ++u)
+      load_token_raw<kContig, NC>(a, start + min(u, len - 1), h, kg, col, buf[u]);
+    const int nfull = len - len % kPrefetch;
+    for (int t0 = 0; t0 < nfull; t0 += kPrefetch) {
+#pragma unroll
+      for (int u = 0; u < kPrefetch; ++u) {
         float o[NC];
-        gdn_step_scaled(s, c, buf[u], o);
-        const int64_t tok = start + t;
-        if (kg == 0) {
-          bf16_t *op = a.out + tok * a.o_t + h * a.o_h + col * a.o_d;
-          if constexpr (NC == kCols)
-            store4<kContig>(op, a.o_d, o);
-          else
-#pragma unroll
-            for (int e = 0; e < NC; ++e) op[e * a.o_d] = bf16_t(f32_to_bf16_bits(o[e]));
-        }
-        if (t + kPrefetch < len) load_token<kContig, NC>(a, tok + kPrefetch, h, kg, col, buf[u]);
+        gdn_step_scaled(s, c, unpack_token(buf[u]), o);
+        store_out(t0 + u, o);
+        load_token_raw<kContig, NC>(a, start + min(t0 + u + kPrefetch, len - 1), h, kg, col,
+                                    buf[u]);
       }
     }
+#pragma unroll
+    for (int u = 0; u < kPrefetch - 1; ++u)
+      if (nfull + u < len) {
+        float o[NC];
+        gdn_step_scaled(s, c, unpack_token(buf[u]), o);
+        store_out(nfull + u, o);
+      }
   }
   float *sp = state_block(a, b, h, kg, col);
 #pragma unroll
@@ -199,7 +221,7 @@ extern "C" int wy_gdn_recurrent_prefill_sequential(
   // is a chain of dependent VALU / DPP work, so fewer columns per lane
   // shorten the chain where there are SIMDs to spare.
   const int64_t wide = int64_t(batch) * num_heads * (value_dim / kWaveCols);
-  const bool narrow = wide < 2048;
+  const bool narrow = wide < WY_GDN_NARROW_BELOW;
   const int64_t blocks = narrow ? wide * 4 : wide;
   if (blocks > 0x7fffffff) return WY_E_SHAPE;
   const hipStream_t st = static_cast<hipStream_t>(stream);

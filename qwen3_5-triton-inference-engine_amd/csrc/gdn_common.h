@@ -108,6 +108,80 @@ __device__ __forceinline__ void load_token(const GdnArgs &a, int64_t t, int h, i
   in.beta = a.beta[t * a.beta_t + h * a.beta_h];
 }
 
+// One token's inputs as loaded (bf16 bits, fp32 g / beta), for prefetching:
+// the bf16 -> fp32 unpack happens at the step (unpack_token), so the loads of
+// later tokens stay in flight while a step runs.  g and beta are read through
+// VGPR addresses: vector loads complete in order, so waiting for this token's
+// values does not wait for the prefetches issued after them (scalar loads
+// return out of order and a wait on one is a wait on all).
+template <int NC>
+struct TokenRaw {
+  u32x4_t k, q;
+  uint32_t v[NC == kCols ? 2 : NC];
+  float g, beta;
+};
+typedef const __attribute__((address_space(1))) float gfloat_t;
+
+template <bool kContig, int NC>
+__device__ __forceinline__ void load_token_raw(const GdnArgs &a, int64_t t, int h, int kg, int col,
+                                               TokenRaw<NC> &r) {
+  const bf16_t *kp = a.k + t * a.k_t + h * a.k_h + kg * kRows * a.k_d;
+  const bf16_t *qp = a.q + t * a.q_t + h * a.q_h + kg * kRows * a.q_d;
+  const bf16_t *vp = a.v + t * a.v_t + h * a.v_h + col * a.v_d;
+  if constexpr (kContig) {
+    r.k = ld16(kp);
+    r.q = ld16(qp);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r.k[e] = uint32_t(kp[2 * e * a.k_d]) | (uint32_t(kp[(2 * e + 1) * a.k_d]) << 16);
+      r.q[e] = uint32_t(qp[2 * e * a.q_d]) | (uint32_t(qp[(2 * e + 1) * a.q_d]) << 16);
+    }
+  }
+  if constexpr (NC == kCols) {
+    if constexpr (kContig) {
+      const u32x2_t w = *reinterpret_cast<const u32x2_t *>(vp);
+      r.v[0] = w[0];
+      r.v[1] = w[1];
+    } else {
+      r.v[0] = uint32_t(vp[0]) | (uint32_t(vp[a.v_d]) << 16);
+      r.v[1] = uint32_t(vp[2 * a.v_d]) | (uint32_t(vp[3 * a.v_d]) << 16);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < NC; ++e) r.v[e] = uint32_t(vp[e * a.v_d]);
+  }
+  gfloat_t *gp = (gfloat_t *)(a.g + t * a.g_t + h * a.g_h);
+  gfloat_t *bp = (gfloat_t *)(a.beta + t * a.beta_t + h * a.beta_h);
+  asm volatile("" : "+v"(gp), "+v"(bp));
+  r.g = *gp;
+  r.beta = *bp;
+}
+
+template <int NC>
+__device__ __forceinline__ TokenInT<NC> unpack_token(const TokenRaw<NC> &r) {
+  TokenInT<NC> in;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    in.k[2 * e] = bf16_lo(r.k[e]);
+    in.k[2 * e + 1] = bf16_hi(r.k[e]);
+    in.q[2 * e] = bf16_lo(r.q[e]);
+    in.q[2 * e + 1] = bf16_hi(r.q[e]);
+  }
+  if constexpr (NC == kCols) {
+    in.v[0] = bf16_lo(r.v[0]);
+    in.v[1] = bf16_hi(r.v[0]);
+    in.v[2] = bf16_lo(r.v[1]);
+    in.v[3] = bf16_hi(r.v[1]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < NC; ++e) in.v[e] = bf16_lo(r.v[e]);
+  }
+  in.g = r.g;
+  in.beta = r.beta;
+  return in;
+}
+
 // One delta-rule step on the lane's 8 x 4 block of S; returns the lane's 4
 // output columns (identical in all 16 lanes of the row).
 __device__ __forceinline__ void gdn_step(float (&s)[kRows][kCols], const TokenIn &in,
