@@ -427,10 +427,31 @@ struct TileCfg {
   static_assert(kATile % 1024 == 0 && kBTile % 1024 == 0, "whole DMA blocks");
 };
 
+// Output tile of workgroup L (a 1-D grid of tm * tn tiles).  Workgroups are
+// dealt to the 8 XCDs round-robin (L % 8), each XCD with its own L2; XCD x
+// takes a contiguous range of the tile order, and that order walks groups of
+// gm M-tiles column by column, so the workgroups an XCD runs together share
+// their x rows and W rows in that XCD's L2 instead of every XCD fetching
+// every tile's operands.
+constexpr int kXcds = 8;
+__device__ __forceinline__ void tile_of(int L, int tm, int tn, int gm, int &mt, int &nt) {
+  const int T = tm * tn;
+  const int per = (T + kXcds - 1) / kXcds;      // tiles of the fuller XCDs
+  const int full = T - kXcds * (per - 1);       // XCDs holding `per` tiles
+  const int x = L % kXcds, i = L / kXcds;
+  const int t = x < full ? x * per + i : full * per + (x - full) * (per - 1) + i;
+  const int grp = gm * tn;
+  const int first_m = (t / grp) * gm;
+  const int gsz = min(tm - first_m, gm);
+  const int r = t - (t / grp) * grp;
+  mt = first_m + r % gsz;
+  nt = r / gsz;
+}
+
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
-    bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K) {
+    bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, int gm) {
   using C = TileCfg<BM, BN, WM, WN>;
   constexpr int kFM = C::kFM, kFN = C::kFN;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -438,7 +459,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int g = lane >> 5, r32 = lane & 31;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  int mt, nt;
+  tile_of(int(blockIdx.x), (M + BM - 1) / BM, (N + BN - 1) / BN, gm, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
 
   // DMA block b (= wave + kWaves*i) of a stage: b < kABlk fills the x tile,
   // the rest the W tile; lane j of a block fills 16-byte slot 64 (b mod
@@ -568,6 +591,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     }
 }
 
+#ifndef WY_GEMM_GROUP_M
+#define WY_GEMM_GROUP_M 4
+#endif
 template <int BM, int BN, int WM, int WN>
 int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                      int64_t ys0, int M, int N, int K, hipStream_t st) {
@@ -580,8 +606,9 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
     if (e != hipSuccess) return int(e);
     attr_set = true;
   }
-  const dim3 grid(unsigned((N + BN - 1) / BN), unsigned((M + BM - 1) / BM));
-  fn<<<grid, 64 * C::kWaves, C::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K);
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  fn<<<unsigned(tm * tn), 64 * C::kWaves, C::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K,
+                                                         WY_GEMM_GROUP_M);
   return wyh::launch_status();
 }
 
