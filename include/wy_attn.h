@@ -641,9 +641,10 @@ int wy_gemm_2d_swiglu(const void *gate_up, int64_t gate_up_stride0, int64_t up_o
  * The gate/up projection with SwiGLU in the epilogue: w [2N, K] holds the gate
  * rows [0, N) and the up rows [N, 2N); y [M, N] = bf16(up * gate *
  * sigmoid(gate)) with gate = bf16(x @ w[0:N]^T), up = bf16(x @ w[N:2N]^T).
- * Equals wy_gemm_2d (x, w) -> wy_swiglu bit for bit when 2N >= 4096 (the
- * same workgroup plan; smaller N differ by fp32 summation order only).
- * M <= 64 (else WY_E_UNSUPPORTED), K % 128 == 0, rows 16-byte aligned;
+ * Equals wy_gemm_2d (x, w) -> wy_swiglu bit for bit, except for M <= 64 with
+ * 2N < 4096 (another workgroup plan: fp32 summation order differs).
+ * M <= 64 (decode) or N % 128 == 0 (else WY_E_UNSUPPORTED), K % 128 == 0,
+ * rows 16-byte aligned;
  * workspace as in wy_gemm_2d, sized by
  * wy_gemm_2d_gate_up_swiglu_workspace_bytes.  No counterpart in the
  * reference: it fuses the gate_up gemm_2d and swiglu of its MLP

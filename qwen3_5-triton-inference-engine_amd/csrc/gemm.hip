@@ -448,11 +448,18 @@ __device__ __forceinline__ void tile_of(int L, int tm, int tn, int gm, int &mt, 
   nt = r / gsz;
 }
 
-template <int BM, int BN, int WM, int WN>
+// kSwiGLU (gate/up pairs): w holds 2N rows, gate rows [0, N) and up rows
+// [N, 2N), and a tile spans BN/2 output columns: each wave's first 32-column
+// MFMA tile loads the gate rows of its 32 columns, its second the up rows of
+// the same columns, so a lane holds gate and up of one output element and the
+// epilogue writes y [M, N] = bf16(swiglu(bf16(gate), bf16(up))).
+template <int BM, int BN, int WM, int WN, bool kSwiGLU = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, int gm) {
   using C = TileCfg<BM, BN, WM, WN>;
+  static_assert(!kSwiGLU || BN / WN == 64, "gate/up pairs: two 32-column tiles per wave");
+  constexpr int kOutBN = kSwiGLU ? BN / 2 : BN;  // output columns per tile
   constexpr int kFM = C::kFM, kFN = C::kFN;
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
@@ -460,8 +467,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   const int wm = wave / WN, wn = wave % WN;
   const int g = lane >> 5, r32 = lane & 31;
   int mt, nt;
-  tile_of(int(blockIdx.x), (M + BM - 1) / BM, (N + BN - 1) / BN, gm, mt, nt);
-  const int m0 = mt * BM, n0 = nt * BN;
+  tile_of(int(blockIdx.x), (M + BM - 1) / BM, (N + kOutBN - 1) / kOutBN, gm, mt, nt);
+  const int m0 = mt * BM, n0 = nt * kOutBN;
 
   // DMA block b (= wave + kWaves*i) of a stage: b < kABlk fills the x tile,
   // the rest the W tile; lane j of a block fills 16-byte slot 64 (b mod
@@ -472,9 +479,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16_t *>(x + int64_t(m0) * xs0), 0,
       int(uint32_t(a_rows - 1) * uint32_t(xs0) * 2u + uint32_t(K) * 2u), 0x00020000);
+  // gate/up pairs: the W buffer is the whole [2N, K] matrix (N % kOutBN == 0,
+  // host), tile row r -> W row (r % 64 < 32 ? 0 : N) + n0 + 32 (r / 64) + r % 32
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t *>(w + int64_t(n0) * ws0), 0,
-      int(uint32_t(b_rows - 1) * uint32_t(ws0) * 2u + uint32_t(K) * 2u), 0x00020000);
+      const_cast<bf16_t *>(kSwiGLU ? w : w + int64_t(n0) * ws0), 0,
+      kSwiGLU ? int(uint32_t(2 * N - 1) * uint32_t(ws0) * 2u + uint32_t(K) * 2u)
+              : int(uint32_t(b_rows - 1) * uint32_t(ws0) * 2u + uint32_t(K) * 2u),
+      0x00020000);
   uint32_t voff[C::kPerWave];
 #pragma unroll
   for (int i = 0; i < C::kPerWave; ++i) {
@@ -483,7 +494,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const int sl = 64 * (is_a ? blk : blk - C::kABlk) + lane;
     const int row = sl / kTSlots, c = sl - (sl / kTSlots) * kTSlots;
     const uint32_t cb = uint32_t(c < kTK / 8 ? c : 0) * 16u;
-    voff[i] = uint32_t(row) * uint32_t(is_a ? xs0 : ws0) * 2u + cb;
+    int wrow = row;
+    if (kSwiGLU && !is_a)
+      wrow = ((row & 63) < 32 ? 0 : N) + n0 + 32 * (row >> 6) + (row & 31);
+    voff[i] = uint32_t(wrow) * uint32_t(is_a ? xs0 : ws0) * 2u + cb;
   }
   auto issue = [&](int kt, int i0 = 0, int i1 = C::kPerWave) {
     unsigned char *st = smem + (kt & 1) * C::kStage;
@@ -558,6 +572,44 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   // stages its sub-tile in LDS (the ring is free once every wave is past its
   // last operand read) and writes whole 16-byte pieces of its rows with
   // non-temporal stores; otherwise element by element.
+  if constexpr (kSwiGLU) {
+    // lane: output column 32 wn + r32 of the tile's BN/2, rows 32 i + (r&3) +
+    // 8(r>>2) + 4g of the wave's 128; the whole BM x BN/2 output tile is
+    // staged in LDS, then stored as whole row pieces by all waves
+    constexpr int kRWs = BM / WM, kSPs = kOutBN * 2 + 16;
+    static_assert(BM * kSPs <= C::kLds, "output stage fits the ring");
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = kRWs * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
+        *reinterpret_cast<bf16_t *>(smem + row * kSPs + (32 * wn + r32) * 2) =
+            bf16_t(f32_to_bf16_bits(
+                swiglu_f(bf16_round(acc[i][0][r]), bf16_round(acc[i][1][r]))));
+      }
+    __syncthreads();
+    const bool vec = ((N | ys0) & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    constexpr int kCPR = kOutBN / 8;  // 16-byte pieces per row
+#pragma unroll 4
+    for (int e = threadIdx.x; e < BM * kCPR; e += 64 * C::kWaves) {
+      const int row = e / kCPR, c = e - row * kCPR;
+      const int grow = m0 + row, gcol = n0 + 8 * c;
+      if (grow >= M) continue;
+      const u32x4_t v = ld16(smem + row * kSPs + 16 * c);
+      bf16_t *dst = y + int64_t(grow) * ys0 + gcol;
+      if (vec) {
+        st16_nt(dst, v);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          dst[2 * h] = bf16_t(v[h] & 0xffffu);
+          dst[2 * h + 1] = bf16_t(v[h] >> 16);
+        }
+      }
+    }
+    return;
+  }
   constexpr int kRW = BM / WM, kCW = BN / WN;   // the wave's sub-tile
   constexpr int kSP = kCW * 2 + 16;             // staged row pitch, bytes
   static_assert(C::kWaves * kRW * kSP <= C::kLds, "output stage fits the ring");
@@ -604,11 +656,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
 #ifndef WY_GEMM_GROUP_M
 #define WY_GEMM_GROUP_M 4
 #endif
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool kSwiGLU = false>
 int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                      int64_t ys0, int M, int N, int K, hipStream_t st) {
   using C = TileCfg<BM, BN, WM, WN>;
-  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN>;
+  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN, kSwiGLU>;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
@@ -616,7 +668,7 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
     if (e != hipSuccess) return int(e);
     attr_set = true;
   }
-  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const int tm = (M + BM - 1) / BM, tn = (N + (kSwiGLU ? BN / 2 : BN) - 1) / (kSwiGLU ? BN / 2 : BN);
   fn<<<unsigned(tm * tn), 64 * C::kWaves, C::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K,
                                                          WY_GEMM_GROUP_M);
   return wyh::launch_status();
@@ -854,7 +906,7 @@ extern "C" int wy_gemm_2d_gate_up_swiglu(const void *x, int64_t x_stride0, const
                                          void *stream) {
   if (!x || !w || !y) return WY_E_NULL;
   if (M < 0 || N < 0 || K <= 0 || K % 128) return WY_E_SHAPE;
-  if (M > kSkinnyMaxM) return WY_E_UNSUPPORTED;
+  if (M > kSkinnyMaxM && N % 128) return WY_E_UNSUPPORTED;
   if (x_stride0 % 8 || w_stride0 % 8 || x_stride0 < K || w_stride0 < K || y_stride0 < N ||
       !wyh::aligned16(x) || !wyh::aligned16(w) || (reinterpret_cast<uintptr_t>(y) & 1u))
     return WY_E_LAYOUT;
@@ -862,6 +914,14 @@ extern "C" int wy_gemm_2d_gate_up_swiglu(const void *x, int64_t x_stride0, const
       (reinterpret_cast<uintptr_t>(workspace) & 3u))
     return WY_E_LAYOUT;
   if (M == 0 || N == 0) return WY_OK;
+  if (M > kSkinnyMaxM) {
+    // 256 x 256 tiles of 128 gate + 128 up columns; 32-bit buffer offsets
+    if (int64_t(256) * x_stride0 * 2 >= INT32_MAX || int64_t(2) * N * w_stride0 * 2 >= INT32_MAX)
+      return WY_E_SHAPE;
+    return launch_tiled_cfg<256, 256, 2, 4, true>(
+        static_cast<const bf16_t *>(x), x_stride0, static_cast<const bf16_t *>(w), w_stride0,
+        static_cast<bf16_t *>(y), y_stride0, M, N, K, static_cast<hipStream_t>(stream));
+  }
   SkinnyArgs a{static_cast<const bf16_t *>(x), x_stride0, static_cast<const bf16_t *>(w),
                w_stride0, static_cast<bf16_t *>(y), y_stride0, M, N, K, 1, nullptr, nullptr,
                ProArgs{}};

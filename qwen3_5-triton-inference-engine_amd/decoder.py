@@ -304,9 +304,7 @@ class DecodeModel:
             else:
                 h = self._gdn_prefill(fused, w, i, packed)
             x, normed = add_rmsnorm(h, x, w.post_attention_layernorm, cfg.eps)
-            gate_up = gemm_2d(normed, w.gate_up)
-            h = gemm_2d(swiglu(gate_up[:, :cfg.intermediate], gate_up[:, cfg.intermediate:]),
-                        w.down_proj)
+            h = gemm_2d(gate_up_swiglu(normed, w.gate_up), w.down_proj)
         # only each prompt's last row reaches the LM head
         last = packed.cu_seqlens[1:].long() - 1
         hidden = add_rmsnorm(h[last].contiguous(), x[last].contiguous(), self.final_norm,

@@ -122,9 +122,11 @@ def _swiglu_gemm_2d_fake(gate_up, weight):
 @torch.library.custom_op("wy_lib::gate_up_swiglu", mutates_args=(), device_types="cuda")
 def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """``swiglu(g, u)`` of ``[g | u] = x @ weight.T`` (weight ``[2I, K]``: gate
-    rows then up rows), ``[M, I]`` bf16.  Decode rows (M <= 64) take one
-    launch with SwiGLU in the GEMM epilogue; larger M run gemm_2d then swiglu.
-    Bit-identical to gemm_2d -> swiglu when 2I >= 4096 (engine/runner.py:560-565)."""
+    rows then up rows), ``[M, I]`` bf16, in one launch with SwiGLU in the GEMM
+    epilogue (decode rows M <= 64 on the skinny kernel, more rows on the tile
+    kernel when I % 128 == 0; other shapes run gemm_2d then swiglu).
+    Bit-identical to gemm_2d -> swiglu except for M <= 64 with 2I < 4096
+    (engine/runner.py:560-565)."""
     from .swiglu import swiglu
 
     assert x.ndim == 2 and x.dtype == weight.dtype == torch.bfloat16
@@ -132,7 +134,7 @@ def gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     M, K = x.shape
     N = weight.shape[0] // 2
     assert weight.shape[1] == K and K % 128 == 0
-    if M > 64:
+    if M > 64 and N % 128:
         gu = gemm_2d(x, weight)
         return swiglu(gu[:, :N], gu[:, N:])
     x = _rows16(x)

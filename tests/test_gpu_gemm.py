@@ -169,10 +169,12 @@ def test_swiglu_gemm_equals_separate_ops(pkg, dev, M):
     assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
 
 
-@pytest.mark.parametrize("M", [1, 17, 32, 64, 100])
+@pytest.mark.parametrize("M", [1, 17, 32, 64, 100, 300, 4096])
 def test_gate_up_swiglu_equals_separate_ops(pkg, dev, M):
     """wy_gemm_2d_gate_up_swiglu == gemm_2d -> swiglu bit for bit on the
-    model's gate/up projection ([7168, 1024]); M > 64 runs those two ops."""
+    model's gate/up projection ([7168, 1024]): the skinny kernel's pair
+    epilogue for M <= 64, the tile kernel's (ragged last row tile at 100 and
+    300) above."""
     say(f"gate_up_swiglu M={M}")
     g = torch.Generator(device=dev).manual_seed(M)
     I, K = 3584, 1024
@@ -185,7 +187,8 @@ def test_gate_up_swiglu_equals_separate_ops(pkg, dev, M):
     assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
 
 
-@pytest.mark.parametrize("M,I,K", [(32, 1024, 2048), (5, 1000, 512), (64, 256, 4096)])
+@pytest.mark.parametrize("M,I,K", [(32, 1024, 2048), (5, 1000, 512), (64, 256, 4096),
+                                   (200, 384, 512), (130, 1000, 256)])
 def test_gate_up_swiglu_small_and_split(pkg, dev, M, I, K):
     """Pair plans unlike the plain GEMM's (2I < 4096; split K with fp32
     partials for I <= 1024): against the fp64 projection rounded to bf16,
