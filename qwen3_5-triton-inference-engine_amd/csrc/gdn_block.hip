@@ -19,13 +19,17 @@ namespace {
 
 // acc = x[t-3] w0 + x[t-2] w1 + x[t-1] w2 + x[t] w3 (fp32, in tap order),
 // y = acc * sigmoid(acc) rounded to bf16.
-__device__ __forceinline__ uint32_t conv4_silu(float s1, float s2, float s3, float x, float w0,
-                                               float w1, float w2, float w3) {
+__device__ __forceinline__ float conv4_silu_f(float s1, float s2, float s3, float x, float w0,
+                                              float w1, float w2, float w3) {
   float acc = s1 * w0;
   acc = __fmaf_rn(s2, w1, acc);
   acc = __fmaf_rn(s3, w2, acc);
   acc = __fmaf_rn(x, w3, acc);
-  return f32_to_bf16_bits(acc * (1.0f / (1.0f + __expf(-acc))));
+  return acc * (1.0f / (1.0f + __expf(-acc)));
+}
+__device__ __forceinline__ uint32_t conv4_silu(float s1, float s2, float s3, float x, float w0,
+                                               float w1, float w2, float w3) {
+  return f32_to_bf16_bits(conv4_silu_f(s1, s2, s3, x, w0, w1, w2, w3));
 }
 
 // Sum of one value per thread over a 128-thread row held by two consecutive
@@ -276,34 +280,61 @@ __global__ __launch_bounds__(256) void conv4_prefill_vec_kernel(
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int j = 0; j < 8; ++j) wt[k][j] = bf16_to_f32(w[(c0 + j) * w_c + k * w_k]);
-  u32x4_t win[kConvRun + 3];   // win[j] = x[t0 - 3 + j, c0 .. c0 + 7] (zero outside [0, T))
+  // win[j] = x[t0 - 3 + j, c0 .. c0 + 7].  Rows outside [0, T) read a clamped
+  // row instead of branching round the load (loads that only some paths
+  // issue make every later wait a wait for all of them): a row before 0 lies
+  // before every sequence's start and is masked below, a row from T on only
+  // feeds tokens from T on, which are not computed.
+  u32x4_t win[kConvRun + 3];
 #pragma unroll
   for (int j = 0; j < kConvRun + 3; ++j) {
-    const int t = t0 - 3 + j;
-    win[j] = (t >= 0 && t < T) ? ld16(x + int64_t(t) * x_t + c0) : u32x4_t{0u, 0u, 0u, 0u};
+    const int t = min(max(t0 - 3 + j, 0), T - 1);
+    win[j] = ld16(x + int64_t(t) * x_t + c0);
   }
+  // each window row is unpacked once into a rolling 4-row float window; the
+  // per-row masks for rows before the sequence's start are only evaluated for
+  // a token whose window reaches past it (a block-uniform branch); the pair
+  // rounding (v_cvt_pk_bf16_f32) equals conv4_silu's for finite values
+  float f[4][8];
+  unpack8(win[0], f[0]);
+  unpack8(win[1], f[1]);
+  unpack8(win[2], f[2]);
 #pragma unroll
   for (int i = 0; i < kConvRun; ++i) {
     const int t = t0 + i;
     if (t >= T) break;
+    unpack8(win[i + 3], f[(i + 3) & 3]);
+    const float(&a0)[8] = f[i & 3];
+    const float(&a1)[8] = f[(i + 1) & 3];
+    const float(&a2)[8] = f[(i + 2) & 3];
+    const float(&a3)[8] = f[(i + 3) & 3];
     const int lo = seq_start ? seq_start[t] : 0;
-    float a0[8], a1[8], a2[8], a3[8];
-    unpack8(win[i], a0);
-    unpack8(win[i + 1], a1);
-    unpack8(win[i + 2], a2);
-    unpack8(win[i + 3], a3);
     u32x4_t o;
+    if (t - 3 >= lo) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t y[2];
+      for (int e = 0; e < 4; ++e) {
+        float y[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = 2 * e + u;
-        y[u] = conv4_silu(t - 3 >= lo ? a0[j] : 0.f, t - 2 >= lo ? a1[j] : 0.f,
-                          t - 1 >= lo ? a2[j] : 0.f, a3[j], wt[0][j], wt[1][j], wt[2][j],
-                          wt[3][j]);
+        for (int u = 0; u < 2; ++u) {
+          const int j = 2 * e + u;
+          y[u] = conv4_silu_f(a0[j], a1[j], a2[j], a3[j], wt[0][j], wt[1][j], wt[2][j],
+                              wt[3][j]);
+        }
+        o[e] = pack_bf16x2(y[0], y[1]);
       }
-      o[e] = y[0] | (y[1] << 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float y[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int j = 2 * e + u;
+          y[u] = conv4_silu_f(t - 3 >= lo ? a0[j] : 0.f, t - 2 >= lo ? a1[j] : 0.f,
+                              t - 1 >= lo ? a2[j] : 0.f, a3[j], wt[0][j], wt[1][j], wt[2][j],
+                              wt[3][j]);
+        }
+        o[e] = pack_bf16x2(y[0], y[1]);
+      }
     }
     st16(out + int64_t(t) * o_t + c0, o);
   }

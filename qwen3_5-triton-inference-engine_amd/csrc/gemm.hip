@@ -100,7 +100,7 @@ __device__ __forceinline__ void gate_up_epilogue(const f32x4v_t (&red)[kNW][kMT 
     if (n0 + col < N) {
       if (n_split == 1) {
         y[int64_t(row) * ys0 + n0 + col] = bf16_t(f32_to_bf16_bits(
-            swiglu_f(bf16_round(sg), bf16_round(su))));
+            swiglu_f(round_bf16(sg), round_bf16(su))));
       } else {
         float *pp = part + blockIdx.y * part_stride + int64_t(row) * pw + n0 + col;
         __hip_atomic_store(pp, sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -140,7 +140,7 @@ __device__ __forceinline__ void gate_up_epilogue(const f32x4v_t (&red)[kNW][kMT 
       su += sp < n_split ? u[sp] : 0.f;
     }
     y[int64_t(row) * ys0 + n0 + col] =
-        bf16_t(f32_to_bf16_bits(swiglu_f(bf16_round(sg), bf16_round(su))));
+        bf16_t(f32_to_bf16_bits(swiglu_f(round_bf16(sg), round_bf16(su))));
   }
 }
 
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
         const int row = kRWs * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
         *reinterpret_cast<bf16_t *>(smem + row * kSPs + (32 * wn + r32) * 2) =
             bf16_t(f32_to_bf16_bits(
-                swiglu_f(bf16_round(acc[i][0][r]), bf16_round(acc[i][1][r]))));
+                swiglu_f(round_bf16(acc[i][0][r]), round_bf16(acc[i][1][r]))));
       }
     __syncthreads();
     const bool vec = ((N | ys0) & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;

@@ -31,10 +31,6 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
-// fp32 rounded to the nearest bf16 value, kept as fp32.
-__device__ __forceinline__ float bf16_round(float f) {
-  return __uint_as_float(f32_to_bf16_bits(f) << 16);
-}
 // Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even:
 // one v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
