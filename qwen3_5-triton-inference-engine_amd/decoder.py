@@ -36,7 +36,7 @@ from .gdn_gated_rmsnorm import gdn_gated_rmsnorm
 from .gdn_qk_norm_gates import gdn_qk_norm_gates
 from .gdn_recurrent_prefill import (
     call_gdn_recurrent_prefill_chunked_triton,
-    gdn_recurrent_prefill_sequential,
+    gdn_prefill_sequential_into,
 )
 
 # A single prompt at least this long takes the chunk-64 GDN prefill (the
@@ -346,10 +346,10 @@ class DecodeModel:
             # one long prompt: the chunk-64 WY path (engine/runner.py:272-273)
             core, state = call_gdn_recurrent_prefill_chunked_triton(qn, kn, v, beta, g)
             state = state.unsqueeze(0)
+            self.rec_states[i].copy_(state)
         else:
-            core, state = gdn_recurrent_prefill_sequential(qn, kn, v, beta, g,
-                                                           packed.cu_seqlens)
-        self.rec_states[i].copy_(state)
+            core = gdn_prefill_sequential_into(qn, kn, v, beta, g, packed.cu_seqlens,
+                                               self.rec_states[i])
         conv_state_from_packed_prefill(self.conv_states[i], qkv, packed.cu_seqlens)
         normed = gdn_gated_rmsnorm(core, fused[:, 3 * HD:4 * HD].view(T, H, D), w.extra["norm"])
         return gemm_2d(normed.view(T, HD), w.out_proj)

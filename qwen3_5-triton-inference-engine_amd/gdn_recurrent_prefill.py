@@ -90,6 +90,27 @@ def _gdn_recurrent_prefill_sequential_fake(q, k, v, beta, g, cu_seqlens=None):
     return torch.empty_like(v), torch.empty(shape, dtype=torch.float32, device=q.device)
 
 
+def gdn_prefill_sequential_into(q, k, v, beta, g, cu_seqlens, state):
+    """The packed sequential prefill writing its final states into ``state``
+    (``[B, H, DK, DV]`` fp32, e.g. a decoder's recurrent-state cache) instead
+    of a new tensor, for callers that validated ``cu_seqlens`` on the host
+    (``PackedBatch``): no device-to-host read of ``cu_seqlens[-1]`` and no
+    state copy.  Returns ``out [T, H, DV]`` bf16."""
+    _check_common(q, k, v, beta, g)
+    token_num, num_heads, key_dim = q.shape
+    value_dim = v.shape[-1]
+    batch = cu_seqlens.numel() - 1
+    assert cu_seqlens.dtype == torch.int32 and cu_seqlens.is_contiguous()
+    assert state.dtype == torch.float32
+    assert state.shape == (batch, num_heads, key_dim, value_dim)
+    out = torch.empty_like(v)
+    _lib.call(
+        "wy_gdn_recurrent_prefill_sequential", *_tensor_args(q, k, v, beta, g, out, state),
+        _lib.ptr(cu_seqlens), batch, num_heads, key_dim, value_dim, _lib.stream(q.device),
+    )
+    return out
+
+
 def call_gdn_recurrent_prefill_sequential_triton(q, k, v, beta, g, cu_seqlens=None):
     return gdn_recurrent_prefill_sequential(q, k, v, beta, g, cu_seqlens)
 
