@@ -579,14 +579,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     constexpr int kRWs = BM / WM, kSPs = kOutBN * 2 + 16;
     static_assert(BM * kSPs <= C::kLds, "output stage fits the ring");
     __syncthreads();
+    // rows r, r + 1 of columns c, c + 1 as one bf16 pair per lane, exchanged
+    // between adjacent lanes as in the plain epilogue below
+    const bool odd = lane & 1;
 #pragma unroll
     for (int i = 0; i < kFM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = kRWs * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
-        *reinterpret_cast<bf16_t *>(smem + row * kSPs + (32 * wn + r32) * 2) =
-            bf16_t(f32_to_bf16_bits(
-                swiglu_f(round_bf16(acc[i][0][r]), round_bf16(acc[i][1][r]))));
+      for (int r = 0; r < 16; r += 2) {
+        const float a0 = swiglu_f(round_bf16(acc[i][0][r]), round_bf16(acc[i][1][r]));
+        const float a1 = swiglu_f(round_bf16(acc[i][0][r + 1]), round_bf16(acc[i][1][r + 1]));
+        const float recv = __int_as_float(__builtin_amdgcn_update_dpp(
+            0, __float_as_int(odd ? a0 : a1), 0xB1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+        const int row = kRWs * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g + (odd ? 1 : 0);
+        *reinterpret_cast<uint32_t *>(smem + row * kSPs + (32 * wn + (r32 & ~1)) * 2) =
+            odd ? pack_bf16x2(recv, a1) : pack_bf16x2(a0, recv);
       }
     __syncthreads();
     const bool vec = ((N | ys0) & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
@@ -617,15 +623,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   if (vec_out) {
     __syncthreads();
     unsigned char *const stg = smem + wave * (kRW * kSP);
+    // rows r, r + 1 (r even) of columns c, c + 1 (c even) sit in lanes c and
+    // c + 1; one DPP swap of adjacent lanes gives the even lane row r and the
+    // odd lane row r + 1 of both columns, written as one bf16 pair (half the
+    // LDS writes of 2-byte stores, and no two lanes share a dword)
+    const bool odd = lane & 1;
 #pragma unroll
     for (int i = 0; i < kFM; ++i)
 #pragma unroll
       for (int j = 0; j < kFN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g;
-          *reinterpret_cast<bf16_t *>(stg + row * kSP + (32 * j + r32) * 2) =
-              bf16_t(f32_to_bf16_bits(acc[i][j][r]));
+        for (int r = 0; r < 16; r += 2) {
+          const float a0 = acc[i][j][r], a1 = acc[i][j][r + 1];
+          const float recv = __int_as_float(__builtin_amdgcn_update_dpp(
+              0, __float_as_int(odd ? a0 : a1), 0xB1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+          const int row = 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g + (odd ? 1 : 0);
+          *reinterpret_cast<uint32_t *>(stg + row * kSP + (32 * j + (r32 & ~1)) * 2) =
+              odd ? pack_bf16x2(recv, a1) : pack_bf16x2(a0, recv);
         }
     // one wave writes and reads its own region: its LDS operations complete
     // in issue order
