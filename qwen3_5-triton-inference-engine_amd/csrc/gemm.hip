@@ -618,38 +618,49 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   }
   constexpr int kRW = BM / WM, kCW = BN / WN;   // the wave's sub-tile
   constexpr int kSP = kCW * 2 + 16;             // staged row pitch, bytes
-  static_assert(C::kWaves * kRW * kSP <= C::kLds, "output stage fits the ring");
   const bool vec_out = ((N | ys0) & 7) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
   if (vec_out) {
-    __syncthreads();
-    unsigned char *const stg = smem + wave * (kRW * kSP);
+    // The ring slot the last K step did not use is free once every wave is
+    // past the last step's barrier (no DMA targets it any more), so each wave
+    // stages its sub-tile there without another barrier: in kParts row
+    // bands when the whole sub-tile does not fit, each band read back before
+    // the next is written (one wave's LDS operations complete in order).
+    constexpr int kParts = C::kWaves * kRW * kSP <= C::kStage ? 1 : 2;
+    static_assert(C::kWaves * (kRW / kParts) * kSP <= C::kStage, "output band fits a slot");
+    static_assert(kFM % kParts == 0, "whole MFMA tiles per band");
+    unsigned char *const stg =
+        smem + (kt_n & 1) * C::kStage + wave * ((kRW / kParts) * kSP);
     // rows r, r + 1 (r even) of columns c, c + 1 (c even) sit in lanes c and
     // c + 1; one DPP swap of adjacent lanes gives the even lane row r and the
     // odd lane row r + 1 of both columns, written as one bf16 pair (half the
     // LDS writes of 2-byte stores, and no two lanes share a dword)
     const bool odd = lane & 1;
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-#pragma unroll
-      for (int j = 0; j < kFN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const float a0 = acc[i][j][r], a1 = acc[i][j][r + 1];
-          const float recv = __int_as_float(__builtin_amdgcn_update_dpp(
-              0, __float_as_int(odd ? a0 : a1), 0xB1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
-          const int row = 32 * i + (r & 3) + 8 * (r >> 2) + 4 * g + (odd ? 1 : 0);
-          *reinterpret_cast<uint32_t *>(stg + row * kSP + (32 * j + (r32 & ~1)) * 2) =
-              odd ? pack_bf16x2(recv, a1) : pack_bf16x2(a0, recv);
-        }
-    // one wave writes and reads its own region: its LDS operations complete
-    // in issue order
     constexpr int kCPR = kCW / 8;   // 16-byte pieces per row
+#pragma unroll
+    for (int part = 0; part < kParts; ++part) {
+#pragma unroll
+      for (int ii = 0; ii < kFM / kParts; ++ii) {
+        const int i = part * (kFM / kParts) + ii;
+#pragma unroll
+        for (int j = 0; j < kFN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const float a0 = acc[i][j][r], a1 = acc[i][j][r + 1];
+            const float recv = __int_as_float(__builtin_amdgcn_update_dpp(
+                0, __float_as_int(odd ? a0 : a1), 0xB1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+            const int row = 32 * ii + (r & 3) + 8 * (r >> 2) + 4 * g + (odd ? 1 : 0);
+            *reinterpret_cast<uint32_t *>(stg + row * kSP + (32 * j + (r32 & ~1)) * 2) =
+                odd ? pack_bf16x2(recv, a1) : pack_bf16x2(a0, recv);
+          }
+      }
+      constexpr int kBandRows = kRW / kParts;
 #pragma unroll 4
-    for (int e = lane; e < kRW * kCPR; e += 64) {
-      const int row = e / kCPR, c = e - row * kCPR;
-      const int grow = m0 + kRW * wm + row, gcol = n0 + kCW * wn + 8 * c;
-      if (grow < M && gcol < N)
-        st16_nt(y + int64_t(grow) * ys0 + gcol, ld16(stg + row * kSP + 16 * c));
+      for (int e = lane; e < kBandRows * kCPR; e += 64) {
+        const int row = e / kCPR, c = e - row * kCPR;
+        const int grow = m0 + kRW * wm + part * kBandRows + row, gcol = n0 + kCW * wn + 8 * c;
+        if (grow < M && gcol < N)
+          st16_nt(y + int64_t(grow) * ys0 + gcol, ld16(stg + row * kSP + 16 * c));
+      }
     }
     return;
   }
