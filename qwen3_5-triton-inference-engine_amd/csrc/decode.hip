@@ -1052,7 +1052,7 @@ __global__ __launch_bounds__(256) void page_stream_kernel(
   }
   __syncthreads();
   const int units = prefix[nseg];
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int u0 = int(int64_t(gw) * units / kStreamWaves);
   const int u1 = int(int64_t(gw + 1) * units / kStreamWaves);
   int seg = 0;
@@ -1065,10 +1065,20 @@ __global__ __launch_bounds__(256) void page_stream_kernel(
     }
     seg = lo;
   }
+  // seg, u and the page are the same in every lane; stating it
+  // (readfirstlane) puts the page's buffer resource in SGPRs, which a buffer
+  // load needs (else each load runs in a loop over the distinct values)
+  seg = __builtin_amdgcn_readfirstlane(seg);
   auto phys_of = [&](int u) -> int64_t {  // advances seg monotonically
     while (u >= prefix[seg + 1]) ++seg;
+    seg = __builtin_amdgcn_readfirstlane(seg);
+    const int first = __builtin_amdgcn_readfirstlane(prefix[seg]);
     const int b = seg / hkv;
-    return int64_t(bt[b * bt_b + (u - prefix[seg])]);
+    // a uniform address read through the constant address space: a scalar
+    // load, which a wait on the page loads' vector-memory counter does not cover
+    typedef const __attribute__((address_space(4))) int32_t cint_t;
+    return int64_t(__builtin_amdgcn_readfirstlane(
+        ((cint_t *)bt)[b * bt_b + (u - first)]));
   };
   u32x4_t buf[2][16];
   auto issue = [&](int d, int u) {
@@ -1083,22 +1093,32 @@ __global__ __launch_bounds__(256) void page_stream_kernel(
     for (int e = 0; e < 8; ++e)
       buf[d][8 + e] = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 1024 * e, 0);
   };
-  float acc = 0.f;
+  float part[4] = {0.f, 0.f, 0.f, 0.f};  // independent sums: no long add chain
   auto consume = [&](int d) {
 #pragma unroll
     for (int e = 0; e < 16; ++e)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) acc += bf16_lo(buf[d][e][w]) + bf16_hi(buf[d][e][w]);
+      for (int w = 0; w < 4; ++w) part[w] += bf16_lo(buf[d][e][w]) + bf16_hi(buf[d][e][w]);
   };
+  // The main loop issues every load unconditionally, so the wait before
+  // consuming one unit leaves the next unit's 16 loads in flight (a load
+  // that only some paths issue makes the compiler wait for everything).
+  int u = u0;
   if (u0 < u1) issue(0, u0);
-  for (int u = u0; u < u1; u += 2) {
-    if (u + 1 < u1) issue(1, u + 1);
+  for (; u + 2 < u1; u += 2) {
+    issue(1, u + 1);
     consume(0);
-    if (u + 1 < u1) {
-      if (u + 2 < u1) issue(0, u + 2);
-      consume(1);
-    }
+    issue(0, u + 2);
+    consume(1);
   }
+  if (u + 1 < u1) {
+    issue(1, u + 1);
+    consume(0);
+    consume(1);
+  } else if (u < u1) {
+    consume(0);
+  }
+  float acc = (part[0] + part[1]) + (part[2] + part[3]);
   acc = wave_sum(acc);
   if (lane == 0) sums[gw] = acc;
 }
