@@ -49,6 +49,29 @@ def test_noalloc_step_rejects_over_capacity_before_any_launch(pkg):
     assert rc == -5 and b"capacity" in lib.wy_status_string(rc)
 
 
+def test_fused_decoder_entry_points_reject_before_launch(pkg):
+    """wy_add_rmsnorm and wy_gemm_2d_gate_up_swiglu refuse NULL, unsupported
+    widths and misaligned rows before any launch (safe without a GPU)."""
+    lib = pkg._lib.load()
+    d, odd = ctypes.c_void_p(4096), ctypes.c_void_p(4098)
+    assert lib.wy_add_rmsnorm(None, d, d, d, d, 4, 1024, 1e-6, None) == -1
+    assert lib.wy_add_rmsnorm(d, d, d, d, d, 4, 1000, 1e-6, None) == -4   # not % 256
+    assert lib.wy_add_rmsnorm(d, d, d, d, d, 4, 2048, 1e-6, None) == -4   # > 1024
+    assert lib.wy_add_rmsnorm(d, odd, d, d, d, 4, 1024, 1e-6, None) == -3
+    assert lib.wy_add_rmsnorm(d, d, d, d, d, -1, 1024, 1e-6, None) == -2
+    assert lib.wy_add_rmsnorm(d, d, d, d, d, 0, 1024, 1e-6, None) == 0    # nothing to do
+    g = lib.wy_gemm_2d_gate_up_swiglu
+    assert g(None, 1024, d, 1024, d, 3584, 4, 3584, 1024, None, 0, None) == -1
+    assert g(d, 1024, d, 1024, d, 3584, 4, 3584, 1000, None, 0, None) == -2   # K % 128
+    assert g(d, 1024, d, 1024, d, 1000, 100, 1000, 1024, None, 0, None) == -4  # M > 64, N % 128
+    assert g(odd, 1024, d, 1024, d, 3584, 4, 3584, 1024, None, 0, None) == -3
+    assert g(d, 1024, d, 1024, d, 3584, 4, 3584, 1024, None, 64, None) == -3  # bytes, no buffer
+    assert g(d, 1024, d, 1024, d, 3584, 0, 3584, 1024, None, 0, None) == 0
+    assert lib.wy_gemm_2d_gate_up_swiglu_workspace_bytes(32, 3584, 1024) == 0  # no split
+    assert lib.wy_gemm_2d_gate_up_swiglu_workspace_bytes(32, 1024, 2048) > 0   # split K
+    assert lib.wy_gemm_2d_gate_up_swiglu_workspace_bytes(100, 1024, 2048) == 0  # tile kernel
+
+
 def test_null_and_unsupported_arguments_are_rejected(pkg):
     lib = pkg._lib.load()
     s4 = (ctypes.c_int64 * 4)(1, 1, 1, 1)
