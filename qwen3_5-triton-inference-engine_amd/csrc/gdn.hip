@@ -20,8 +20,11 @@ using namespace wy::gdn;
 
 namespace {
 
-// tokens whose inputs are in flight in the prefill: deep for the latency-
-// bound narrow layout, shallow for the wide one (registers set occupancy)
+// Tokens whose inputs are in flight in the prefill: deep for the latency-
+// bound narrow layout, shallow for the wide one (registers set occupancy),
+// and the wave count (16-column waves) below which the narrow layout is
+// used.  Build-time tunables (-D) for measurement; the defaults are the
+// measured best.
 #ifndef WY_GDN_PREFETCH_NARROW
 #define WY_GDN_PREFETCH_NARROW 4
 #endif
