@@ -887,6 +887,26 @@ def gemm_bench(pkg, dev):
         out[name] = rec
         log(f"gemm {name}: {rec}")
         del x, wt
+    # the MLP's gate/up projection with SwiGLU in the GEMM epilogue
+    # (wy_lib::gate_up_swiglu) vs gemm_2d then swiglu, and hipBLASLt's GEMM
+    for name, M in (("gate_up+SwiGLU decode B=32 [7168,1024]", 32),
+                    ("gate_up+SwiGLU prefill T=4096 [7168,1024]", 4096)):
+        I, K = 3584, 1024
+        x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+        wt = (torch.randn(2 * I, K, device=dev, generator=gen) * 0.05).to(torch.bfloat16)
+        ms = time_graph_events(lambda: pkg.gate_up_swiglu(x, wt), 20)
+
+        def two_ops():
+            gu = pkg.gemm_2d(x, wt)
+            return pkg.swiglu(gu[:, :I], gu[:, I:])
+        ms2 = time_graph_events(two_ops, 20)
+        ms_ref = time_graph_events(lambda: torch.nn.functional.linear(x, wt), 20)
+        rec = {"M": M, "I": I, "K": K, "us": round(ms * 1e3, 2),
+               "gemm_then_swiglu_us": round(ms2 * 1e3, 2),
+               "hipblaslt_gemm_only_us": round(ms_ref * 1e3, 2)}
+        out[name] = rec
+        log(f"gemm {name}: {rec}")
+        del x, wt
     return out
 
 
