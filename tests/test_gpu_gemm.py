@@ -40,7 +40,8 @@ SHAPES = [
     (4096, 512, 1024), (2000, 900, 256),
     # grids of >= 384 256x256 tiles take the 8-wave 256 x 256 kernel; ragged edges
     (8292, 8132, 128), (8192, 8192, 128), (8192 + 255, 8192 + 129, 384),
-    (4096, 8224, 256),  # the GDN in_proj width at 4096 tokens (528 tiles, last column tile 32 wide)
+    (4096, 8224, 256),  # the GDN in_proj width at 4096 tokens (last 32 columns: a second launch)
+    (8192 + 100, 4128, 256), (8292, 8200, 128),  # narrow last columns (32, 8) with ragged M
 ]
 
 
