@@ -147,13 +147,17 @@ def test_two_layer_model_vs_oracle_chain(pkg, dev):
         torch.testing.assert_close(k.cpu().float(), kcs[a].float(), atol=5e-2, rtol=5e-2)
 
 
-def test_graphed_decoder_replays_equal_eager_steps(pkg, dev):
-    say("graphed decoder 4 layers, B=4, 5 replays")
+@pytest.mark.parametrize("B", [4, 20])
+def test_graphed_decoder_replays_equal_eager_steps(pkg, dev, B):
+    """B=4: the GEMM prologue fusions; B=20: the mixer blocks with add_rmsnorm
+    and the gate/up SwiGLU epilogue, whose split-K counters must be back at
+    zero for every replay."""
+    say(f"graphed decoder 4 layers, B={B}, 5 replays")
     from qwen35_amd.decoder import GraphedDecoder
     cfg = tiny_cfg(pkg, layers=4)
-    eager = build(pkg, dev, cfg, 4, 32, True, seed=3)
-    graphed = build(pkg, dev, cfg, 4, 32, True, seed=3)
-    tok = torch.tensor([5, 6, 7, 8], dtype=torch.int64, device=dev)
+    eager = build(pkg, dev, cfg, B, 32, True, seed=3)
+    graphed = build(pkg, dev, cfg, B, 32, True, seed=3)
+    tok = torch.arange(5, 5 + B, dtype=torch.int64, device=dev)
     g = GraphedDecoder(graphed, tok)
     t = tok.clone()
     for i in range(5):
