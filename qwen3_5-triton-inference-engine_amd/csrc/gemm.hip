@@ -362,18 +362,16 @@ __global__ __launch_bounds__(64 * kNW) void gemm_skinny_kernel(
 
 // ------------------------------------------------------------ tiled (M > 64)
 // Output tile BM x BN, WM x WN waves of (BM/WM) x (BN/WN) as 32 x 32 MFMA
-// tiles; K in 64-wide steps through a two-stage LDS ring filled by LDS-DMA
-// buffer loads (rows past M / N lie outside the buffer range and read zero).
+// tiles; K in 64-wide steps through an LDS ring of kS stages (two, or four
+// for a grid of at most one workgroup per CU) filled by LDS-DMA buffer loads
+// (rows past M / N lie outside the buffer range and read zero).
 // The MFMA operands are read from LDS with explicit waits: the reads of
 // k-step ks+1 are issued before the MFMAs of ks and awaited after them, so
 // the LDS latency hides behind the MFMAs (left to the compiler, each read
 // pair was awaited right before its MFMA).
-//   <128, 128, 2, 2>: 72 KiB of LDS, two workgroups per CU (small grids);
-//   <256, 256, 2, 4>: 8 waves of 128 x 64, 144 KiB, one workgroup per CU --
+//   <128, 128, 2, 2>: 64 KiB of LDS (swizzled rows), two workgroups per CU;
+//   <256, 256, 2, 4>: 8 waves of 128 x 64, 128 KiB, one workgroup per CU --
 //   half the LDS bytes per MFMA; used when the grid fills the chip.
-constexpr int kTK = 64;
-constexpr int kTSlots = kTK / 8 + 1;   // 16-byte slots per LDS row (one pad)
-constexpr int kTPitch = kTSlots * 16;  // 144 B: 16 consecutive rows hit disjoint banks
 
 // One 1 KiB global -> LDS block (16 bytes per lane).  A plain device function:
 // inside a kernel template the host-side pass cannot instantiate the builtin.
@@ -400,6 +398,9 @@ __device__ __forceinline__ void lgkm_wait_all(u32x4_t (&a)[kFM], u32x4_t (&b)[kF
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]));
   else if constexpr (kFM == 2 && kFN == 1)
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]));
+  else if constexpr (kFM == 4 && kFN == 1)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]));
   else if constexpr (kFM == 4 && kFN == 2)
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]));
@@ -414,15 +415,35 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-template <int BM, int BN, int WM, int WN>
+// LDS row layout of a stage, TK columns of k per row: padded (one spare
+// 16-byte slot per row, so consecutive rows start in different banks) or
+// swizzled (no pad; 16-byte chunk c of row r sits in slot c ^ swz(r), so the
+// rows that one ds_read_b128 touches spread over all banks with 2 TK bytes
+// per row -- a stage is 1/9 (TK = 64) or 1/5 (TK = 32) smaller).
+template <int TK, bool kSwz>
+struct TileRows {
+  static constexpr int kChunks = TK / 8;                       // 16-byte chunks of k
+  static constexpr int kSlots = kSwz ? kChunks : kChunks + 1;  // slots per LDS row
+  static constexpr int kPitch = kSlots * 16;
+  // rows sharing one 256-byte line of the 64 banks; the swizzle makes the 16
+  // rows that a quarter-wave of ds_read_b128 touches fill all 16 slots
+  static constexpr int kRowsPerLine = kSwz ? 256 / (2 * TK) : 1;
+  static_assert(TK == 32 || TK == 64, "k step");
+  __device__ static constexpr int swz(int row) {
+    return kSwz ? (row / kRowsPerLine) % kChunks : 0;
+  }
+};
+
+template <int BM, int BN, int WM, int WN, int kS = 2, int TK = 64, bool kSwz = false>
 struct TileCfg {
+  using R = TileRows<TK, kSwz>;
   static constexpr int kWaves = WM * WN;
-  static constexpr int kATile = BM * kTPitch, kBTile = BN * kTPitch;
+  static constexpr int kATile = BM * R::kPitch, kBTile = BN * R::kPitch;
   static constexpr int kStage = kATile + kBTile;
   static constexpr int kABlk = kATile / 1024;           // DMA blocks of the x tile
   static constexpr int kBlk = kABlk + kBTile / 1024;     // DMA blocks per stage
   static constexpr int kPerWave = (kBlk + kWaves - 1) / kWaves;
-  static constexpr int kLds = 2 * kStage;
+  static constexpr int kLds = kS * kStage;  // a ring of kS stages
   static constexpr int kFM = BM / WM / 32, kFN = BN / WN / 32;  // MFMA tiles per wave
   static_assert(kATile % 1024 == 0 && kBTile % 1024 == 0, "whole DMA blocks");
 };
@@ -453,11 +474,14 @@ __device__ __forceinline__ void tile_of(int L, int tm, int tn, int gm, int &mt, 
 // MFMA tile loads the gate rows of its 32 columns, its second the up rows of
 // the same columns, so a lane holds gate and up of one output element and the
 // epilogue writes y [M, N] = bf16(swiglu(bf16(gate), bf16(up))).
-template <int BM, int BN, int WM, int WN, bool kSwiGLU = false>
+template <int BM, int BN, int WM, int WN, bool kSwiGLU = false, int kS = 2, int TK = 64,
+          bool kSwz = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, int gm) {
-  using C = TileCfg<BM, BN, WM, WN>;
+  using C = TileCfg<BM, BN, WM, WN, kS, TK, kSwz>;
+  using R = typename C::R;
+  constexpr int kTPitch = R::kPitch, kTK = TK;
   static_assert(!kSwiGLU || BN / WN == 64, "gate/up pairs: two 32-column tiles per wave");
   constexpr int kOutBN = kSwiGLU ? BN / 2 : BN;  // output columns per tile
   constexpr int kFM = C::kFM, kFN = C::kFN;
@@ -489,25 +513,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   uint32_t voff[C::kPerWave];
 #pragma unroll
   for (int i = 0; i < C::kPerWave; ++i) {
-    const int blk = wave + C::kWaves * i;
+    const int blk = min(wave + C::kWaves * i, C::kBlk - 1);
     const bool is_a = blk < C::kABlk;
     const int sl = 64 * (is_a ? blk : blk - C::kABlk) + lane;
-    const int row = sl / kTSlots, c = sl - (sl / kTSlots) * kTSlots;
-    const uint32_t cb = uint32_t(c < kTK / 8 ? c : 0) * 16u;
+    const int row = sl / R::kSlots, c = sl - (sl / R::kSlots) * R::kSlots;
+    const uint32_t cb =
+        uint32_t(kSwz ? c ^ R::swz(row) : (c < R::kChunks ? c : 0)) * 16u;
     int wrow = row;
     if (kSwiGLU && !is_a)
       wrow = ((row & 63) < 32 ? 0 : N) + n0 + 32 * (row >> 6) + (row & 31);
     voff[i] = uint32_t(wrow) * uint32_t(is_a ? xs0 : ws0) * 2u + cb;
   }
+  // With more than two stages every wave issues exactly kPerWave DMAs per
+  // stage (a wave past the last block repeats it: the same bytes to the same
+  // LDS slot), so that the wait for the oldest stage is a fixed count of the
+  // wave's younger loads.
   auto issue = [&](int kt, int i0 = 0, int i1 = C::kPerWave) {
-    unsigned char *st = smem + (kt & 1) * C::kStage;
+    unsigned char *st = smem + (kt % kS) * C::kStage;
     const uint32_t soff = uint32_t(kt * kTK) * 2u;
 #pragma unroll
     for (int i = 0; i < C::kPerWave; ++i) {
       if (i < i0 || i >= i1) continue;
-      const int blk = wave + C::kWaves * i;  // wave-uniform
+      const int blk0 = wave + C::kWaves * i;  // wave-uniform
+      if (kS == 2 && blk0 >= C::kBlk) continue;
+      const int blk = min(blk0, C::kBlk - 1);
       if (blk < C::kABlk) dma_block(a_rsrc, st + blk * 1024, voff[i], soff);
-      else if (blk < C::kBlk) dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
+      else dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
     }
   };
 
@@ -520,32 +551,60 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   const int kt_n = K / kTK;
-  issue(0);
-  const uint32_t a_lane = uint32_t((BM / WM * wm + r32) * kTPitch + 16 * g);
-  const uint32_t b_lane = uint32_t(C::kATile + (BN / WN * wn + r32) * kTPitch + 16 * g);
+#pragma unroll
+  for (int s0 = 0; s0 + 1 < kS; ++s0)
+    if (s0 < kt_n) issue(s0);
+  // lane address of k sub-step ks's chunk (2 ks + g) in the wave's first
+  // row (r32); rows 32 apart share the swizzle
+  static_assert(!kSwz || 32 % (R::kRowsPerLine * R::kChunks) == 0, "swizzle period");
+  uint32_t a_lane[kTK / 16], b_lane[kTK / 16];
+#pragma unroll
+  for (int ks = 0; ks < kTK / 16; ++ks) {
+    const uint32_t cs = uint32_t(16 * ((2 * ks + g) ^ R::swz(r32)));
+    a_lane[ks] = uint32_t((BM / WM * wm + r32) * kTPitch) + cs;
+    b_lane[ks] = uint32_t(C::kATile + (BN / WN * wn + r32) * kTPitch) + cs;
+  }
   for (int kt = 0; kt < kt_n; ++kt) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this stage has landed
-    __syncthreads();                                   // and every wave is done with the other
+    // this stage has landed: the wave's loads younger than it are the
+    // stages kt + 1 .. kt + kS - 2 (fewer near the end of K)
+    if constexpr (kS == 2) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      static_assert((kS - 2) * C::kPerWave <= 63, "vmcnt range");
+      if (kt + kS - 2 < kt_n)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kS - 2) * C::kPerWave) : "memory");
+      else if (kS == 4 && kt + 1 < kt_n)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::kPerWave) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    // and every wave is done with the slot refilled next (its operand reads
+    // were awaited before its last MFMAs).  A bare s_barrier: __syncthreads'
+    // workgroup release fence would also wait for every DMA in flight
+    // (vmcnt(0)), which collapses a ring of more than two stages to one.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     // the next stage's DMA blocks: issued together after the barrier, or for
-    // the 8-wave tile spread over the first two k-steps (fewer LDS writes
-    // landing while all waves read their first operands: 256 x 256 shapes
-    // 3-6% faster, the 4-wave tiles slower)
-    constexpr int kSpread = C::kWaves == 8 ? 2 : 1;
+    // the 8-wave two-stage tile spread over the first two k-steps (fewer LDS
+    // writes landing while all waves read their first operands: 256 x 256
+    // shapes 3-6% faster, the 4-wave tiles slower)
+    constexpr int kSpread = C::kWaves == 8 && kS == 2 ? 2 : 1;
     constexpr int kPerStep = (C::kPerWave + kSpread - 1) / kSpread;
-    const bool more = kt + 1 < kt_n;
-    if (more) issue(kt + 1, 0, kPerStep);
-    const uint32_t st = lds_u32(smem + (kt & 1) * C::kStage);
-    const uint32_t abase = st + a_lane, bbase = st + b_lane;
+    const bool more = kt + kS - 1 < kt_n;
+    if (more) issue(kt + kS - 1, 0, kPerStep);
+    const uint32_t st = lds_u32(smem + (kt % kS) * C::kStage);
     u32x4_t av[2][kFM], bv[2][kFN];
     auto load = [&](auto bufc, auto ksc) {
       constexpr int buf = decltype(bufc)::value, ks = decltype(ksc)::value;
+      const uint32_t abase = st + a_lane[ks], bbase = st + b_lane[ks];
       static_for<0, kFM>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
-        av[buf][t] = ds_read16<t * 32 * kTPitch + ks * 32>(abase);
+        av[buf][t] = ds_read16<t * 32 * kTPitch>(abase);
       });
       static_for<0, kFN>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
-        bv[buf][t] = ds_read16<t * 32 * kTPitch + ks * 32>(bbase);
+        bv[buf][t] = ds_read16<t * 32 * kTPitch>(bbase);
       });
     };
     load(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
@@ -562,7 +621,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
               __builtin_bit_cast(bf16x8_t, av[cur][i]), __builtin_bit_cast(bf16x8_t, bv[cur][j]),
               acc[i][j], 0, 0, 0);
       if constexpr (ks + 1 < kSpread)
-        if (more) issue(kt + 1, (ks + 1) * kPerStep, (ks + 2) * kPerStep);
+        if (more) issue(kt + kS - 1, (ks + 1) * kPerStep, (ks + 2) * kPerStep);
       if constexpr (ks + 1 < kTK / 16) lgkm_wait_all<kFM, kFN>(av[cur ^ 1], bv[cur ^ 1]);
     });
   }
@@ -625,11 +684,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     // stages its sub-tile there without another barrier: in kParts row
     // bands when the whole sub-tile does not fit, each band read back before
     // the next is written (one wave's LDS operations complete in order).
-    constexpr int kParts = C::kWaves * kRW * kSP <= C::kStage ? 1 : 2;
-    static_assert(C::kWaves * (kRW / kParts) * kSP <= C::kStage, "output band fits a slot");
-    static_assert(kFM % kParts == 0, "whole MFMA tiles per band");
-    unsigned char *const stg =
-        smem + (kt_n & 1) * C::kStage + wave * ((kRW / kParts) * kSP);
+    // (when no band of whole MFMA tiles fits one slot, all waves first meet
+    // at a barrier and the bands go to the whole ring)
+    constexpr auto fits = [](int parts, int room) {
+      return kFM % parts == 0 && C::kWaves * (kRW / parts) * kSP <= room;
+    };
+    constexpr bool kInSlot = fits(1, C::kStage) || fits(2, C::kStage) || fits(4, C::kStage);
+    constexpr int kRoom = kInSlot ? C::kStage : C::kLds;
+    constexpr int kParts = fits(1, kRoom) ? 1 : fits(2, kRoom) ? 2 : 4;
+    static_assert(fits(kParts, kRoom), "output band fits");
+    if constexpr (!kInSlot) __syncthreads();
+    unsigned char *const stg = smem + (kInSlot ? (kt_n % kS) * C::kStage : 0) +
+                               wave * ((kRW / kParts) * kSP);
     // rows r, r + 1 (r even) of columns c, c + 1 (c even) sit in lanes c and
     // c + 1; one DPP swap of adjacent lanes gives the even lane row r and the
     // odd lane row r + 1 of both columns, written as one bf16 pair (half the
@@ -681,11 +747,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
 #ifndef WY_GEMM_GROUP_M
 #define WY_GEMM_GROUP_M 4
 #endif
-template <int BM, int BN, int WM, int WN, bool kSwiGLU = false>
+template <int BM, int BN, int WM, int WN, bool kSwiGLU = false, int kS = 2, int TK = 64,
+          bool kSwz = false>
 int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                      int64_t ys0, int M, int N, int K, hipStream_t st) {
-  using C = TileCfg<BM, BN, WM, WN>;
-  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN, kSwiGLU>;
+  using C = TileCfg<BM, BN, WM, WN, kS, TK, kSwz>;
+  static_assert(C::kLds <= 160 * 1024, "LDS");
+  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN, kSwiGLU, kS, TK, kSwz>;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
@@ -704,8 +772,39 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
 // 73 -> 68 us; at 320 tiles, [4096, 5120], it lost 54 -> 65 us), else 128 x
 // 128 (two workgroups per CU, four times the workgroups, so a partial last
 // round costs less), or 128 x 64 below two 128 x 128 tiles per CU.
+// Build-time tunables of the tile launches (measured defaults): the swizzled
+// LDS rows, and per tile shape the ring depth (stages) and the k step.
+// 128 x 64 tiles take a 4-stage ring when the grid is at most one workgroup
+// per CU (nothing else hides the latency), else two stages (two workgroups
+// per CU).  Deeper rings that cost a second workgroup per CU, and 32-wide k
+// steps, measured slower.
+#ifndef WY_GEMM_SWZ
+#define WY_GEMM_SWZ 1
+#endif
+#ifndef WY_GEMM_S256
+#define WY_GEMM_S256 2
+#endif
+#ifndef WY_GEMM_TK256
+#define WY_GEMM_TK256 64
+#endif
+#ifndef WY_GEMM_S128
+#define WY_GEMM_S128 2
+#endif
+#ifndef WY_GEMM_TK128
+#define WY_GEMM_TK128 64
+#endif
+#ifndef WY_GEMM_SMID
+#define WY_GEMM_SMID 2
+#endif
+#ifndef WY_GEMM_TKMID
+#define WY_GEMM_TKMID 64
+#endif
+#ifndef WY_GEMM_SMID1
+#define WY_GEMM_SMID1 4
+#endif
 int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                  int64_t ys0, int M, int N, int K, hipStream_t st) {
+  constexpr bool kSw = WY_GEMM_SWZ != 0;
   const int64_t big = int64_t((M + 255) / 256) * ((N + 255) / 256);
   // A narrow last column of 256-wide tiles (N % 256 <= 64, e.g. the GDN
   // in_proj's 8224 = 8192 + 32) costs a whole extra round of tiles for a
@@ -715,17 +814,27 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
   const int tail = N % 256;
   if (big >= 384 && tail != 0 && tail <= 64 && N > 256) {
     const int n_main = N - tail;
-    const int rc = launch_tiled_cfg<256, 256, 2, 4>(x, xs0, w, ws0, y, ys0, M, n_main, K, st);
+    const int rc = launch_tiled_cfg<256, 256, 2, 4, false, WY_GEMM_S256, WY_GEMM_TK256, kSw>(
+        x, xs0, w, ws0, y, ys0, M, n_main, K, st);
     if (rc != WY_OK) return rc;
     return launch_tiled(x, xs0, w + int64_t(n_main) * ws0, ws0, y + n_main, ys0, M, tail, K, st);
   }
   if (big >= 384)
-    return launch_tiled_cfg<256, 256, 2, 4>(x, xs0, w, ws0, y, ys0, M, N, K, st);
+    return launch_tiled_cfg<256, 256, 2, 4, false, WY_GEMM_S256, WY_GEMM_TK256, kSw>(
+        x, xs0, w, ws0, y, ys0, M, N, K, st);
   // fewer 128 x 128 tiles than two per CU (e.g. k_proj and o_proj at 4096
   // tokens): 128 x 64 tiles put twice as many workgroups on the chip
   const int64_t mid = int64_t((M + 127) / 128) * ((N + 127) / 128);
-  if (mid < 512) return launch_tiled_cfg<128, 64, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
-  return launch_tiled_cfg<128, 128, 2, 2>(x, xs0, w, ws0, y, ys0, M, N, K, st);
+  if (mid < 512) {
+    const int64_t t64 = int64_t((M + 127) / 128) * ((N + 63) / 64);
+    if (t64 <= 256)
+      return launch_tiled_cfg<128, 64, 2, 2, false, WY_GEMM_SMID1, WY_GEMM_TKMID, kSw>(
+          x, xs0, w, ws0, y, ys0, M, N, K, st);
+    return launch_tiled_cfg<128, 64, 2, 2, false, WY_GEMM_SMID, WY_GEMM_TKMID, kSw>(
+        x, xs0, w, ws0, y, ys0, M, N, K, st);
+  }
+  return launch_tiled_cfg<128, 128, 2, 2, false, WY_GEMM_S128, WY_GEMM_TK128, kSw>(
+      x, xs0, w, ws0, y, ys0, M, N, K, st);
 }
 
 struct SkinnyArgs {
@@ -955,7 +1064,7 @@ extern "C" int wy_gemm_2d_gate_up_swiglu(const void *x, int64_t x_stride0, const
     // 256 x 256 tiles of 128 gate + 128 up columns; 32-bit buffer offsets
     if (int64_t(256) * x_stride0 * 2 >= INT32_MAX || int64_t(2) * N * w_stride0 * 2 >= INT32_MAX)
       return WY_E_SHAPE;
-    return launch_tiled_cfg<256, 256, 2, 4, true>(
+    return launch_tiled_cfg<256, 256, 2, 4, true, WY_GEMM_S256, WY_GEMM_TK256, WY_GEMM_SWZ != 0>(
         static_cast<const bf16_t *>(x), x_stride0, static_cast<const bf16_t *>(w), w_stride0,
         static_cast<bf16_t *>(y), y_stride0, M, N, K, static_cast<hipStream_t>(stream));
   }
