@@ -812,14 +812,23 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
   // element's K order is the same in every tile shape, so the result is
   // unchanged; 4096 x 8224: 90.5 -> 68.1 + 9.2 us).
   const int tail = N % 256;
-  if (big >= 384 && tail != 0 && tail <= 64 && N > 256) {
+#ifndef WY_GEMM_BIG_MIN
+#define WY_GEMM_BIG_MIN 384
+#endif
+#ifndef WY_GEMM_BIG_ROUND
+#define WY_GEMM_BIG_ROUND 240
+#endif
+  // 256 x 256 tiles from WY_GEMM_BIG_MIN of them, or when they make one
+  // nearly full round of the 256 CUs
+  const bool use_big = big >= WY_GEMM_BIG_MIN || (big >= WY_GEMM_BIG_ROUND && big <= 256);
+  if (use_big && tail != 0 && tail <= 64 && N > 256) {
     const int n_main = N - tail;
     const int rc = launch_tiled_cfg<256, 256, 2, 4, false, WY_GEMM_S256, WY_GEMM_TK256, kSw>(
         x, xs0, w, ws0, y, ys0, M, n_main, K, st);
     if (rc != WY_OK) return rc;
     return launch_tiled(x, xs0, w + int64_t(n_main) * ws0, ws0, y + n_main, ys0, M, tail, K, st);
   }
-  if (big >= 384)
+  if (use_big)
     return launch_tiled_cfg<256, 256, 2, 4, false, WY_GEMM_S256, WY_GEMM_TK256, kSw>(
         x, xs0, w, ws0, y, ys0, M, N, K, st);
   // fewer 128 x 128 tiles than two per CU (e.g. k_proj and o_proj at 4096
@@ -830,6 +839,13 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
     if (t64 <= 256)
       return launch_tiled_cfg<128, 64, 2, 2, false, WY_GEMM_SMID1, WY_GEMM_TKMID, kSw>(
           x, xs0, w, ws0, y, ys0, M, N, K, st);
+#ifndef WY_GEMM_MIDBIG
+#define WY_GEMM_MIDBIG 1
+#endif
+    if constexpr (WY_GEMM_MIDBIG == 1)
+      return launch_tiled_cfg<128, 128, 2, 2, false, 4, 64, kSw>(x, xs0, w, ws0, y, ys0, M, N, K, st);
+    if constexpr (WY_GEMM_MIDBIG == 2)
+      return launch_tiled_cfg<128, 128, 2, 2, false, 3, 64, kSw>(x, xs0, w, ws0, y, ys0, M, N, K, st);
     return launch_tiled_cfg<128, 64, 2, 2, false, WY_GEMM_SMID, WY_GEMM_TKMID, kSw>(
         x, xs0, w, ws0, y, ys0, M, N, K, st);
   }

@@ -42,6 +42,11 @@ SHAPES = [
     (8292, 8132, 128), (8192, 8192, 128), (8192 + 255, 8192 + 129, 384),
     (4096, 8224, 256),  # the GDN in_proj width at 4096 tokens (last 32 columns: a second launch)
     (8192 + 100, 4128, 256), (8292, 8200, 128),  # narrow last columns (32, 8) with ragged M
+    # deeper LDS rings: 128 x 128 tiles with 4 stages (o_proj at 4096 tokens; ragged, K
+    # steps not a multiple of the ring), 128 x 64 with 4 stages down to K = 128 (two steps)
+    (4096, 1024, 2048), (3000, 1000, 1152), (1000, 1024, 128),
+    # 256 x 256 tiles when they make one nearly full round of the CUs (ragged M)
+    (8192 - 100, 2048, 384),
 ]
 
 
