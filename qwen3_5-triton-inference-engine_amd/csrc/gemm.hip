@@ -535,10 +535,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     for (int i = 0; i < C::kPerWave; ++i) {
       if (i < i0 || i >= i1) continue;
       const int blk0 = wave + C::kWaves * i;  // wave-uniform
-      if (kS == 2 && blk0 >= C::kBlk) continue;
-      const int blk = min(blk0, C::kBlk - 1);
-      if (blk < C::kABlk) dma_block(a_rsrc, st + blk * 1024, voff[i], soff);
-      else dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
+      if constexpr (C::kABlk % C::kWaves == 0 && C::kBlk % C::kWaves == 0) {
+        // block i of every wave is an x block for i < kABlk / kWaves: no branch
+        dma_block(i < C::kABlk / C::kWaves ? a_rsrc : b_rsrc, st + blk0 * 1024, voff[i], soff);
+      } else {
+        if (kS == 2 && blk0 >= C::kBlk) continue;
+        const int blk = min(blk0, C::kBlk - 1);
+        if (blk < C::kABlk) dma_block(a_rsrc, st + blk * 1024, voff[i], soff);
+        else dma_block(b_rsrc, st + blk * 1024, voff[i], soff);
+      }
     }
   };
 
@@ -564,27 +569,102 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     a_lane[ks] = uint32_t((BM / WM * wm + r32) * kTPitch) + cs;
     b_lane[ks] = uint32_t(C::kATile + (BN / WN * wn + r32) * kTPitch) + cs;
   }
-  for (int kt = 0; kt < kt_n; ++kt) {
-    // this stage has landed: the wave's loads younger than it are the
-    // stages kt + 1 .. kt + kS - 2 (fewer near the end of K)
+#ifndef WY_GEMM_EARLY_BARRIER
+#define WY_GEMM_EARLY_BARRIER 1
+#endif
+  // wait until stage t has landed: the wave's loads younger than it are the
+  // stages t + 1 .. t + kS - 2 that were issued (fewer near the end of K)
+  auto wait_stage = [&](int t) {
     if constexpr (kS == 2) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
       static_assert((kS - 2) * C::kPerWave <= 63, "vmcnt range");
-      if (kt + kS - 2 < kt_n)
+      if (t + kS - 2 < kt_n)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kS - 2) * C::kPerWave) : "memory");
-      else if (kS == 4 && kt + 1 < kt_n)
+      else if (kS == 4 && t + 1 < kt_n)
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::kPerWave) : "memory");
       else
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    // and every wave is done with the slot refilled next (its operand reads
-    // were awaited before its last MFMAs).  A bare s_barrier: __syncthreads'
-    // workgroup release fence would also wait for every DMA in flight
-    // (vmcnt(0)), which collapses a ring of more than two stages to one.
+  };
+  // A bare s_barrier: __syncthreads' workgroup release fence would also wait
+  // for every DMA in flight (vmcnt(0)), which collapses the ring to one stage.
+  auto barrier = [&]() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+  };
+  u32x4_t av[2][kFM], bv[2][kFN];
+  auto load = [&](uint32_t st, auto bufc, auto ksc) {
+    constexpr int buf = decltype(bufc)::value, ks = decltype(ksc)::value;
+    const uint32_t abase = st + a_lane[ks], bbase = st + b_lane[ks];
+    static_for<0, kFM>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      av[buf][t] = ds_read16<t * 32 * kTPitch>(abase);
+    });
+    static_for<0, kFN>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      bv[buf][t] = ds_read16<t * 32 * kTPitch>(bbase);
+    });
+  };
+  auto mfmas = [&](auto bufc) {
+    constexpr int cur = decltype(bufc)::value;
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, av[cur][i]), __builtin_bit_cast(bf16x8_t, bv[cur][j]),
+            acc[i][j], 0, 0, 0);
+  };
+  const uint32_t smem0 = lds_u32(smem);
+  constexpr int kKS = kTK / 16;  // MFMA k sub-steps per stage (even)
+  static_assert(kKS % 2 == 0, "sub-step buffers alternate");
+  if constexpr (WY_GEMM_EARLY_BARRIER && C::kWaves == 4) {
+    // The barrier that hands slot kt back to the DMA and makes stage kt + 1
+    // visible sits before the last sub-step of step kt: the reads of step
+    // kt + 1's first sub-step and the refill DMA then overlap that sub-step's
+    // MFMAs instead of opening every step with an exposed LDS round trip
+    // (4-wave tiles 2-5% faster; the 8-wave tile keeps its DMA spread over
+    // two sub-steps after a barrier that opens the step, which measured 3%
+    // better there).
+    wait_stage(0);
+    barrier();
+    load(smem0, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    if (kS - 1 < kt_n) issue(kS - 1);
+    for (int kt = 0; kt < kt_n; ++kt) {
+      const uint32_t st = smem0 + uint32_t((kt % kS) * C::kStage);
+      const bool more = kt + 1 < kt_n;
+      lgkm_wait_all<kFM, kFN>(av[0], bv[0]);
+      static_for<0, kKS>([&](auto ksc) {
+        constexpr int ks = decltype(ksc)::value, cur = ks & 1;
+        if constexpr (ks + 1 < kKS) {
+          load(st, std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, ks + 1>{});
+        } else {
+          if (more) {
+            wait_stage(kt + 1);
+            barrier();
+            load(smem0 + uint32_t(((kt + 1) % kS) * C::kStage),
+                 std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, 0>{});
+            if (kt + kS < kt_n) issue(kt + kS);
+            // keep this sub-step's MFMAs after the barrier (they touch no
+            // memory, so the compiler would otherwise hoist them above it)
+            u32x4_t(&ac)[kFM] = av[cur];
+            u32x4_t(&bc)[kFN] = bv[cur];
+#pragma unroll
+            for (int t = 0; t < kFM; ++t) asm volatile("" : "+v"(ac[t]));
+#pragma unroll
+            for (int t = 0; t < kFN; ++t) asm volatile("" : "+v"(bc[t]));
+          }
+        }
+        mfmas(std::integral_constant<int, cur>{});
+        if constexpr (ks + 1 < kKS) lgkm_wait_all<kFM, kFN>(av[cur ^ 1], bv[cur ^ 1]);
+      });
+    }
+  } else {
+  for (int kt = 0; kt < kt_n; ++kt) {
+    wait_stage(kt);
+    barrier();  // and every wave is done with the slot refilled next
     // the next stage's DMA blocks: issued together after the barrier, or for
     // the 8-wave two-stage tile spread over the first two k-steps (fewer LDS
     // writes landing while all waves read their first operands: 256 x 256
@@ -593,37 +673,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     constexpr int kPerStep = (C::kPerWave + kSpread - 1) / kSpread;
     const bool more = kt + kS - 1 < kt_n;
     if (more) issue(kt + kS - 1, 0, kPerStep);
-    const uint32_t st = lds_u32(smem + (kt % kS) * C::kStage);
-    u32x4_t av[2][kFM], bv[2][kFN];
-    auto load = [&](auto bufc, auto ksc) {
-      constexpr int buf = decltype(bufc)::value, ks = decltype(ksc)::value;
-      const uint32_t abase = st + a_lane[ks], bbase = st + b_lane[ks];
-      static_for<0, kFM>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        av[buf][t] = ds_read16<t * 32 * kTPitch>(abase);
-      });
-      static_for<0, kFN>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        bv[buf][t] = ds_read16<t * 32 * kTPitch>(bbase);
-      });
-    };
-    load(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    const uint32_t st = smem0 + uint32_t((kt % kS) * C::kStage);
+    load(st, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
     lgkm_wait_all<kFM, kFN>(av[0], bv[0]);
-    static_for<0, kTK / 16>([&](auto ksc) {
+    static_for<0, kKS>([&](auto ksc) {
       constexpr int ks = decltype(ksc)::value, cur = ks & 1;
-      if constexpr (ks + 1 < kTK / 16)
-        load(std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, ks + 1>{});
-#pragma unroll
-      for (int i = 0; i < kFM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8_t, av[cur][i]), __builtin_bit_cast(bf16x8_t, bv[cur][j]),
-              acc[i][j], 0, 0, 0);
+      if constexpr (ks + 1 < kKS)
+        load(st, std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, ks + 1>{});
+      mfmas(std::integral_constant<int, cur>{});
       if constexpr (ks + 1 < kSpread)
         if (more) issue(kt + kS - 1, (ks + 1) * kPerStep, (ks + 2) * kPerStep);
-      if constexpr (ks + 1 < kTK / 16) lgkm_wait_all<kFM, kFN>(av[cur ^ 1], bv[cur ^ 1]);
+      if constexpr (ks + 1 < kKS) lgkm_wait_all<kFM, kFN>(av[cur ^ 1], bv[cur ^ 1]);
     });
+  }
   }
 
   // acc[i][j] register r of lane l: row (r&3) + 8(r>>2) + 4(l/32) of m-tile i,
