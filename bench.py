@@ -868,6 +868,8 @@ def gemm_bench(pkg, dev):
               ("prefill T=4096 q_proj [2048,1024]", 4096, 2048, 1024),
               ("prefill T=4096 k_proj [512,1024]", 4096, 512, 1024),
               ("prefill T=4096 o_proj [1024,2048]", 4096, 1024, 2048),
+              ("prefill T=4096 down_proj [1024,3584]", 4096, 1024, 3584),
+              ("prefill T=4096 GDN in_proj [8224,1024]", 4096, 8224, 1024),
               ("prefill T=16384 [6144,1024]", 16384, 6144, 1024)]
     out = {}
     for name, M, N, K in shapes:
