@@ -415,28 +415,23 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-// LDS row layout of a stage, TK columns of k per row: padded (one spare
-// 16-byte slot per row, so consecutive rows start in different banks) or
-// swizzled (no pad; 16-byte chunk c of row r sits in slot c ^ swz(r), so the
-// rows that one ds_read_b128 touches spread over all banks with 2 TK bytes
-// per row -- a stage is 1/9 (TK = 64) or 1/5 (TK = 32) smaller).
-template <int TK, bool kSwz>
+// LDS row layout of a stage: a tile row holds its 64 k values (128 bytes, no
+// pad slot) with 16-byte chunk c in slot c ^ swz(r).  Two rows share a
+// 256-byte line of the 64 banks, and swz(r) = (r / 2) % 8 makes the 16 rows
+// that a quarter-wave of ds_read_b128 touches fill all 16 slots of the line
+// (swizzling on r % 8 left every read 2-way conflicted; a pad slot per row
+// costs 1/9 more LDS per stage).
+constexpr int kTK = 64;  // k values per ring stage
 struct TileRows {
-  static constexpr int kChunks = TK / 8;                       // 16-byte chunks of k
-  static constexpr int kSlots = kSwz ? kChunks : kChunks + 1;  // slots per LDS row
-  static constexpr int kPitch = kSlots * 16;
-  // rows sharing one 256-byte line of the 64 banks; the swizzle makes the 16
-  // rows that a quarter-wave of ds_read_b128 touches fill all 16 slots
-  static constexpr int kRowsPerLine = kSwz ? 256 / (2 * TK) : 1;
-  static_assert(TK == 32 || TK == 64, "k step");
-  __device__ static constexpr int swz(int row) {
-    return kSwz ? (row / kRowsPerLine) % kChunks : 0;
-  }
+  static constexpr int kChunks = kTK / 8;  // 16-byte chunks of k per row
+  static constexpr int kPitch = kChunks * 16;
+  static constexpr int kRowsPerLine = 256 / kPitch;
+  __device__ static constexpr int swz(int row) { return (row / kRowsPerLine) % kChunks; }
 };
 
-template <int BM, int BN, int WM, int WN, int kS = 2, int TK = 64, bool kSwz = false>
+template <int BM, int BN, int WM, int WN, int kS = 2>
 struct TileCfg {
-  using R = TileRows<TK, kSwz>;
+  using R = TileRows;
   static constexpr int kWaves = WM * WN;
   static constexpr int kATile = BM * R::kPitch, kBTile = BN * R::kPitch;
   static constexpr int kStage = kATile + kBTile;
@@ -474,14 +469,13 @@ __device__ __forceinline__ void tile_of(int L, int tm, int tn, int gm, int &mt, 
 // MFMA tile loads the gate rows of its 32 columns, its second the up rows of
 // the same columns, so a lane holds gate and up of one output element and the
 // epilogue writes y [M, N] = bf16(swiglu(bf16(gate), bf16(up))).
-template <int BM, int BN, int WM, int WN, bool kSwiGLU = false, int kS = 2, int TK = 64,
-          bool kSwz = false>
+template <int BM, int BN, int WM, int WN, bool kSwiGLU = false, int kS = 2>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const bf16_t *__restrict__ x, int64_t xs0, const bf16_t *__restrict__ w, int64_t ws0,
     bf16_t *__restrict__ y, int64_t ys0, int M, int N, int K, int gm) {
-  using C = TileCfg<BM, BN, WM, WN, kS, TK, kSwz>;
+  using C = TileCfg<BM, BN, WM, WN, kS>;
   using R = typename C::R;
-  constexpr int kTPitch = R::kPitch, kTK = TK;
+  constexpr int kTPitch = R::kPitch;
   static_assert(!kSwiGLU || BN / WN == 64, "gate/up pairs: two 32-column tiles per wave");
   constexpr int kOutBN = kSwiGLU ? BN / 2 : BN;  // output columns per tile
   constexpr int kFM = C::kFM, kFN = C::kFN;
@@ -516,9 +510,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     const int blk = min(wave + C::kWaves * i, C::kBlk - 1);
     const bool is_a = blk < C::kABlk;
     const int sl = 64 * (is_a ? blk : blk - C::kABlk) + lane;
-    const int row = sl / R::kSlots, c = sl - (sl / R::kSlots) * R::kSlots;
+    const int row = sl / R::kChunks, c = sl - (sl / R::kChunks) * R::kChunks;
     const uint32_t cb =
-        uint32_t(kSwz ? c ^ R::swz(row) : (c < R::kChunks ? c : 0)) * 16u;
+        uint32_t(c ^ R::swz(row)) * 16u;
     int wrow = row;
     if (kSwiGLU && !is_a)
       wrow = ((row & 63) < 32 ? 0 : N) + n0 + 32 * (row >> 6) + (row & 31);
@@ -561,7 +555,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     if (s0 < kt_n) issue(s0);
   // lane address of k sub-step ks's chunk (2 ks + g) in the wave's first
   // row (r32); rows 32 apart share the swizzle
-  static_assert(!kSwz || 32 % (R::kRowsPerLine * R::kChunks) == 0, "swizzle period");
+  static_assert(32 % (R::kRowsPerLine * R::kChunks) == 0, "swizzle period");
   uint32_t a_lane[kTK / 16], b_lane[kTK / 16];
 #pragma unroll
   for (int ks = 0; ks < kTK / 16; ++ks) {
@@ -569,9 +563,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     a_lane[ks] = uint32_t((BM / WM * wm + r32) * kTPitch) + cs;
     b_lane[ks] = uint32_t(C::kATile + (BN / WN * wn + r32) * kTPitch) + cs;
   }
-#ifndef WY_GEMM_EARLY_BARRIER
-#define WY_GEMM_EARLY_BARRIER 1
-#endif
   // wait until stage t has landed: the wave's loads younger than it are the
   // stages t + 1 .. t + kS - 2 that were issued (fewer near the end of K)
   auto wait_stage = [&](int t) {
@@ -610,12 +601,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
 // The MFMA batch runs at raised wave priority (s_setprio), so the wave that
 // has operands keeps the matrix pipe fed while the SIMD's other wave issues
 // its LDS reads and DMA (1-4% on every tile shape).
-#ifndef WY_GEMM_SETPRIO
-#define WY_GEMM_SETPRIO 1
-#endif
   auto mfmas = [&](auto bufc) {
     constexpr int cur = decltype(bufc)::value;
-    if constexpr (WY_GEMM_SETPRIO) __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int i = 0; i < kFM; ++i)
 #pragma unroll
@@ -623,12 +611,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8_t, av[cur][i]), __builtin_bit_cast(bf16x8_t, bv[cur][j]),
             acc[i][j], 0, 0, 0);
-    if constexpr (WY_GEMM_SETPRIO) __builtin_amdgcn_s_setprio(0);
+    __builtin_amdgcn_s_setprio(0);
   };
   const uint32_t smem0 = lds_u32(smem);
   constexpr int kKS = kTK / 16;  // MFMA k sub-steps per stage (even)
   static_assert(kKS % 2 == 0, "sub-step buffers alternate");
-  if constexpr (WY_GEMM_EARLY_BARRIER && C::kWaves == 4) {
+  if constexpr (C::kWaves == 4) {
     // The barrier that hands slot kt back to the DMA and makes stage kt + 1
     // visible sits before the last sub-step of step kt: the reads of step
     // kt + 1's first sub-step and the refill DMA then overlap that sub-step's
@@ -817,13 +805,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
 #ifndef WY_GEMM_GROUP_M
 #define WY_GEMM_GROUP_M 4
 #endif
-template <int BM, int BN, int WM, int WN, bool kSwiGLU = false, int kS = 2, int TK = 64,
-          bool kSwz = false>
+template <int BM, int BN, int WM, int WN, bool kSwiGLU = false, int kS = 2>
 int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                      int64_t ys0, int M, int N, int K, hipStream_t st) {
-  using C = TileCfg<BM, BN, WM, WN, kS, TK, kSwz>;
+  using C = TileCfg<BM, BN, WM, WN, kS>;
   static_assert(C::kLds <= 160 * 1024, "LDS");
-  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN, kSwiGLU, kS, TK, kSwz>;
+  auto *fn = gemm_tiled_kernel<BM, BN, WM, WN, kSwiGLU, kS>;
   static bool attr_set = false;
   if (!attr_set) {
     const hipError_t e = hipFuncSetAttribute(
@@ -842,85 +829,49 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
 // 73 -> 68 us; at 320 tiles, [4096, 5120], it lost 54 -> 65 us), else 128 x
 // 128 (two workgroups per CU, four times the workgroups, so a partial last
 // round costs less), or 128 x 64 below two 128 x 128 tiles per CU.
-// Build-time tunables of the tile launches (measured defaults): the swizzled
-// LDS rows, and per tile shape the ring depth (stages) and the k step.
-// 128 x 64 tiles take a 4-stage ring when the grid is at most one workgroup
-// per CU (nothing else hides the latency), else two stages (two workgroups
-// per CU).  Deeper rings that cost a second workgroup per CU, and 32-wide k
-// steps, measured slower.
-#ifndef WY_GEMM_SWZ
-#define WY_GEMM_SWZ 1
-#endif
-#ifndef WY_GEMM_S256
-#define WY_GEMM_S256 2
-#endif
-#ifndef WY_GEMM_TK256
-#define WY_GEMM_TK256 64
-#endif
-#ifndef WY_GEMM_S128
-#define WY_GEMM_S128 2
-#endif
-#ifndef WY_GEMM_TK128
-#define WY_GEMM_TK128 64
-#endif
-#ifndef WY_GEMM_SMID
-#define WY_GEMM_SMID 2
-#endif
-#ifndef WY_GEMM_TKMID
-#define WY_GEMM_TKMID 64
-#endif
-#ifndef WY_GEMM_SMID1
-#define WY_GEMM_SMID1 4
-#endif
+// Tile shape and ring depth per grid (every variant swizzles its LDS rows and
+// steps K by 64; 32-wide K steps measured slower on every shape):
+//   256 x 256, 2 stages: from 384 tiles, or when 240..256 tiles make one
+//     round of the 256 CUs (the 3 stages a deeper ring needs do not fit);
+//   128 x 64, 4 stages: at most 256 such tiles, i.e. at most one workgroup
+//     per CU, where nothing else hides the latency (k_proj at 4096 tokens);
+//   128 x 128, 4 stages: fewer than two 128 x 128 tiles per CU but more than
+//     one round of 128 x 64 ones (o_proj and down_proj at 4096 tokens: one
+//     workgroup per CU with a deep ring beat two per CU with two stages);
+//   128 x 128, 2 stages: otherwise (two workgroups per CU; a deeper ring
+//     would cost the second one).
+constexpr int kBigMinTiles = 384, kBigRoundTiles = 240, kCUs = 256;
 int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf16_t *y,
                  int64_t ys0, int M, int N, int K, hipStream_t st) {
-  constexpr bool kSw = WY_GEMM_SWZ != 0;
   const int64_t big = int64_t((M + 255) / 256) * ((N + 255) / 256);
+  const bool use_big = big >= kBigMinTiles || (big >= kBigRoundTiles && big <= kCUs);
   // A narrow last column of 256-wide tiles (N % 256 <= 64, e.g. the GDN
   // in_proj's 8224 = 8192 + 32) costs a whole extra round of tiles for a
   // few columns: those columns run as a second, narrow launch (each output
   // element's K order is the same in every tile shape, so the result is
   // unchanged; 4096 x 8224: 90.5 -> 68.1 + 9.2 us).
   const int tail = N % 256;
-#ifndef WY_GEMM_BIG_MIN
-#define WY_GEMM_BIG_MIN 384
-#endif
-#ifndef WY_GEMM_BIG_ROUND
-#define WY_GEMM_BIG_ROUND 240
-#endif
-  // 256 x 256 tiles from WY_GEMM_BIG_MIN of them, or when they make one
-  // nearly full round of the 256 CUs
-  const bool use_big = big >= WY_GEMM_BIG_MIN || (big >= WY_GEMM_BIG_ROUND && big <= 256);
   if (use_big && tail != 0 && tail <= 64 && N > 256) {
     const int n_main = N - tail;
-    const int rc = launch_tiled_cfg<256, 256, 2, 4, false, WY_GEMM_S256, WY_GEMM_TK256, kSw>(
-        x, xs0, w, ws0, y, ys0, M, n_main, K, st);
+    const int rc = launch_tiled_cfg<256, 256, 2, 4, false, 2>(x, xs0, w, ws0, y, ys0,
+                                                                       M, n_main, K, st);
     if (rc != WY_OK) return rc;
     return launch_tiled(x, xs0, w + int64_t(n_main) * ws0, ws0, y + n_main, ys0, M, tail, K, st);
   }
   if (use_big)
-    return launch_tiled_cfg<256, 256, 2, 4, false, WY_GEMM_S256, WY_GEMM_TK256, kSw>(
-        x, xs0, w, ws0, y, ys0, M, N, K, st);
-  // fewer 128 x 128 tiles than two per CU (e.g. k_proj and o_proj at 4096
-  // tokens): 128 x 64 tiles put twice as many workgroups on the chip
+    return launch_tiled_cfg<256, 256, 2, 4, false, 2>(x, xs0, w, ws0, y, ys0, M, N, K,
+                                                               st);
   const int64_t mid = int64_t((M + 127) / 128) * ((N + 127) / 128);
-  if (mid < 512) {
-    const int64_t t64 = int64_t((M + 127) / 128) * ((N + 63) / 64);
-    if (t64 <= 256)
-      return launch_tiled_cfg<128, 64, 2, 2, false, WY_GEMM_SMID1, WY_GEMM_TKMID, kSw>(
-          x, xs0, w, ws0, y, ys0, M, N, K, st);
-#ifndef WY_GEMM_MIDBIG
-#define WY_GEMM_MIDBIG 1
-#endif
-    if constexpr (WY_GEMM_MIDBIG == 1)
-      return launch_tiled_cfg<128, 128, 2, 2, false, 4, 64, kSw>(x, xs0, w, ws0, y, ys0, M, N, K, st);
-    if constexpr (WY_GEMM_MIDBIG == 2)
-      return launch_tiled_cfg<128, 128, 2, 2, false, 3, 64, kSw>(x, xs0, w, ws0, y, ys0, M, N, K, st);
-    return launch_tiled_cfg<128, 64, 2, 2, false, WY_GEMM_SMID, WY_GEMM_TKMID, kSw>(
-        x, xs0, w, ws0, y, ys0, M, N, K, st);
+  if (mid < 2 * kCUs) {
+    const int64_t narrow = int64_t((M + 127) / 128) * ((N + 63) / 64);
+    if (narrow <= kCUs)
+      return launch_tiled_cfg<128, 64, 2, 2, false, 4>(x, xs0, w, ws0, y, ys0, M, N,
+                                                                K, st);
+    return launch_tiled_cfg<128, 128, 2, 2, false, 4>(x, xs0, w, ws0, y, ys0, M, N, K,
+                                                               st);
   }
-  return launch_tiled_cfg<128, 128, 2, 2, false, WY_GEMM_S128, WY_GEMM_TK128, kSw>(
-      x, xs0, w, ws0, y, ys0, M, N, K, st);
+  return launch_tiled_cfg<128, 128, 2, 2, false, 2>(x, xs0, w, ws0, y, ys0, M, N, K,
+                                                             st);
 }
 
 struct SkinnyArgs {
@@ -1150,7 +1101,7 @@ extern "C" int wy_gemm_2d_gate_up_swiglu(const void *x, int64_t x_stride0, const
     // 256 x 256 tiles of 128 gate + 128 up columns; 32-bit buffer offsets
     if (int64_t(256) * x_stride0 * 2 >= INT32_MAX || int64_t(2) * N * w_stride0 * 2 >= INT32_MAX)
       return WY_E_SHAPE;
-    return launch_tiled_cfg<256, 256, 2, 4, true, WY_GEMM_S256, WY_GEMM_TK256, WY_GEMM_SWZ != 0>(
+    return launch_tiled_cfg<256, 256, 2, 4, true, 2>(
         static_cast<const bf16_t *>(x), x_stride0, static_cast<const bf16_t *>(w), w_stride0,
         static_cast<bf16_t *>(y), y_stride0, M, N, K, static_cast<hipStream_t>(stream));
   }
