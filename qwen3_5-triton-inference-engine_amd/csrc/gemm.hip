@@ -835,9 +835,11 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
 //     round of the 256 CUs (the 3 stages a deeper ring needs do not fit);
 //   128 x 64, 4 stages: at most 256 such tiles, i.e. at most one workgroup
 //     per CU, where nothing else hides the latency (k_proj at 4096 tokens);
-//   128 x 128, 4 stages: fewer than two 128 x 128 tiles per CU but more than
-//     one round of 128 x 64 ones (o_proj and down_proj at 4096 tokens: one
-//     workgroup per CU with a deep ring beat two per CU with two stages);
+//   128 x 128 on 8 waves (64 x 32 each), 4 stages: fewer than two 128 x 128
+//     tiles per CU but more than one round of 128 x 64 ones (o_proj and
+//     down_proj at 4096 tokens: one workgroup per CU with a deep ring beat
+//     two per CU with two stages, and 8 waves beat 4 there: o_proj 22.4 ->
+//     20.1 us);
 //   128 x 128, 2 stages: otherwise (two workgroups per CU; a deeper ring
 //     would cost the second one).
 constexpr int kBigMinTiles = 384, kBigRoundTiles = 240, kCUs = 256;
@@ -867,7 +869,7 @@ int launch_tiled(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0, bf1
     if (narrow <= kCUs)
       return launch_tiled_cfg<128, 64, 2, 2, false, 4>(x, xs0, w, ws0, y, ys0, M, N,
                                                                 K, st);
-    return launch_tiled_cfg<128, 128, 2, 2, false, 4>(x, xs0, w, ws0, y, ys0, M, N, K,
+    return launch_tiled_cfg<128, 128, 2, 4, false, 4>(x, xs0, w, ws0, y, ys0, M, N, K,
                                                                st);
   }
   return launch_tiled_cfg<128, 128, 2, 2, false, 2>(x, xs0, w, ws0, y, ys0, M, N, K,
