@@ -616,14 +616,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   const uint32_t smem0 = lds_u32(smem);
   constexpr int kKS = kTK / 16;  // MFMA k sub-steps per stage (even)
   static_assert(kKS % 2 == 0, "sub-step buffers alternate");
-  if constexpr (C::kWaves == 4) {
+  if constexpr (C::kWaves == 4 || kS > 2) {
+    // split of a stage's DMA: the first part right after the barrier, the
+    // rest after the next step's first sub-step (8-wave tile)
+    constexpr int kHalf = C::kWaves == 8 ? (C::kPerWave + 1) / 2 : C::kPerWave;
     // The barrier that hands slot kt back to the DMA and makes stage kt + 1
     // visible sits before the last sub-step of step kt: the reads of step
     // kt + 1's first sub-step and the refill DMA then overlap that sub-step's
     // MFMAs instead of opening every step with an exposed LDS round trip
-    // (4-wave tiles 2-5% faster; the 8-wave tile keeps its DMA spread over
-    // two sub-steps after a barrier that opens the step, which measured 3%
-    // better there).
+    // (4-wave tiles 2-5% faster, the 8-wave 4-stage tile 5%, with its DMA
+    // split around the barrier; the 8-wave 2-stage 256 x 256 tile keeps a
+    // barrier that opens the step and its DMA spread over the first two
+    // sub-steps, 1-3% better there).
     wait_stage(0);
     barrier();
     load(smem0, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
@@ -642,7 +646,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
             barrier();
             load(smem0 + uint32_t(((kt + 1) % kS) * C::kStage),
                  std::integral_constant<int, cur ^ 1>{}, std::integral_constant<int, 0>{});
-            if (kt + kS < kt_n) issue(kt + kS);
+            if (kt + kS < kt_n) issue(kt + kS, 0, kHalf);
             // keep this sub-step's MFMAs after the barrier (they touch no
             // memory, so the compiler would otherwise hoist them above it)
             u32x4_t(&ac)[kFM] = av[cur];
@@ -654,6 +658,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
           }
         }
         mfmas(std::integral_constant<int, cur>{});
+        if constexpr (ks == 0 && kHalf < C::kPerWave)
+          if (kt >= 1 && kt - 1 + kS < kt_n) issue(kt - 1 + kS, kHalf, C::kPerWave);
         if constexpr (ks + 1 < kKS) lgkm_wait_all<kFM, kFN>(av[cur ^ 1], bv[cur ^ 1]);
       });
     }
