@@ -32,6 +32,15 @@
 // With min_pps = 1 this is exactly the reference partition
 // (gqa_attention_decode_paged.py:675-682, 779-784); a larger min_pps trades
 // split count for less fp32 scratch traffic.
+//
+// Workgroup order.  The direct order gives workgroup id b + B*(h + H*s).  The
+// balanced order (batches of 16..256 sequences) lists the active splits only,
+// full-size splits first and the shorter last splits after them, and hands
+// item k to workgroup k: the launch then runs one round of equal-sized work
+// items instead of leaving holes for inactive splits, and consecutive ids --
+// which the dispatcher deals round-robin over the XCDs -- carry equal page
+// counts.  The order only decides where a split runs, never its pages or its
+// arithmetic, so results are identical under both orders.
 #include <mutex>
 #include <type_traits>
 
@@ -73,6 +82,7 @@ struct DecodeArgs {
   const float *inv_freq;
   float eps;
   int rope_dim;
+  int balanced;  // workgroup order: 0 direct, 1 balanced (see the file comment)
 };
 
 __device__ __forceinline__ int split_pps(int npg, int min_pps) {
@@ -116,14 +126,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const bf16_t *base) 
 
 // ctx = bf16(A / L), then optionally bf16(ctx * sigmoid(gate)): the same two
 // roundings as the reference's combine kernel followed by its gate pack.
+// The gate's bf16 values at dims d..d+3 of query head hq, as two packed pairs.
+__device__ __forceinline__ u32x2_t load_gate4(const DecodeArgs &a, int b, int hq, int d) {
+  const bf16_t *g = a.gate + b * a.g_b + hq * a.g_h;
+  if (a.g_d == 1 && ((a.g_b | a.g_h) & 3) == 0 && (reinterpret_cast<uintptr_t>(a.gate) & 7) == 0)
+    return *reinterpret_cast<const u32x2_t *>(g + d);
+  return u32x2_t{uint32_t(g[d * a.g_d]) | (uint32_t(g[(d + 1) * a.g_d]) << 16),
+                 uint32_t(g[(d + 2) * a.g_d]) | (uint32_t(g[(d + 3) * a.g_d]) << 16)};
+}
+
+// gpre: the gate values, already loaded (else they are loaded here).
 __device__ __forceinline__ void store_out4(const DecodeArgs &a, int b, int hq, int d,
-                                           float4 A, float L) {
+                                           float4 A, float L, const u32x2_t *gpre = nullptr) {
   float o[4] = {round_bf16(A.x / L), round_bf16(A.y / L), round_bf16(A.z / L),
                 round_bf16(A.w / L)};
   if (a.gate) {
-    const bf16_t *g = a.gate + b * a.g_b + hq * a.g_h;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = o[e] * gate_sigmoid(bf16_to_f32(g[(d + e) * a.g_d]));
+    const u32x2_t gw = gpre ? *gpre : load_gate4(a, b, hq, d);
+    o[0] *= gate_sigmoid(bf16_lo(gw[0]));
+    o[1] *= gate_sigmoid(bf16_hi(gw[0]));
+    o[2] *= gate_sigmoid(bf16_lo(gw[1]));
+    o[3] *= gate_sigmoid(bf16_hi(gw[1]));
   }
   bf16_t *orow = a.out + b * a.o_b + hq * a.o_h;
   if (a.o_d == 1) {
@@ -175,7 +197,8 @@ __device__ __forceinline__ float4 ld_f4(const float *p) {
 // and the accumulator rows are fetched 8 at a time, so the merge costs a few
 // memory round trips rather than one per split.
 template <bool kCoherent>
-__device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lane) {
+__device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lane,
+                           const u32x2_t *gpre = nullptr) {
   const float *mrow = a.mp + b * a.ml_b + hq * a.ml_h;
   const float *lrow = a.lp + b * a.ml_b + hq * a.ml_h;
   const float *arow = a.ap + b * a.a_b + hq * a.a_h + lane * 4;
@@ -213,7 +236,61 @@ __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lan
       }
     }
   }
-  store_out4(a, b, hq, lane * 4, A, L);
+  store_out4(a, b, hq, lane * 4, A, L, gpre);
+}
+
+
+// Balanced workgroup order: work item k (k = blockIdx.x) of the launch.  The
+// full-size splits of every (sequence, KV head) come first, sequence-major
+// with the KV head and then the split index fastest, then the partial last
+// splits in sequence order.  pos is read once per 64 sequences into
+// registers.  Returns false for ids past the last item.
+constexpr int kBalancedMinBatch = 16;
+constexpr int kBalancedChunks = 4;  // batch <= 256
+__device__ bool balanced_item(const DecodeArgs &a, int k, int lane, int &b, int &h, int &s,
+                              int &seq_len) {
+  const int H = a.hkv;
+  const int nch = (a.batch + 63) >> 6;
+  int plo[kBalancedChunks], npg[kBalancedChunks], pps[kBalancedChunks];
+#pragma unroll
+  for (int c = 0; c < kBalancedChunks; ++c) {
+    const int bb = c * 64 + lane;
+    plo[c] = c < nch && bb < a.batch ? int(a.pos[bb]) : -1;
+  }
+#pragma unroll
+  for (int c = 0; c < kBalancedChunks; ++c) {
+    npg[c] = (plo[c] + kPage) / kPage;
+    pps[c] = split_pps(npg[c], a.min_pps);
+  }
+  int carry = 0;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int c = 0; c < kBalancedChunks; ++c) {
+      if (c >= nch) break;
+      const int full = npg[c] / pps[c];
+      const int x = (pass == 0 ? full : int(full * pps[c] < npg[c])) * H;
+      int incl = x;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      incl += carry;
+      const uint64_t m = __ballot(k < incl);
+      if (m) {
+        const int L = __builtin_ctzll(m);
+        const int r = k - __shfl(incl - x, L);
+        b = __builtin_amdgcn_readfirstlane(c * 64 + L);
+        h = __builtin_amdgcn_readfirstlane(r % H);
+        s = __builtin_amdgcn_readfirstlane(pass == 0 ? r / H : __shfl(full, L));
+        seq_len = __builtin_amdgcn_readfirstlane(__shfl(plo[c], L) + 1);
+        return true;
+      }
+      carry = __shfl(incl, 63);
+    }
+  }
+  return false;
 }
 
 // Split partial pass.  kFused additionally (i) takes the new token's K/V
@@ -246,36 +323,48 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   auto &sm_acc = sm.acc;
   auto &sm_q = sm.q;
 
-  // 1-D grid of batch * H_kv * max_splits workgroups, sequence index fastest.
-  // Splits past a sequence's end exit at once.
+  // 1-D grid of batch * H_kv * max_splits workgroups (see the file comment
+  // for the two orders).  Splits past a sequence's end exit at once.
   const int lane = threadIdx.x & 63;
-  const int b = blockIdx.x % a.batch;
-  const int h = (blockIdx.x / a.batch) % a.hkv;
-  const int s = blockIdx.x / (a.batch * a.hkv);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   typedef const __attribute__((address_space(4))) int32_t *bt_const_t;
+  int b, h, s, seq_len = 0;
+  if (a.balanced) {
+    if (!balanced_item(a, blockIdx.x, lane, b, h, s, seq_len)) return;
+  } else {
+    b = blockIdx.x % a.batch;
+    h = (blockIdx.x / a.batch) % a.hkv;
+    s = blockIdx.x / (a.batch * a.hkv);
+  }
   const int32_t *btrow = a.bt + b * a.bt_b;
   const bt_const_t bt_s = (bt_const_t)btrow;
-  // The block-table entry of this wave's first page is requested together
-  // with pos, for the usual partition (pps == min_pps), instead of after it:
-  // the first page's address then costs one memory round trip, not two.
-  // The q rows are requested at the same time.  (pos < 2^31: its low word.)
-  const int first_guess = s * a.min_pps + wave;
-  const int32_t *bt_first = btrow + (first_guess < a.bt_cols ? first_guess : a.bt_cols - 1);
   const int r_q = threadIdx.x >> 5, c_q = (threadIdx.x & 31) * 8;
   const bf16_t *q_src = a.q + b * a.qs_b + (h * kG + r_q) * a.qs_h + c_q;
   const bool q_fast = threadIdx.x < kG * kD / 8 && (kProlog || a.qs_d == 1);
   u32x4_t q_pre = {0u, 0u, 0u, 0u};
   if (q_fast) q_pre = ld16(q_src);
-  int32_t bt_guess, pos_lo;
-  asm volatile(
-      "s_load_dword %0, %2, 0x0\n\t"
-      "s_load_dword %1, %3, 0x0\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=s"(pos_lo), "=s"(bt_guess)
-      : "s"(a.pos + b), "s"(bt_first)
-      : "memory");
-  const int seq_len = pos_lo + 1;
+  // The block-table entry of this wave's first page is requested together
+  // with the q rows (and, in the direct order, with pos: for the usual
+  // partition, pps == min_pps, its index is known before pos), so the first
+  // page's address costs one memory round trip.  (pos < 2^31: its low word.)
+  int32_t bt_guess;
+  if (a.balanced) {
+    const int npg_b = (seq_len + kPage - 1) / kPage;
+    const int first = s * split_pps(npg_b, a.min_pps) + wave;
+    bt_guess = bt_s[first < npg_b ? first : npg_b - 1];
+  } else {
+    const int first_guess = s * a.min_pps + wave;
+    const int32_t *bt_first = btrow + (first_guess < a.bt_cols ? first_guess : a.bt_cols - 1);
+    int32_t pos_lo;
+    asm volatile(
+        "s_load_dword %0, %2, 0x0\n\t"
+        "s_load_dword %1, %3, 0x0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=s"(pos_lo), "=s"(bt_guess)
+        : "s"(a.pos + b), "s"(bt_first)
+        : "memory");
+    seq_len = pos_lo + 1;
+  }
   const int npg = (seq_len + kPage - 1) / kPage;
   const int pps = split_pps(npg, a.min_pps);
   const int nact = (npg + pps - 1) / pps;
@@ -284,6 +373,10 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   const int p1 = min(p0 + pps, npg);
 
   const int n16 = lane & 15, g4 = lane >> 4;
+  // The step's gate values for this wave's query head are requested up
+  // front: the output epilogue then does not wait a memory round trip for them.
+  u32x2_t gate_pre = {0u, 0u};
+  if (kFused && a.gate && wave < kG) gate_pre = load_gate4(a, b, h * kG + wave, lane * 4);
 
   float m_run[kG], l_run[kG], acc[kG][4];
 #pragma unroll
@@ -309,11 +402,11 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   // launch), one page ahead, so a page's address never waits on the vector
   // memory counter that its K/V loads share.
   const int npw = p0 + wave < p1 ? (p1 - p0 - wave + kW - 1) / kW : 0;
-  int32_t bt_ahead = npw > 0 ? (pps == a.min_pps ? bt_guess : bt_s[p0 + wave]) : 0;
+  int32_t bt_ahead = npw > 0 ? (a.balanced || pps == a.min_pps ? bt_guess : bt_s[p0 + wave]) : 0;
   // Register pipeline, no extra registers: K of page i+1 is requested as soon
-  // as the score MFMAs have consumed K of page i, and V of page i+1 as soon as
-  // P.V has consumed V of page i, so each load overlaps the other half of the
-  // page's work.
+  // as the score MFMAs have consumed K of page i, and each pair of V rows of
+  // page i+1 as soon as P.V has consumed that pair of page i, so each load
+  // overlaps the rest of the page's work.
   u32x4_t kr[8];
   u32x2_t vr[kPage];
   int64_t phys_next = 0;
@@ -334,6 +427,11 @@ void paged_decode_split_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < kPage; ++e)
       vr[e] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, v_row_bytes * e, 0);
+  };
+  auto issue_v_pair = [&](int j) {  // rows 2j, 2j+1 of the next page
+    const __amdgpu_buffer_rsrc_t rv = page_rsrc(vh + phys_next * a.vc_p);
+    vr[2 * j] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, v_row_bytes * (2 * j), 0);
+    vr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, v_row_bytes * (2 * j + 1), 0);
   };
 
   // Fused step: the new token's K and V rows come from k_new / v_new (the
@@ -577,9 +675,9 @@ void paged_decode_split_kernel(const DecodeArgs a) {
                                                       __builtin_bit_cast(bf16x2_t, vd[e]),
                                                       acc[r][e], false);
       }
+      if constexpr (kMore) issue_v_pair(j);
     }
     __builtin_amdgcn_wave_barrier();
-    if constexpr (kMore) issue_v(i + 1);
   };
   if (npw > 0) {
     for (int i = 0; i + 1 < npw; ++i) page(i, std::true_type{});
@@ -622,7 +720,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   const int hq = h * kG + r;
   if constexpr (kFused) {
     if (nact == 1) {  // the only split: finish here, no scratch round trip
-      if (head_wave) store_out4(a, b, hq, lane * 4, A, L);
+      if (head_wave) store_out4(a, b, hq, lane * 4, A, L, &gate_pre);
       return;
     }
   }
@@ -663,7 +761,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     }
     __syncthreads();
     if (!sm.last || !head_wave) return;
-    merge_head<true>(a, b, hq, nact, lane);
+    merge_head<true>(a, b, hq, nact, lane, &gate_pre);
   }
 }
 
@@ -696,6 +794,8 @@ bool out_layout_ok(const void *out, const int64_t *os) {
                         (reinterpret_cast<uintptr_t>(out) & 7u) == 0);
 }
 
+constexpr int kLongSplitPages = 128;
+
 int split_grid_z(int max_pages, int min_pps) {
   const int z = (max_pages + min_pps - 1) / min_pps;
   return z > kMaxSplits ? kMaxSplits : z;
@@ -721,6 +821,11 @@ int launch_split(const DecodeArgs &args, int batch, int num_kv_heads, int max_pa
   DecodeArgs a = args;
   a.batch = batch;
   a.bt_cols = max_pages;
+  // The balanced order for mid-size batches of short/medium contexts; long
+  // contexts (many full splits per sequence) and small batches keep the
+  // direct order, which needs no pass over pos before the first loads.
+  a.balanced = batch >= kBalancedMinBatch && batch <= 64 * kBalancedChunks &&
+               min_pps < kLongSplitPages;
   const dim3 grid(unsigned(batch) * unsigned(num_kv_heads) *
                   unsigned(split_grid_z(max_pages, min_pps)));
   return launch_split_w<kFused, kWaves, kProlog>(grid, a, static_cast<hipStream_t>(stream));

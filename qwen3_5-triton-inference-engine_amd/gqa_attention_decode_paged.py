@@ -36,10 +36,13 @@ MAX_SPLITS = 128
 # Lower bound on pages per split shared by split and combine (see module doc).
 # Small batches keep 4 pages (64 tokens) per split so a lone sequence still
 # spreads over many workgroups; large batches already fill the GPU and gain
-# more from fewer partials to merge (32 pages = 512 tokens).  Both ops derive
-# it from the batch size alone, a static shape, so the pair stays graph-safe.
+# more from fewer partials to merge (24 pages = 384 tokens: at B=32 with
+# contexts up to 2048 tokens this keeps the active splits within one round of
+# the 256 CUs, one per CU in the kernels' balanced workgroup order).  Both ops
+# derive it from the batch size alone, a static shape, so the pair stays
+# graph-safe.
 MIN_PAGES_PER_SPLIT = 4
-MIN_PAGES_PER_SPLIT_LARGE_BATCH = 32
+MIN_PAGES_PER_SPLIT_LARGE_BATCH = 24
 LARGE_BATCH = 16
 
 
