@@ -82,7 +82,8 @@ struct DecodeArgs {
   const float *inv_freq;
   float eps;
   int rope_dim;
-  int balanced;  // workgroup order: 0 direct, 1 balanced (see the file comment)
+  int balanced;   // workgroup order: 0 direct, 1 balanced (see the file comment)
+  int two_level;  // merge more than kMergeGroup splits through groups (batch < 16)
 };
 
 __device__ __forceinline__ int split_pps(int npg, int min_pps) {
@@ -191,43 +192,42 @@ __device__ __forceinline__ float4 ld_f4(const float *p) {
   }
 }
 
-// Merge the nact split states of (b, hq) with one wavefront; lane owns dims
-// 4*lane..4*lane+3.  Shared by the combine kernel and the fused step.  The
-// split weights are formed lane-parallel (lane s holds split s, nact <= 128)
-// and the accumulator rows are fetched 8 at a time, so the merge costs a few
-// memory round trips rather than one per split.
-template <bool kCoherent>
-__device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lane,
-                           const u32x2_t *gpre = nullptr) {
-  const float *mrow = a.mp + b * a.ml_b + hq * a.ml_h;
-  const float *lrow = a.lp + b * a.ml_b + hq * a.ml_h;
-  const float *arow = a.ap + b * a.a_b + hq * a.a_h + lane * 4;
-  // The first 8 accumulator rows are requested together with m and l, so a
-  // merge of up to 8 splits costs one memory round trip.
+// Merging split states.  A state is (m, l, acc): the running max, the sum of
+// exp(score - m) and the unnormalised accumulator.  One wavefront merges n
+// states of one query head; lane owns dims 4*lane..4*lane+3.  The caller
+// hands over lane-parallel m/l (lane i: state i, lane i+64: state i+64) and
+// a function returning state i's accumulator row.  The weights are formed
+// lane-parallel and the accumulator rows fetched 8 at a time, so a merge
+// costs a few memory round trips rather than one per state.  The same code
+// runs in the combine kernel and in the one-launch step, so both produce the
+// same bits.
+struct Merged {
+  float M, L;
+  float4 A;
+};
+
+template <class AccFn>
+__device__ __forceinline__ Merged merge_core(int n, float m0, float m1, float l0, float l1,
+                                             AccFn acc_row) {
   float4 x[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u)
-    if (u < nact) x[u] = ld_f4<kCoherent>(arow + u * a.a_s);
-  const bool has0 = lane < nact, has1 = lane + 64 < nact;
-  const float m0 = has0 ? ld_f<kCoherent>(mrow + lane * a.ml_s) : -INFINITY;
-  const float m1 = has1 ? ld_f<kCoherent>(mrow + (lane + 64) * a.ml_s) : -INFINITY;
-  const float l0 = has0 ? ld_f<kCoherent>(lrow + lane * a.ml_s) : 0.f;
-  const float l1 = has1 ? ld_f<kCoherent>(lrow + (lane + 64) * a.ml_s) : 0.f;
+    if (u < n) x[u] = acc_row(u);
   const float mx = wave_max(fmaxf(m0, m1));
-  const float w0 = has0 ? __expf(m0 - mx) : 0.f;
-  const float w1 = has1 ? __expf(m1 - mx) : 0.f;
+  const float w0 = m0 == -INFINITY ? 0.f : __expf(m0 - mx);
+  const float w1 = m1 == -INFINITY ? 0.f : __expf(m1 - mx);
   const float L = wave_sum(w0 * l0 + w1 * l1);
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < nact; s0 += 8) {
+  for (int s0 = 0; s0 < n; s0 += 8) {
     if (s0 > 0) {
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (s0 + u < nact) x[u] = ld_f4<kCoherent>(arow + (s0 + u) * a.a_s);
+        if (s0 + u < n) x[u] = acc_row(s0 + u);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int sp = s0 + u;
-      if (sp < nact) {
+      if (sp < n) {
         const float w = __shfl(sp < 64 ? w0 : w1, sp & 63);
         A.x += w * x[u].x;
         A.y += w * x[u].y;
@@ -236,9 +236,66 @@ __device__ void merge_head(const DecodeArgs &a, int b, int hq, int nact, int lan
       }
     }
   }
-  store_out4(a, b, hq, lane * 4, A, L, gpre);
+  return Merged{mx, L, A};
 }
 
+// Merge n states of (b, hq) stored in the scratch at slots first + i*stride.
+// kCoherent: they were published by other workgroups of this launch.
+template <bool kCoherent>
+__device__ Merged merge_slots(const DecodeArgs &a, int b, int hq, int first, int stride, int n,
+                              int lane) {
+  const float *mrow = a.mp + b * a.ml_b + hq * a.ml_h;
+  const float *lrow = a.lp + b * a.ml_b + hq * a.ml_h;
+  const float *arow = a.ap + b * a.a_b + hq * a.a_h + lane * 4;
+  const bool has0 = lane < n, has1 = lane + 64 < n;
+  const int s0 = first + lane * stride, s1 = first + (lane + 64) * stride;
+  const float m0 = has0 ? ld_f<kCoherent>(mrow + s0 * a.ml_s) : -INFINITY;
+  const float m1 = has1 ? ld_f<kCoherent>(mrow + s1 * a.ml_s) : -INFINITY;
+  const float l0 = has0 ? ld_f<kCoherent>(lrow + s0 * a.ml_s) : 0.f;
+  const float l1 = has1 ? ld_f<kCoherent>(lrow + s1 * a.ml_s) : 0.f;
+  return merge_core(n, m0, m1, l0, l1, [&](int i) {
+    return ld_f4<kCoherent>(arow + (first + i * stride) * a.a_s);
+  });
+}
+
+// Splits per merge group.  Up to kMergeGroup splits merge in one level (the
+// last split of the sequence and KV head to finish merges them all); with
+// two_level set (batches below 16, where one long sequence is cut into up to
+// 128 splits of 4+ pages) more merge in two: the last split of each group of
+// kMergeGroup merges its group into the group's first slot, and the last
+// group to finish merges the group states.  One merging wavefront then reads
+// at most 16 accumulator rows (16 KiB) instead of up to 128.
+constexpr int kMergeGroup = 16;
+
+// Merge all nact split states of (b, hq) as the one-launch step does.
+template <bool kCoherent>
+__device__ Merged merge_all(const DecodeArgs &a, int b, int hq, int nact, int lane) {
+  if (!a.two_level || nact <= kMergeGroup)
+    return merge_slots<kCoherent>(a, b, hq, 0, 1, nact, lane);
+  const int ng = (nact + kMergeGroup - 1) / kMergeGroup;  // <= 8
+  float mg = -INFINITY, lg = 0.f;
+  float4 ag[kMaxSplits / kMergeGroup];
+#pragma unroll
+  for (int g = 0; g < kMaxSplits / kMergeGroup; ++g) {
+    ag[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g < ng) {
+      const Merged r = merge_slots<kCoherent>(a, b, hq, g * kMergeGroup, 1,
+                                              min(kMergeGroup, nact - g * kMergeGroup), lane);
+      if (lane == g) {
+        mg = r.M;
+        lg = r.L;
+      }
+      ag[g] = r.A;
+    }
+  }
+  return merge_core(ng, mg, -INFINITY, lg, 0.f, [&](int i) {
+    float4 v = ag[0];
+#pragma unroll
+    for (int g = 1; g < kMaxSplits / kMergeGroup; ++g)
+      if (i == g) v = ag[g];
+    return v;
+  });
+}
 
 // Balanced workgroup order: work item k (k = blockIdx.x) of the launch.  The
 // full-size splits of every (sequence, KV head) come first, sequence-major
@@ -737,31 +794,58 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     }
   } else {
     // Publish this split with device-coherent stores, wait until they have
-    // completed, then count it.  The workgroup that brings the count to nact
+    // completed, then count it.  The workgroup that completes the count
     // merges, reading the partials coherently.  (A workgroup-scope release
     // fence alone does not wait for the stores to complete on gfx950, hence
-    // the explicit vmcnt wait before the barrier.)
-    if (head_wave) {
-      st_coherent4(adst, A);
-      if (lane == 0) {
-        st_coherent(mdst, M);
-        st_coherent(ldst, L);
+    // the explicit vmcnt wait before the barrier.)  With more than
+    // kMergeGroup splits the count is per group of kMergeGroup splits, whose
+    // last workgroup publishes the group's merged state in the group's first
+    // slot and counts it on the (b, h) counter.
+    auto publish = [&](float *ad, float *md, float *ldp, float4 Av, float Mv, float Lv) {
+      if (head_wave) {
+        st_coherent4(ad, Av);
+        if (lane == 0) {
+          st_coherent(md, Mv);
+          st_coherent(ldp, Lv);
+        }
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __syncthreads();
+    };
+    auto count = [&](int *cnt, int need) {
+      if (threadIdx.x == 0) {
+        const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        const int last = done == need - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.last = last;
+      }
+      __syncthreads();
+      return sm.last != 0;
+    };
+    publish(adst, mdst, ldst, A, M, L);
+    int *top = a.counters + b * a.hkv + h;
+    const int ng = a.two_level ? (nact + kMergeGroup - 1) / kMergeGroup : 1;
+    if (ng == 1) {
+      if (!count(top, nact) || !head_wave) return;
+      const Merged mr = merge_slots<true>(a, b, hq, 0, 1, nact, lane);
+      store_out4(a, b, hq, lane * 4, mr.A, mr.L, &gate_pre);
+      return;
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int *cnt = a.counters + b * a.hkv + h;
-      const int done = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-      const int last = done == nact - 1;
-      if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sm.last = last;
-    }
-    __syncthreads();
-    if (!sm.last || !head_wave) return;
-    merge_head<true>(a, b, hq, nact, lane, &gate_pre);
+    const int g = s / kMergeGroup;
+    const int g0 = g * kMergeGroup;
+    int *gcnt = a.counters + a.batch * a.hkv + (b * a.hkv + h) * (kMaxSplits / kMergeGroup) + g;
+    if (!count(gcnt, min(kMergeGroup, nact - g0))) return;
+    Merged gm = {0.f, 0.f, make_float4(0.f, 0.f, 0.f, 0.f)};
+    if (head_wave) gm = merge_slots<true>(a, b, hq, g0, 1, min(kMergeGroup, nact - g0), lane);
+    float *gslot_a = a.ap + b * a.a_b + hq * a.a_h + g0 * a.a_s + lane * 4;
+    float *gslot_m = a.mp + b * a.ml_b + hq * a.ml_h + g0 * a.ml_s;
+    float *gslot_l = a.lp + b * a.ml_b + hq * a.ml_h + g0 * a.ml_s;
+    publish(gslot_a, gslot_m, gslot_l, gm.A, gm.M, gm.L);
+    if (!count(top, ng) || !head_wave) return;
+    const Merged mr = merge_slots<true>(a, b, hq, 0, kMergeGroup, ng, lane);
+    store_out4(a, b, hq, lane * 4, mr.A, mr.L, &gate_pre);
   }
 }
 
@@ -771,7 +855,8 @@ __global__ __launch_bounds__(64) void paged_decode_combine_kernel(const DecodeAr
   const int seq_len = int(a.pos[b]) + 1;
   const int npg = (seq_len + kPage - 1) / kPage;
   const int pps = split_pps(npg, a.min_pps);
-  merge_head<false>(a, b, hq, (npg + pps - 1) / pps, threadIdx.x);
+  const Merged mr = merge_all<false>(a, b, hq, (npg + pps - 1) / pps, threadIdx.x);
+  store_out4(a, b, hq, threadIdx.x * 4, mr.A, mr.L);
 }
 
 bool cache_layout_ok(const void *kc, const void *vc, const int64_t *kcs, const int64_t *vcs) {
@@ -826,6 +911,7 @@ int launch_split(const DecodeArgs &args, int batch, int num_kv_heads, int max_pa
   // direct order, which needs no pass over pos before the first loads.
   a.balanced = batch >= kBalancedMinBatch && batch <= 64 * kBalancedChunks &&
                min_pps < kLongSplitPages;
+  a.two_level = batch < kBalancedMinBatch;
   const dim3 grid(unsigned(batch) * unsigned(num_kv_heads) *
                   unsigned(split_grid_z(max_pages, min_pps)));
   return launch_split_w<kFused, kWaves, kProlog>(grid, a, static_cast<hipStream_t>(stream));
@@ -919,6 +1005,7 @@ extern "C" int wy_paged_decode_combine(const float *m_partial, const float *l_pa
   a.a_s = as[2];
   a.pos = pos;
   a.min_pps = min_pages_per_split;
+  a.two_level = batch < kBalancedMinBatch;
   a.out = static_cast<bf16_t *>(out);
   a.o_b = os[0];
   a.o_h = os[1];
@@ -1044,7 +1131,7 @@ namespace {
 constexpr int kNoAllocMaxRows = 512;
 constexpr size_t kNoAllocMlFloats = size_t(kNoAllocMaxRows) * kMaxSplits;
 constexpr size_t kNoAllocAccFloats = kNoAllocMlFloats * kD;
-constexpr size_t kNoAllocCounters = kNoAllocMaxRows;  // >= batch * num_kv_heads
+constexpr size_t kNoAllocCounters = kNoAllocMaxRows / 4 * 9;  // >= batch * num_kv_heads * 9
 constexpr size_t kNoAllocBytes = (2 * kNoAllocMlFloats + kNoAllocAccFloats) * 4 +
                                  kNoAllocCounters * 4;
 constexpr int kNoAllocMaxDevices = 64;

@@ -86,10 +86,12 @@ def allocate_paged_kv_cache(
 
 
 class SplitScratch(tuple):
-    """``(m, l, acc)`` as in the reference, plus ``counters``: one int32 per
-    (sequence, query head) slot used by the one-launch decode step to elect
-    the workgroup that merges the splits.  Counters start at zero and every
-    step leaves them at zero.  Unpacks like the reference's 3-tuple."""
+    """``(m, l, acc)`` as in the reference, plus ``counters``: the int32
+    counters the one-launch decode step uses to elect the workgroups that
+    merge the splits (``B * H_kv`` per-(sequence, KV head) counters and
+    ``B * H_kv * 8`` merge-group counters; allocated as ``B * H_q * 4``).
+    Counters start at zero and every step leaves them at zero.  Unpacks like
+    the reference's 3-tuple."""
 
     def __new__(cls, m, l, acc, counters):
         obj = super().__new__(cls, (m, l, acc))
@@ -106,13 +108,13 @@ def allocate_split_scratch(
 ):
     """Split-K workspace shared by all attention layers: m, l ``[B, H_q, 128]``
     and acc ``[B, H_q, 128, D]`` fp32 (reference :591-609), plus the merge
-    counters of the fused step (``.counters``, ``[B * H_q]`` int32 zeros)."""
+    counters of the fused step (``.counters``, ``[B * H_q * 4]`` int32 zeros)."""
     m = torch.zeros((batch, num_q_heads, MAX_SPLITS), dtype=torch.float32, device=device)
     l = torch.zeros((batch, num_q_heads, MAX_SPLITS), dtype=torch.float32, device=device)
     acc = torch.zeros(
         (batch, num_q_heads, MAX_SPLITS, head_dim), dtype=torch.float32, device=device
     )
-    counters = torch.zeros((batch * num_q_heads,), dtype=torch.int32, device=device)
+    counters = torch.zeros((batch * num_q_heads * 4,), dtype=torch.int32, device=device)
     return SplitScratch(m, l, acc, counters)
 
 
@@ -365,7 +367,7 @@ def paged_gqa_attention_decode_fused(
     assert l_partial.shape == m_partial.shape and l_partial.stride() == m_partial.stride()
     assert acc_partial.shape == (batch, num_q_heads, MAX_SPLITS, head_dim)
     assert counters.dtype == torch.int32 and counters.is_contiguous()
-    assert counters.numel() >= batch * num_kv_heads
+    assert counters.numel() >= batch * num_kv_heads * 9
     assert num_q_heads % num_kv_heads == 0
     if gate is not None:
         assert gate.shape == q.shape and gate.dtype == torch.bfloat16
@@ -441,7 +443,7 @@ def paged_gqa_attention_decode_block(
     assert l_partial.shape == m_partial.shape and l_partial.stride() == m_partial.stride()
     assert acc_partial.shape == (batch, num_q_heads, MAX_SPLITS, head_dim)
     assert counters.dtype == torch.int32 and counters.is_contiguous()
-    assert counters.numel() >= batch * num_kv_heads
+    assert counters.numel() >= batch * num_kv_heads * 9
     out = torch.empty((batch, num_q_heads, head_dim), dtype=torch.bfloat16, device=q_raw.device)
     _lib.call(
         "wy_paged_decode_block",
