@@ -155,7 +155,9 @@ int wy_paged_decode_step(const void *q, const int64_t *q_strides, const void *k_
  * otherwise.  batch * num_q_heads must not exceed
  * wy_paged_decode_step_noalloc_max_rows() (512), else WY_E_CAPACITY and
  * nothing is launched.  The first call on a device resolves the array's
- * address and clears its counters on `stream`.  All calls on one GPU share
+ * address and clears its counters on `stream`; that first call must run
+ * eagerly (returns WY_E_UNSUPPORTED, nothing launched, if `stream` is being
+ * captured), later calls may be captured into a graph.  All calls on one GPU share
  * the array: calls that may overlap on one GPU (concurrent streams, host
  * threads) race.  No counterpart in the reference; for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
@@ -230,6 +232,16 @@ int wy_varlen_causal_prefill(const void *q, const int64_t *q_strides,
  * (its launch takes no workspace).
  */
 int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_kv_heads, int max_seqlen);
+
+/*
+ * Test hook, no counterpart in the reference: the order in which later
+ * wy_varlen_causal_prefill / wy_prefill_attention_block launches (both the
+ * one-workgroup-per-block and the queue launch) hand out their query blocks.
+ * 0 (default) heaviest first, 1 lightest first, 2 alternately from both ends;
+ * other values select 0.  Results do not depend on it (tests check this bit
+ * for bit).  Process-wide; not for concurrent use with running launches.
+ */
+void wy_prefill_set_ticket_order(int order);
 
 /*
  * Prefill attention block: the reference's prefill attention sequence after
@@ -405,7 +417,8 @@ int wy_gdn_recurrent_decode(const void *q, const int64_t *q_strides, const void 
  * solutions of (I + L) X = B with L[t, i] = beta_t exp(G_t - G_i) <k_t, k_i>
  * (i < t): u_base = X for B = beta v ([N, H, 64, value_dim]), w = X for
  * B = beta exp(G) k ([N, H, 64, key_dim]); all fp32, contiguous, N =
- * ceil(T/64), rows past T zero.  k, v [T, H, 128] bf16 (unit inner stride,
+ * ceil(T/64).  Rows past T: w and u_base are zero; g_cumsum repeats the last
+ * valid cumulative value (the reference's unmasked store writes the same).  k, v [T, H, 128] bf16 (unit inner stride,
  * 16-byte aligned rows), beta, g [T, H] fp32.  key_dim = value_dim = 128.
  * Replaces wy_lib::gdn_chunk_prepare_wy
  *   (triton_kernels/gdn_recurrent_prefill.py:703-826, kernel :249-402).

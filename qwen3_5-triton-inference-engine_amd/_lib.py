@@ -94,7 +94,10 @@ _SIZE_QUERIES = ("wy_varlen_causal_prefill_workspace_bytes", "wy_gemm_2d_workspa
                  "wy_lm_head_argmax_workspace_bytes", "wy_paged_decode_step_noalloc_max_rows",
                  "wy_page_stream_read_waves")
 
-EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES, *_SIZE_QUERIES)
+# test hooks returning nothing
+_HOOKS = ("wy_prefill_set_ticket_order",)
+
+EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES, *_SIZE_QUERIES, *_HOOKS)
 
 _lib: ctypes.CDLL | None = None
 
@@ -126,6 +129,8 @@ def load() -> ctypes.CDLL:
     for fn in (lib.wy_paged_decode_step_noalloc_max_rows, lib.wy_page_stream_read_waves):
         fn.argtypes = []
         fn.restype = ctypes.c_int64
+    lib.wy_prefill_set_ticket_order.argtypes = [_i]
+    lib.wy_prefill_set_ticket_order.restype = None
     _lib = lib
     return lib
 

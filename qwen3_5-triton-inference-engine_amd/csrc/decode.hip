@@ -1150,7 +1150,9 @@ unsigned char *g_noalloc_ptr[kNoAllocMaxDevices];
 
 // Device address of this device's `scratch`, resolved on the first call; that
 // call also clears the counters on `st` (a fill kernel, ordered before the
-// step it precedes on the same stream).
+// step it precedes on the same stream).  The first call must not be under
+// graph capture: the symbol lookup would run during the capture and the
+// clearing kernel would only be recorded, not run, so it is refused.
 int noalloc_scratch(hipStream_t st, unsigned char **out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -1158,6 +1160,10 @@ int noalloc_scratch(hipStream_t st, unsigned char **out) {
   if (dev < 0 || dev >= kNoAllocMaxDevices) return WY_E_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   if (!g_noalloc_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) return int(e);
+    if (cs != hipStreamCaptureStatusNone) return WY_E_UNSUPPORTED;
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return int(e);

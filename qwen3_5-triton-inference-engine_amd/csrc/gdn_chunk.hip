@@ -557,13 +557,12 @@ extern "C" int wy_gdn_chunk_state(const void *k, const int64_t *ks, const float 
   if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
   if (!rows_ok(k, ks) || !wyh::aligned16(w)) return WY_E_LAYOUT;
   const int N = (token_num + kC - 1) / kC;
-  static bool lds_set = false;   // the attribute is per function, set once
-  if (!lds_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gdn_chunk_state_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kStateLds);
-    if (e != hipSuccess) return int(e);
-    lds_set = true;
-  }
+  // the attribute is per function: set once (a function-local static is
+  // initialised exactly once, also under concurrent first calls)
+  static const hipError_t lds_rc = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&gdn_chunk_state_kernel),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kStateLds);
+  if (lds_rc != hipSuccess) return int(lds_rc);
   gdn_chunk_state_kernel<<<dim3(num_heads, kDV / kBV), 512, kStateLds,
                            static_cast<hipStream_t>(stream)>>>(
       static_cast<const bf16_t *>(k), ks[0], ks[1], w, u_base, g_cumsum, delta, chunk_state,
@@ -582,13 +581,10 @@ extern "C" int wy_gdn_chunk_output(const void *q, const int64_t *qs, const void 
   if (key_dim != kDK || value_dim != kDV) return WY_E_UNSUPPORTED;
   if (!rows_ok(q, qs) || !rows_ok(k, ks) || os[2] != 1) return WY_E_LAYOUT;
   const int N = (token_num + kC - 1) / kC;
-  static bool lds_set = false;   // the attribute is per function, set once
-  if (!lds_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gdn_chunk_output_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kOutLds);
-    if (e != hipSuccess) return int(e);
-    lds_set = true;
-  }
+  static const hipError_t lds_rc = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&gdn_chunk_output_kernel),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kOutLds);  // once, thread-safe
+  if (lds_rc != hipSuccess) return int(lds_rc);
   gdn_chunk_output_kernel<<<dim3(N, num_heads), 256, kOutLds, static_cast<hipStream_t>(stream)>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0], ks[1],
       delta, g_cumsum, chunk_state, static_cast<bf16_t *>(out), os[0], os[1], token_num,

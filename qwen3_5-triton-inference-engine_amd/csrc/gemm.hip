@@ -817,13 +817,11 @@ int launch_tiled_cfg(const bf16_t *x, int64_t xs0, const bf16_t *w, int64_t ws0,
   using C = TileCfg<BM, BN, WM, WN, kS>;
   static_assert(C::kLds <= 160 * 1024, "LDS");
   auto *fn = gemm_tiled_kernel<BM, BN, WM, WN, kSwiGLU, kS>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
-    if (e != hipSuccess) return int(e);
-    attr_set = true;
-  }
+  // once per instantiation; a function-local static is initialised exactly
+  // once, also under concurrent first calls
+  static const hipError_t attr_rc = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::kLds);
+  if (attr_rc != hipSuccess) return int(attr_rc);
   const int tm = (M + BM - 1) / BM, tn = (N + (kSwiGLU ? BN / 2 : BN) - 1) / (kSwiGLU ? BN / 2 : BN);
   fn<<<unsigned(tm * tn), 64 * C::kWaves, C::kLds, st>>>(x, xs0, w, ws0, y, ys0, M, N, K,
                                                          WY_GEMM_GROUP_M);

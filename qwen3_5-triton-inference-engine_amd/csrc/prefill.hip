@@ -31,6 +31,7 @@
 // first (LPT): as a grid of one workgroup per block when that grid fits the
 // chip, otherwise as a persistent grid of one workgroup per CU drawing blocks
 // from a shared ticket counter.
+#include <atomic>
 #include <type_traits>
 
 #include "wy_common.h"
@@ -135,7 +136,8 @@ void varlen_causal_prefill_kernel(
     const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t *__restrict__ out,
     int64_t os_t,
     int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
-    int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters, const BlockArgs blk) {
+    int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters, const BlockArgs blk,
+    int ticket_order) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_next_item;
   __shared__ int s_scan[256];
@@ -211,6 +213,13 @@ void varlen_causal_prefill_kernel(
     n_items = pre[n_qblocks];
     item = s_next_item;
   }
+  // Test hook (wy_prefill_set_ticket_order): the same blocks in another
+  // order.  0 heaviest first; 1 lightest first; 2 alternately from both ends.
+  auto permute = [&](int it, int n) {
+    if (ticket_order == 1) return n - 1 - it;
+    if (ticket_order == 2) return (it & 1) ? n - 1 - (it >> 1) : (it >> 1);
+    return it;
+  };
   for (;;) {
   int b, h, qb;
   if constexpr (kList) {
@@ -223,18 +232,19 @@ void varlen_causal_prefill_kernel(
       }
       return;
     }
-    // slice: the last s with pre[s] <= item (64-ary search, one probe per lane)
+    const int tk = permute(item, n_items);
+    // slice: the last s with pre[s] <= tk (64-ary search, one probe per lane)
     int lo = 0, hi = n_qblocks;
     while (hi - lo > 1) {
       const int step = (hi - lo + 63) / 64;
       const int probe = lo + lane * step;
-      const bool le = probe < hi && pre[probe] <= item;
+      const bool le = probe < hi && pre[probe] <= tk;
       const int k = 63 - __builtin_clzll(__ballot(le));  // lane 0 always qualifies
       lo += k * step;
       hi = min(lo + step, hi);
     }
     qb = n_qblocks - 1 - lo;
-    const int j = item - pre[lo];
+    const int j = tk - pre[lo];
     const int pair = j / n_kv_heads;
     h = j - pair * n_kv_heads;
     // b: the pair-th sequence (ascending) longer than 32 * qb
@@ -254,8 +264,9 @@ void varlen_causal_prefill_kernel(
       seen += c;
     }
   } else {
-    const int slice = item / bh_count;
-    const int bh = item - slice * bh_count;
+    const int it = permute(item, int(gridDim.x));
+    const int slice = it / bh_count;
+    const int bh = it - slice * bh_count;
     b = bh / n_kv_heads;
     h = bh - b * n_kv_heads;
     qb = n_qblocks - 1 - slice;
@@ -725,15 +736,11 @@ namespace {
 
 template <bool kList, int kRot>
 int set_prefill_lds() {
-  static bool done = false;
-  if (!done) {
-    const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<kList, kRot>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-    if (e != hipSuccess) return int(e);
-    done = true;
-  }
-  return WY_OK;
+  // once per instantiation (thread-safe function-local static initialisation)
+  static const hipError_t rc = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&varlen_causal_prefill_kernel<kList, kRot>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  return rc == hipSuccess ? WY_OK : int(rc);
 }
 
 bool prefill_layout_ok(const void *q, const int64_t *qs, const void *k, const int64_t *ks,
@@ -743,6 +750,10 @@ bool prefill_layout_ok(const void *q, const int64_t *qs, const void *k, const in
            !wyh::aligned16(q) || !wyh::aligned16(k) || !wyh::aligned16(v) ||
            !wyh::aligned16(out));
 }
+
+// Order in which the launches hand out query blocks (see the kernel's
+// permute); 0 outside tests.
+std::atomic<int> g_ticket_order{0};
 
 // Validated arguments -> one launch (direct or queue).
 template <int kRot>
@@ -772,15 +783,20 @@ int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_
   }
   auto *kern = counters ? varlen_causal_prefill_kernel<true, kRot>
                         : varlen_causal_prefill_kernel<false, kRot>;
+  const int order = g_ticket_order.load(std::memory_order_relaxed);
   kern<<<dim3(grid), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
       ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],
       os[1], cu_seqlens, kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks,
-      counters, blk);
+      counters, blk, order);
   return wyh::launch_status();
 }
 
 }  // namespace
+
+extern "C" void wy_prefill_set_ticket_order(int order) {
+  g_ticket_order.store(order >= 0 && order <= 2 ? order : 0, std::memory_order_relaxed);
+}
 
 extern "C" int wy_varlen_causal_prefill(const void *q, const int64_t *qs, const void *k,
                                         const int64_t *ks, const void *v,

@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "wy_attn.h"
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int64_t|int|size_t|const char \*)\s*(wy_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int64_t|int|void|size_t|const char \*)\s*(wy_\w+)\(", text, re.M)))
 
 
 def test_header_declares_expected_entry_points():

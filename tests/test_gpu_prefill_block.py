@@ -132,3 +132,38 @@ def test_block_equals_op_sequence_random_lengths(pkg, dev, seed):
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
     assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
+
+
+@pytest.mark.parametrize("lengths,seed", [
+    ([1, 3, 17, 64, 1000, 2000, 5], 3),         # queue launch
+    ([128] * 32, 7),                            # config 3: one-workgroup-per-block launch
+    ([16, 4096, 1500, 33, 700, 2500, 90, 1200], 11),  # queue launch, long and short
+])
+def test_block_independent_of_block_order(pkg, dev, lengths, seed):
+    """The attention block with its query blocks handed out heaviest first,
+    lightest first and alternately from both ends (wy_prefill_set_ticket_order):
+    bit-identical to one another and to the op sequence.  Any dependence of a
+    block's result on what ran before it on the same workgroup (LDS or
+    register state left by an earlier block) or on which workgroups run
+    together would show here."""
+    lib = pkg._lib.load()
+    say(f"prefill block order independence lengths={lengths}")
+    q, k, v, gate, bt, kc, vc, packed = make(pkg, dev, lengths, seed)
+    inv = pkg.rope_inv_freq(64, 1e7, device=dev)
+    ref = pkg.prefill_attention_packed(q, k, v, gate, inv, 64, packed, kc.clone(), vc.clone(),
+                                       bt)
+    try:
+        for order in (0, 1, 2):
+            lib.wy_prefill_set_ticket_order(order)
+            got = pkg.prefill_attention_block(q, k, v, gate, inv, 64, packed, kc.clone(),
+                                              vc.clone(), bt)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), f"order {order}"
+            plain = pkg.gqa_attention_varlen_causal(
+                q, k, v.view(-1, HKV, D), packed.cu_seqlens, max(lengths))
+            torch.cuda.synchronize()
+            if order == 0:
+                plain0 = plain
+            assert torch.equal(plain, plain0), f"plain op, order {order}"
+    finally:
+        lib.wy_prefill_set_ticket_order(0)

@@ -3,7 +3,9 @@ counters live in the library's static device array) against
 wy_paged_decode_step with a caller workspace (the op
 wy_lib::paged_gqa_attention_decode_fused), through the C ABI: outputs and the
 appended pages bit-identical, on two calls in a row, the second with a
-smaller batch, and a batch over the capacity rejected before any launch."""
+smaller batch, and a batch over the capacity rejected before any launch; and
+the entry point captured into a graph after an eager first call, every replay
+bit-identical to the workspace step."""
 
 import ctypes
 import sys
@@ -86,3 +88,33 @@ def test_noalloc_rejects_batch_over_capacity(pkg, dev):
     assert b"capacity" in lib.wy_status_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(kc, w["kc"]), "a rejected call must not launch"
+
+
+def test_noalloc_step_graph_replays(pkg, dev):
+    """After an eager call (which resolves the array and clears its counters),
+    the entry point is captured; each replay, with eager work in between,
+    equals the workspace step bit for bit."""
+    say("noalloc decode step under graph capture")
+    lens = [700, 64, 1900, 300]
+    w = case(dev, lens, seed=91)
+    ref, kc_ref, vc_ref = reference(pkg, dev, w)
+    kc, vc = w["kc"].clone(), w["vc"].clone()
+    out = torch.empty_like(ref)
+    assert call_noalloc(pkg, w, kc, vc, out) == 0
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(g, stream=s):
+        rcs.append(call_noalloc(pkg, w, kc, vc, out))
+    assert rcs == [0]
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}: output differs"
+        assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), f"replay {i}: pages differ"
+        # eager work between replays: the workspace step on other buffers
+        reference(pkg, dev, case(dev, [100, 33], seed=92 + i))
+        torch.cuda.synchronize()
