@@ -248,8 +248,9 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
     ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-prefill3", "pmc-gemm",
-                             "pmc-gdn"],
-                    help="pmc-*: eager launches only, for rocprofv3 counter runs")
+                             "pmc-gdn", "floor"],
+                    help="pmc-*: eager launches only, for rocprofv3 counter runs; floor: "
+                         "vendor kernels over the headline's bytes, for a rocprofv3 trace")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the attention path "
@@ -364,6 +365,38 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"mode": "pmc-gdn",
                           "decode_algorithmic_bytes": Bg * Hg * (2 * Dg * Dg * 4 + 4 * Dg * 2 + 8)}))
+        return
+    if args.mode == "floor":
+        # Vendor kernels moving the headline step's bytes, each layer on its
+        # own buffers (6 x, > MALL), 40 eager rounds each: a device copy of
+        # 40 MB into 40 MB (80 MB of traffic), torch.index_select of the step's
+        # K and of its V page rows (each 40 MB read + 40 MB written), a bf16
+        # sum of 80 MB, next to wy_page_stream_read and the step itself.
+        kvb = sum(lens) * HKV * D * 2 * 2
+        src = [torch.ones(kvb // 4, dtype=torch.bfloat16, device=dev) for _ in layers]
+        dst = [torch.empty_like(x) for x in src]
+        flat = [torch.ones(kvb // 2, dtype=torch.bfloat16, device=dev) for _ in layers]
+        btc = layers[0]["bt"].cpu()
+        rows = torch.tensor([int(btc[b, p]) * HKV + h for b, n in enumerate(lens)
+                             for h in range(HKV) for p in range(-(-n // PAGE))],
+                            device=dev, dtype=torch.int64)
+        gath = torch.empty(rows.numel(), PAGE * D, dtype=torch.bfloat16, device=dev)
+        cases = {
+            "copy": lambda i: dst[i].copy_(src[i]),
+            "index_select": lambda i: (
+                torch.index_select(layers[i]["kc"].view(-1, PAGE * D), 0, rows, out=gath),
+                torch.index_select(layers[i]["vc"].view(-1, PAGE * D), 0, rows, out=gath)),
+            "sum": lambda i: flat[i].sum(dtype=torch.float32),
+            "page_stream_read": lambda i: pkg.page_stream_read(layers[i]["kc"], layers[i]["vc"],
+                                                               layers[i]["bt"], layers[i]["pos"]),
+            "decode_step": lambda i: layer_step(layers[i]),
+        }
+        for fn in cases.values():
+            for _ in range(40):
+                for i in range(ATTN_LAYERS):
+                    fn(i)
+            torch.cuda.synchronize()
+        print(json.dumps({"mode": "floor", "kv_bytes": kvb, "rounds": 40}))
         return
     if args.mode == "pmc-copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
