@@ -469,11 +469,21 @@ def test_prefill_then_decode_consistency(pkg, dev):
 
 # ------------------------------------------------------------------ fused decode step
 
-@pytest.mark.parametrize("lens", [[1], [17, 64, 65], [256], [5000, 3, 700], [2048 * 4 + 3]])
+def _lens(n, lo, hi, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, (n,), generator=g).tolist()
+
+
+# batches of 16..256 take the balanced workgroup order (one to four chunks of
+# 64 sequences in its pass over pos); smaller ones the direct order, where a
+# sequence of more than 16 splits merges in two levels
+@pytest.mark.parametrize("lens", [[1], [17, 64, 65], [256], [5000, 3, 700], [2048 * 4 + 3],
+                                  _lens(16, 1, 3000, 1), _lens(80, 1, 1500, 2) + [2600],
+                                  _lens(256, 1, 400, 3)])
 def test_fused_step_equals_three_op_path(pkg, dev, lens):
     """One-launch step == append + split + combine (same device math, same
     rounding): bit-identical output and pools; counters return to zero."""
-    say(f"fused vs 3-op lens={lens}")
+    say(f"fused vs 3-op B={len(lens)} lens={lens[:8]}")
     gen = torch.Generator().manual_seed(sum(lens))
     B = len(lens)
     max_pages = -(-max(lens) // 16) + 1
