@@ -569,10 +569,7 @@ def main():
         extra["decode_B1_curve"] = b1_curve_bench(pkg, dev)
     # ---- length skew at config 2's total tokens --------------------------------
     if want("skew"):
-        # Switched off: its first run (one 35k-token sequence among 31 of 128
-        # tokens, B=32, in a build that also merged >16 splits in two levels
-        # at B=32) ended in a GPU memory fault whose cause is not found yet.
-        extra["decode_length_skew"] = {"status": "not run (see DESIGN.md, decode length skew)"}
+        extra["decode_length_skew"] = skew_bench(pkg, dev, sum(lens), args.steps, args.warmup)
 
     # ---- config 3: varlen prefill 32 x 128 -------------------------------------
     if want("c3"):

@@ -413,11 +413,14 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     const int first_guess = s * a.min_pps + wave;
     const int32_t *bt_first = btrow + (first_guess < a.bt_cols ? first_guess : a.bt_cols - 1);
     int32_t pos_lo;
+    // Both outputs are early-clobber: the first load's destination must not
+    // share registers with the second load's address, which is read when the
+    // second load issues -- possibly after the first has returned.
     asm volatile(
         "s_load_dword %0, %2, 0x0\n\t"
         "s_load_dword %1, %3, 0x0\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=s"(pos_lo), "=s"(bt_guess)
+        : "=&s"(pos_lo), "=&s"(bt_guess)
         : "s"(a.pos + b), "s"(bt_first)
         : "memory");
     seq_len = pos_lo + 1;

@@ -480,3 +480,26 @@ def test_ctypes_signatures_match_header():
         assert name in decls, name
         params = [p for p in decls[name].split(",") if p.strip()]
         assert len(params) == len(argtypes), (name, len(params), len(argtypes))
+
+
+def test_multi_instruction_asm_outputs_are_early_clobber():
+    """An inline-asm block of several instructions whose outputs are written
+    asynchronously (scalar or vector memory loads) must mark every output
+    early-clobber ("=&"): otherwise the compiler may give an output the
+    registers of a later instruction's input, and that input is read after the
+    earlier instruction's result may have landed.  (Unmarked, the decode
+    step's pos / block-table pair of scalar loads got the first load's
+    destination on the second load's address and faulted now and then.)"""
+    import re
+
+    for f in sorted((ROOT / "qwen3_5-triton-inference-engine_amd" / "csrc").glob("*.hip")):
+        text = f.read_text()
+        for m in re.finditer(r"asm\s+volatile\s*\((.*?)\);", text, re.S):
+            body = m.group(1)
+            parts = body.split(":")
+            insts = parts[0]
+            if "\\n" not in insts or len(parts) < 2:
+                continue
+            outs = re.findall(r'"(=[^"]*)"', parts[1])
+            for o in outs:
+                assert o.startswith("=&"), (f.name, body[:80], o)
