@@ -101,10 +101,10 @@ int wy_paged_decode_split(const void *q, const int64_t *q_strides,
 /*
  * Split-K merge: out[b, hq, :] = sum_s a_s acc_s / sum_s a_s l_s with
  * a_s = exp(m_s - max m), over the active splits of sequence b (same
- * partition formula as wy_paged_decode_split).  For B < 16, more than 16
- * splits merge in two levels (each group of 16 splits, then the group
- * states), the order the one-launch step uses, so both give the same bits.  out [B, H_q, D] bf16 with
- * strides out_strides.
+ * partition formula as wy_paged_decode_split).  More than 16 splits merge
+ * in two levels (each group of 16 splits, then the group states), the order
+ * the one-launch step uses, so both give the same bits for the same
+ * partition.  out [B, H_q, D] bf16 with strides out_strides.
  * Replaces wy_lib::paged_gqa_attention_decode_combine
  *   (triton_kernels/gqa_attention_decode_paged.py:901-939, kernel :747-817).
  */
@@ -120,12 +120,16 @@ int wy_paged_decode_combine(const float *m_partial, const float *l_partial,
  * (+ optional sigmoid gate).  The new token's K/V rows are taken from
  * k_new/v_new [B, H_kv, D] and written to their page by the workgroup that
  * owns that page; the last workgroup of each (b, kv head) to finish merges
- * the splits -- for B < 16 in two levels, through groups of 16 splits, when a
- * sequence has more than 16 -- (counters [B*H_kv*9] int32: B*H_kv per-(b, kv head)
+ * the splits -- in two levels, through groups of 16 splits, when a sequence
+ * has more than 16 -- (counters [B*H_kv*9] int32: B*H_kv per-(b, kv head)
  * counters, then B*H_kv*8 group counters; zero before the first call and
  * left zero by every call).  gate (may be NULL) [B, H_q, D] with strides
  * gate_strides: out = bf16(bf16(ctx) * sigmoid(gate)), the rounding of the
  * reference's combine followed by its gate pack.  out [B, H_q, D] bf16.
+ * Partition: that of wy_paged_decode_split, except that for B <= 256 when
+ * B >= 16 or max_pages >= 1024 the floor is raised on the device to
+ * max(min_pages_per_split, ceil(H_kv * sum_b npg_b / 256)), so a batch holds
+ * about 256 work items (one per CU) once its total length calls for it.
  * Concurrent calls sharing one counters/scratch set race.
  * Replaces the sequence paged_kv_append -> paged_gqa_attention_decode_split
  * -> paged_gqa_attention_decode_combine (-> attention_gate_pack) of

@@ -32,6 +32,10 @@
 // With min_pps = 1 this is exactly the reference partition
 // (gqa_attention_decode_paged.py:675-682, 779-784); a larger min_pps trades
 // split count for less fp32 scratch traffic.
+// The one-launch step in the balanced order raises min_pps further to
+// ceil(H_kv * sum(npg) / kWorkItems), computed by every workgroup from the
+// same pos, so long batches get long splits and a lone long sequence among
+// short ones still gets many.
 //
 // Workgroup order.  The direct order gives workgroup id b + B*(h + H*s).  The
 // balanced order (batches of 16..256 sequences) lists the active splits only,
@@ -41,6 +45,7 @@
 // which the dispatcher deals round-robin over the XCDs -- carry equal page
 // counts.  The order only decides where a split runs, never its pages or its
 // arithmetic, so results are identical under both orders.
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -82,8 +87,10 @@ struct DecodeArgs {
   const float *inv_freq;
   float eps;
   int rope_dim;
-  int balanced;   // workgroup order: 0 direct, 1 balanced (see the file comment)
-  int two_level;  // merge more than kMergeGroup splits through groups (batch < 16)
+  int balanced;    // workgroup order: 0 direct, 1 balanced (see the file comment)
+  int two_level;   // merge more than kMergeGroup splits through groups
+  int work_items;  // balanced fused order: raise the split floor to keep the
+                   // active (split, KV head) items within this many (0: off)
 };
 
 __device__ __forceinline__ int split_pps(int npg, int min_pps) {
@@ -260,8 +267,8 @@ __device__ Merged merge_slots(const DecodeArgs &a, int b, int hq, int first, int
 
 // Splits per merge group.  Up to kMergeGroup splits merge in one level (the
 // last split of the sequence and KV head to finish merges them all); with
-// two_level set (batches below 16, where one long sequence is cut into up to
-// 128 splits of 4+ pages) more merge in two: the last split of each group of
+// two_level set (a long sequence cut into up to 128 splits) more merge in
+// two: the last split of each group of
 // kMergeGroup merges its group into the group's first slot, and the last
 // group to finish merges the group states.  One merging wavefront then reads
 // at most 16 accumulator rows (16 KiB) instead of up to 128.
@@ -305,7 +312,7 @@ __device__ Merged merge_all(const DecodeArgs &a, int b, int hq, int nact, int la
 constexpr int kBalancedMinBatch = 16;
 constexpr int kBalancedChunks = 4;  // batch <= 256
 __device__ bool balanced_item(const DecodeArgs &a, int k, int lane, int &b, int &h, int &s,
-                              int &seq_len) {
+                              int &seq_len, int &min_pps) {
   const int H = a.hkv;
   const int nch = (a.batch + 63) >> 6;
   int plo[kBalancedChunks], npg[kBalancedChunks], pps[kBalancedChunks];
@@ -315,10 +322,22 @@ __device__ bool balanced_item(const DecodeArgs &a, int k, int lane, int &b, int 
     plo[c] = c < nch && bb < a.batch ? int(a.pos[bb]) : -1;
   }
 #pragma unroll
-  for (int c = 0; c < kBalancedChunks; ++c) {
-    npg[c] = (plo[c] + kPage) / kPage;
-    pps[c] = split_pps(npg[c], a.min_pps);
+  for (int c = 0; c < kBalancedChunks; ++c) npg[c] = (plo[c] + kPage) / kPage;
+  min_pps = a.min_pps;
+  if (a.work_items > 0) {
+    // Split floor from the batch's total pages: ceil(H * total / work_items),
+    // so the launch holds at most work_items + B*H items whatever the
+    // lengths (every workgroup computes the same value from the same pos).
+    int tot = 0;
+#pragma unroll
+    for (int c = 0; c < kBalancedChunks; ++c) tot += npg[c];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o);
+    const int need = int((int64_t(tot) * H + a.work_items - 1) / a.work_items);
+    min_pps = __builtin_amdgcn_readfirstlane(need > min_pps ? need : min_pps);
   }
+#pragma unroll
+  for (int c = 0; c < kBalancedChunks; ++c) pps[c] = split_pps(npg[c], min_pps);
   int carry = 0;
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
@@ -385,9 +404,9 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   typedef const __attribute__((address_space(4))) int32_t *bt_const_t;
-  int b, h, s, seq_len = 0;
+  int b, h, s, seq_len = 0, min_pps = a.min_pps;
   if (a.balanced) {
-    if (!balanced_item(a, blockIdx.x, lane, b, h, s, seq_len)) return;
+    if (!balanced_item(a, blockIdx.x, lane, b, h, s, seq_len, min_pps)) return;
   } else {
     b = blockIdx.x % a.batch;
     h = (blockIdx.x / a.batch) % a.hkv;
@@ -407,7 +426,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   int32_t bt_guess;
   if (a.balanced) {
     const int npg_b = (seq_len + kPage - 1) / kPage;
-    const int first = s * split_pps(npg_b, a.min_pps) + wave;
+    const int first = s * split_pps(npg_b, min_pps) + wave;
     bt_guess = bt_s[first < npg_b ? first : npg_b - 1];
   } else {
     const int first_guess = s * a.min_pps + wave;
@@ -426,7 +445,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     seq_len = pos_lo + 1;
   }
   const int npg = (seq_len + kPage - 1) / kPage;
-  const int pps = split_pps(npg, a.min_pps);
+  const int pps = split_pps(npg, min_pps);
   const int nact = (npg + pps - 1) / pps;
   if (s * pps >= npg) return;  // inactive split: uniform over the workgroup
   const int p0 = s * pps;
@@ -462,7 +481,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   // launch), one page ahead, so a page's address never waits on the vector
   // memory counter that its K/V loads share.
   const int npw = p0 + wave < p1 ? (p1 - p0 - wave + kW - 1) / kW : 0;
-  int32_t bt_ahead = npw > 0 ? (a.balanced || pps == a.min_pps ? bt_guess : bt_s[p0 + wave]) : 0;
+  int32_t bt_ahead = npw > 0 ? (a.balanced || pps == min_pps ? bt_guess : bt_s[p0 + wave]) : 0;
   // Register pipeline, no extra registers: K of page i+1 is requested as soon
   // as the score MFMAs have consumed K of page i, and each pair of V rows of
   // page i+1 as soon as P.V has consumed that pair of page i, so each load
@@ -882,7 +901,19 @@ bool out_layout_ok(const void *out, const int64_t *os) {
                         (reinterpret_cast<uintptr_t>(out) & 7u) == 0);
 }
 
-constexpr int kLongSplitPages = 128;
+// Target item count of the one-launch step's balanced order: one per CU.
+// A batch whose splits at the caller's floor would exceed it gets longer
+// splits (64 x 32k tokens: 1024 pages each, 256 items), while a batch with
+// one very long sequence among short ones keeps the short floor and cuts the
+// long sequence into many splits.  Measured over 256/512/1024/2048/4096 on
+// B = 1..64 x 32k tokens: fewer, longer splits stream faster at every batch
+// (64 x 32k: 741 us at 256, 766 us at 2048), and short batches never reach
+// the target, so they are unchanged.
+#ifndef WY_DECODE_WORK_ITEMS
+#define WY_DECODE_WORK_ITEMS 256
+#endif
+constexpr int kWorkItems = WY_DECODE_WORK_ITEMS;
+constexpr int kLongTablePages = 1024;
 
 int split_grid_z(int max_pages, int min_pps) {
   const int z = (max_pages + min_pps - 1) / min_pps;
@@ -909,14 +940,20 @@ int launch_split(const DecodeArgs &args, int batch, int num_kv_heads, int max_pa
   DecodeArgs a = args;
   a.batch = batch;
   a.bt_cols = max_pages;
-  // The balanced order for mid-size batches of short/medium contexts; long
-  // contexts (many full splits per sequence) and small batches keep the
+  // The balanced order for mid-size batches, and for the one-launch step of
+  // small batches over long tables; small batches over short tables keep the
   // direct order, which needs no pass over pos before the first loads.
-  a.balanced = batch >= kBalancedMinBatch && batch <= 64 * kBalancedChunks &&
-               min_pps < kLongSplitPages;
-  a.two_level = batch < kBalancedMinBatch;
-  const dim3 grid(unsigned(batch) * unsigned(num_kv_heads) *
-                  unsigned(split_grid_z(max_pages, min_pps)));
+  a.balanced = batch <= 64 * kBalancedChunks &&
+               (batch >= kBalancedMinBatch || (kFused && max_pages >= kLongTablePages));
+  a.two_level = 1;
+  int64_t items = int64_t(batch) * num_kv_heads * split_grid_z(max_pages, min_pps);
+  if (kFused && a.balanced) {
+    // The one-launch step merges its own splits, so it may size them from
+    // the batch's total length: at most kWorkItems + B*H items.
+    a.work_items = kWorkItems;
+    items = std::min<int64_t>(items, kWorkItems + int64_t(batch) * num_kv_heads);
+  }
+  const dim3 grid{unsigned(items)};
   return launch_split_w<kFused, kWaves, kProlog>(grid, a, static_cast<hipStream_t>(stream));
 }
 
@@ -1008,7 +1045,7 @@ extern "C" int wy_paged_decode_combine(const float *m_partial, const float *l_pa
   a.a_s = as[2];
   a.pos = pos;
   a.min_pps = min_pages_per_split;
-  a.two_level = batch < kBalancedMinBatch;
+  a.two_level = 1;
   a.out = static_cast<bf16_t *>(out);
   a.o_b = os[0];
   a.o_h = os[1];

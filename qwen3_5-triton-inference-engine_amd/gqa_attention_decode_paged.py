@@ -51,15 +51,18 @@ def min_pages_per_split(batch: int) -> int:
 
 
 # The one-launch step and block merge their own splits (no combine op has to
-# agree on the partition), so they may also use the table width: with long
-# contexts (>= 1024 pages = 16k tokens) 128-page splits stream each split's
-# pages longer and cut the merge work (config 5: 818 -> 767 us per step).
+# agree on the partition).  For batches up to 256 the kernel raises the floor
+# itself from the batch's total length (about one work item per CU: 64 x 32k
+# tokens gets 1024-page splits, while one long sequence among short ones
+# still gets many short splits); beyond 256 sequences a table of >= 1024
+# pages (16k tokens) raises the floor to 128 pages.
 LONG_CONTEXT_PAGES = 1024
 MIN_PAGES_PER_SPLIT_LONG = 128
+BALANCED_MAX_BATCH = 256
 
 
 def min_pages_per_split_fused(batch: int, max_pages: int) -> int:
-    if max_pages >= LONG_CONTEXT_PAGES:
+    if max_pages >= LONG_CONTEXT_PAGES and batch > BALANCED_MAX_BATCH:
         return MIN_PAGES_PER_SPLIT_LONG
     return min_pages_per_split(batch)
 

@@ -475,11 +475,14 @@ def _lens(n, lo, hi, seed):
 
 
 # batches of 16..256 take the balanced workgroup order (one to four chunks of
-# 64 sequences in its pass over pos); smaller ones the direct order, where a
-# sequence of more than 16 splits merges in two levels
+# 64 sequences in its pass over pos), as do smaller ones over tables of 1024+
+# pages (the last two cases); other small batches the direct order.  A
+# sequence of more than 16 splits merges in two levels (B=1 x 8195 tokens:
+# 128 splits; one 35129-token sequence among 31 short ones: 92 splits).
 @pytest.mark.parametrize("lens", [[1], [17, 64, 65], [256], [5000, 3, 700], [2048 * 4 + 3],
-                                  _lens(16, 1, 3000, 1), _lens(80, 1, 1500, 2) + [2600],
-                                  _lens(256, 1, 400, 3)])
+                                  _lens(16, 1, 3000, 1), _lens(80, 1, 1000, 2) + [2600],
+                                  _lens(256, 1, 300, 3), [35129] + [128] * 31,
+                                  [32768], [16400, 1, 60, 33]])
 def test_fused_step_equals_three_op_path(pkg, dev, lens):
     """One-launch step == append + split + combine (same device math, same
     rounding): bit-identical output and pools; counters return to zero."""
@@ -487,6 +490,13 @@ def test_fused_step_equals_three_op_path(pkg, dev, lens):
     gen = torch.Generator().manual_seed(sum(lens))
     B = len(lens)
     max_pages = -(-max(lens) // 16) + 1
+    # the step's device-side floor from the total length, where it applies,
+    # leaves every sequence's partition as the split op's
+    floor = pkg.gqa_attention_decode_paged.min_pages_per_split(B)
+    if B <= 256 and (B >= 16 or max_pages >= 1024):
+        step_floor = max(floor, -(-HKV * sum(-(-n // 16) for n in lens) // 256))
+        assert all(orc.split_partition(n, floor) == orc.split_partition(n, step_floor)
+                   for n in lens)
     num_pages = B * max_pages + 3
     bt = rand_table(B, max_pages, num_pages, gen)
     kc, vc = bf((num_pages, HKV, 16, D), gen), bf((num_pages, HKV, 16, D), gen)
@@ -505,6 +515,39 @@ def test_fused_step_equals_three_op_path(pkg, dev, lens):
     assert int(sc.counters.abs().sum()) == 0
     orc.paged_kv_append(kc, vc, kn, vn, bt, pos.cpu())
     close(fused, orc.paged_decode(q, kc, vc, bt, pos.cpu() + 1), what=f"fused {lens}")
+
+
+def test_fused_step_split_floor_from_total_length(pkg, dev):
+    """B=16 at 24k..32k tokens: the one-launch step raises its split floor
+    from the batch's total pages (ceil(2 * sum(npg) / 256) > the 24-page
+    floor), a partition the three-op path does not use, so it is checked
+    against the oracle (and the three-op path within tolerance)."""
+    lens = _lens(16, 24000, 32768, 5)
+    say(f"fused work floor B=16 lens={lens[:4]}")
+    gen = torch.Generator().manual_seed(5)
+    B = len(lens)
+    max_pages = -(-max(lens) // 16) + 1
+    num_pages = B * max_pages + 3
+    bt = rand_table(B, max_pages, num_pages, gen)
+    kc, vc = bf((num_pages, HKV, 16, D), gen), bf((num_pages, HKV, 16, D), gen)
+    q, kn, vn = bf((B, HQ, D), gen), bf((B, HKV, D), gen), bf((B, HKV, D), gen)
+    npg = [-(-n // 16) for n in lens]
+    assert -(-2 * sum(npg) // 256) > 24
+    pos = torch.tensor([n - 1 for n in lens], device=dev)
+    sc = pkg.allocate_split_scratch(HQ, D, batch=B, device=dev)
+    k1, v1 = kc.to(dev), vc.to(dev)
+    fused = pkg.call_paged_gqa_attention_decode_triton(q.to(dev), kn.to(dev), vn.to(dev), k1,
+                                                       v1, bt.to(dev), pos, sc)
+    k2, v2 = kc.to(dev), vc.to(dev)
+    plain = pkg.call_paged_gqa_attention_decode_triton(q.to(dev), kn.to(dev), vn.to(dev), k2,
+                                                       v2, bt.to(dev), pos, tuple(sc))
+    torch.cuda.synchronize()
+    assert int(sc.counters.abs().sum()) == 0
+    orc.paged_kv_append(kc, vc, kn, vn, bt, pos.cpu())
+    assert torch.equal(k1.cpu(), kc) and torch.equal(v1.cpu(), vc)
+    ref = orc.paged_decode(q, kc, vc, bt, pos.cpu() + 1)
+    close(fused, ref, what="fused work floor")
+    close(fused, plain.float(), what="fused vs 3-op")
 
 
 def test_decode_attention_step_with_gate(pkg, dev):
