@@ -248,7 +248,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no extras/CPU")
     ap.add_argument("--only", default="", help="comma list of extras to run")
     ap.add_argument("--mode", default="bench", choices=["bench", "pmc-step", "pmc-copy", "pmc-prefill", "pmc-prefill3", "pmc-gemm",
-                             "pmc-gdn", "floor"],
+                             "pmc-gdn", "floor", "trace-c5"],
                     help="pmc-*: eager launches only, for rocprofv3 counter runs; floor: "
                          "vendor kernels over the headline's bytes, for a rocprofv3 trace")
     args = ap.parse_args()
@@ -397,6 +397,20 @@ def main():
                     fn(i)
             torch.cuda.synchronize()
         print(json.dumps({"mode": "floor", "kv_bytes": kvb, "rounds": 40}))
+        return
+    if args.mode == "trace-c5":
+        # config 5 alone (B=64 x 32768, one 4 GiB pool): 5 warm-up steps, then 20,
+        # eager, for a kernel trace of the one-launch step at that size
+        w5 = decode_workload([32768] * 64, dev, seed=5, kv_scale=0.5)
+        sc5 = pkg.allocate_split_scratch(HQ, D, batch=64, device=dev)
+        g5 = w5["gate"][0].permute(1, 0, 2)
+        for _ in range(25):
+            torch.ops.wy_lib.paged_gqa_attention_decode_fused(
+                w5["q"], w5["kn"], w5["vn"], w5["kc"], w5["vc"], w5["bt"], w5["pos"], *sc5,
+                sc5.counters, g5)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "trace-c5", "launches": 25,
+                          "algorithmic_bytes_per_launch": decode_bytes(w5["lens"])}))
         return
     if args.mode == "pmc-copy":
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
