@@ -59,11 +59,15 @@ static_assert(2 * 32 * kQPitch <= kTileV, "two waves' q rows fit one V slot");
 constexpr int kKDma = kTileK / 1024 + (kTileK % 1024 != 0);  // 1 KiB DMA blocks: 33
 constexpr int kVDma = kTileV / 1024;                          // 36
 static_assert(kTileV % 1024 == 0, "V tile is a whole number of DMA blocks");
-constexpr int kLdsBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 KiB
+constexpr int kRingBytes = 2 * (kTileK + kTileV);  // two K + two V slots: 138 KiB
+// The K tile is 33 DMA blocks: in the steady tile loop every wave issues 9 K
+// blocks, and the ninth of waves 1..3 lands in this unread 1 KiB, so the
+// issue needs no branch.
+constexpr int kLdsBytes = kRingBytes + 1024;
 // Output staging in the epilogue (reuses the rings): 32 rows of 4 heads x
 // 256 dims, rows padded by 16 bytes against bank conflicts of the lane writes.
 constexpr int kStagePitch = 4 * 256 + 8;   // bf16
-static_assert(32 * kStagePitch * 2 <= kLdsBytes, "output stage fits the rings");
+static_assert(32 * kStagePitch * 2 <= kRingBytes, "output stage fits the rings");
 // Exponentials are taken against a per-row reference fixed by the first KV
 // tile; a later score may exceed it by a factor up to 2^64 (P stays finite in
 // bf16 and fp32).  Beyond that the block is recomputed exactly.
@@ -98,6 +102,20 @@ __device__ __forceinline__ u32x2_t ds_read_tr16(uint32_t lds_addr) {
   u32x2_t r;
   asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds_addr), "i"(kOff));
   return r;
+}
+template <int kOff>
+__device__ __forceinline__ u32x4_t ds_read_b128_at(uint32_t lds_addr) {
+  u32x4_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(lds_addr), "i"(kOff));
+  return r;
+}
+template <int kN>
+__device__ __forceinline__ void lgkm_wait1(u32x4_t &a) {
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "n"(kN));
+}
+template <int kN>
+__device__ __forceinline__ void lgkm_wait2(u32x2_t &a, u32x2_t &b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(kN));
 }
 template <int kN>
 __device__ __forceinline__ void lgkm_wait(u32x2_t (&a)[4], u32x2_t (&b)[4]) {
@@ -621,6 +639,150 @@ void varlen_causal_prefill_kernel(
     if constexpr (kMode == 1) m_ref = m_acc;
   };
 
+
+  // The pass the kernel normally takes (the first-tile reference of kMode 0
+  // above, same arithmetic), as a software pipeline with no branch inside a
+  // tile: after the barrier of tile t the wave issues S^T(t+1) on the MFMA
+  // pipe and, between those MFMAs, turns S^T(t) into P (exponentials, row
+  // sum, bf16 packing) and issues the next tiles' DMA, so the VALU work runs
+  // under the MFMAs instead of after them; then PV(t), its V operands
+  // streamed a window of 8 MFMAs ahead, with the score registers handed on
+  // for the next tile in its gaps.  Every LDS operand read is inline asm
+  // with an explicit lgkmcnt count (LDS reads complete in order).  In the
+  // last loop iteration the K DMA of the tile past the end lies outside the
+  // buffer range (nothing fetched) and lands in a slot nobody reads again.
+  // Only the last tile reaches the diagonal or the sequence end, so only it
+  // is masked, after the loop.
+  const uint32_t k_lane = lds_u32(k_ring) + uint32_t(col * kKPitch + g * 16);
+  auto issue_k1 = [&](int t, int slot, auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const uint32_t soff = uint32_t(t * kBN) * k_row_bytes;
+    unsigned char *dst = k_ring + slot * kTileK + (wave + 4 * i) * 1024;
+    if constexpr (4 * i + 3 >= kKDma) dst = wave + 4 * i < kKDma ? dst : smem + kRingBytes;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rsrc, (lds_void_t *)dst, 16, k_voff[i], soff, 0,
+                                             0);
+  };
+  auto issue_v1 = [&](int t, int slot, auto ic) {
+    constexpr int i = decltype(ic)::value;
+    const uint32_t soff = uint32_t(t * kBN) * v_row_bytes;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        v_rsrc, (lds_void_t *)(v_ring + slot * kTileV + (wave + 4 * i) * 1024), 16, v_voff[i],
+        soff, 0, 0);
+  };
+  // Operand of S^T MFMA i (i = 8 kb + 2 c + mt): K rows 32 mt + col, k-step
+  // 4 kb + c; of PV MFMA j (j = 8 ks + dt): V^T of dims 32 dt.., k-step ks.
+  auto k_read = [&](uint32_t base, auto ic) {
+    constexpr int i = decltype(ic)::value;
+    constexpr int off = (i & 1) * 32 * kKPitch + (4 * (i >> 3) + ((i & 7) >> 1)) * 32;
+    return ds_read_b128_at<off>(base);
+  };
+  auto v_read = [&](uint32_t base, u32x2_t &lo, u32x2_t &hi, auto jc) {
+    constexpr int j = decltype(jc)::value;
+    constexpr int ks = j >> 3, dt = j & 7;
+    constexpr int off = (32 * (ks >> 1) + 8 * (ks & 1)) * kVPitch + dt * 64;
+    lo = ds_read_tr16<off>(base);
+    hi = ds_read_tr16<off + 4 * kVPitch>(base);
+  };
+  auto softmax_pair = [&](f32x16_t(&s)[2], u32x4_t(&pb)[4], float &psum, auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr int mt = p >> 3, kk = (p >> 2) & 1, w = p & 3;
+    const float a = __builtin_amdgcn_exp2f(s[mt][8 * kk + 2 * w]);
+    const float c = __builtin_amdgcn_exp2f(s[mt][8 * kk + 2 * w + 1]);
+    psum += a + c;
+    pb[2 * mt + kk][w] = pack_bf16x2(a, c);
+  };
+  auto mask_tile = [&](f32x16_t(&s)[2], int t) {
+    const int kv0 = t * kBN;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int thr = row_lim - (kv0 + 32 * mt + 16 * g);  // keep registers e <= thr
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[mt][e] = e > thr ? -INFINITY : s[mt][e];
+    }
+  };
+  // O^T += V^T P^T of the tile in V slot `vslot`; `gap(j)` runs after MFMA j.
+  auto pv = [&](int vslot, u32x4_t(&pb)[4], auto &&gap) {
+    const uint32_t vr = lds_u32(v_ring + vslot * kTileV) + v_lane_off;
+    u32x2_t va[8][2];
+    static_for<0, 8>([&](auto jc) { v_read(vr, va[jc][0], va[jc][1], jc); });
+    static_for<0, 32>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int ks = j >> 3, dt = j & 7, rest = 31 - j < 7 ? 31 - j : 7;
+      lgkm_wait2<2 * rest>(va[j & 7][0], va[j & 7][1]);
+      const u32x4_t a = {va[j & 7][0][0], va[j & 7][0][1], va[j & 7][1][0], va[j & 7][1][1]};
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                      __builtin_bit_cast(bf16x8_t, pb[ks]),
+                                                      o[dt], 0, 0, 0);
+      if constexpr (j + 8 < 32) v_read(vr, va[j & 7][0], va[j & 7][1], std::integral_constant<int, j + 8>{});
+      gap(jc);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  auto run_fast = [&] {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // K(0), V(0), K(1) landed
+    f32x16_t s_cur[2], s_nxt[2];
+    qk(0, s_cur, zero16, no_dma);
+    if (n_tiles == 1) mask_tile(s_cur, 0);
+    {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[mt][e]);
+      m_ref = fmaxf(mx, __shfl_xor(mx, 32));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_cur[mt][e] -= m_ref;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_nxt[mt][e] = -m_ref;
+    }
+    int t = 0;
+    for (; t + 1 < n_tiles; ++t) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K(t+1), V(t) landed
+      __syncthreads();  // and every wave is done with S^T(t) and PV(t-1)
+      const uint32_t kb = k_lane + uint32_t(((t + 1) & 1) * kTileK);
+      u32x4_t ka[8];
+      static_for<0, 8>([&](auto ic) { ka[ic] = k_read(kb, ic); });
+      u32x4_t pb[4];
+      float psum = 0.f;
+      const uint32_t vr0 = lds_u32(v_ring + (t & 1) * kTileV) + v_lane_off;
+      static_for<0, 32>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int ii = i & 7, mt = ii & 1, ks = 4 * (i >> 3) + (ii >> 1);
+        lgkm_wait1<(i < 24 ? 7 : 31 - i)>(ka[ii]);
+        s_nxt[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8_t, ka[ii]), qb_op[ks], s_nxt[mt], 0, 0, 0);
+        if constexpr (i + 8 < 32) ka[ii] = k_read(kb, std::integral_constant<int, i + 8>{});
+        if constexpr (i & 1) softmax_pair(s_cur, pb, psum, std::integral_constant<int, i / 2>{});
+        if constexpr (i < 9) issue_k1(t + 2, t & 1, ic);
+        else if constexpr (i < 18) issue_v1(t + 1, (t + 1) & 1, std::integral_constant<int, i - 9>{});
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      (void)vr0;
+      l_part += psum;
+      pv(t & 1, pb, [&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int mt = j >> 4, e = j & 15;
+        s_cur[mt][e] = s_nxt[mt][e];
+        s_nxt[mt][e] = -m_ref;
+      });
+    }
+    if (n_tiles > 1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V(t) landed
+      __syncthreads();
+      mask_tile(s_cur, t);
+    }
+    u32x4_t pb[4];
+    float psum = 0.f;
+    static_for<0, 16>([&](auto pc) { softmax_pair(s_cur, pb, psum, pc); });
+    l_part += psum;
+    pv(t & 1, pb, [](auto) {});
+  };
+
   auto zero_acc = [&] {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
@@ -630,7 +792,7 @@ void varlen_causal_prefill_kernel(
   };
 
   zero_acc();
-  run_pass(std::integral_constant<int, 0>{});
+  run_fast();
   float l = l_part + __shfl_xor(l_part, 32);
   // Some score exceeded its row's first-tile maximum by a factor over 2^64
   // (or is not finite): l is then at least 2^64.
