@@ -39,6 +39,9 @@
 using namespace wy;
 
 namespace {
+#if WY_TRACE
+__device__ unsigned long long g_trace[256 * 64 * 8];
+#endif
 
 constexpr int kD = 256;
 constexpr int kG = 4;
@@ -67,7 +70,7 @@ constexpr int kLdsBytes = kRingBytes + 1024;
 // Output staging in the epilogue (reuses the rings): 32 rows of 4 heads x
 // 256 dims, rows padded by 16 bytes against bank conflicts of the lane writes.
 constexpr int kStagePitch = 4 * 256 + 8;   // bf16
-static_assert(32 * kStagePitch * 2 <= kRingBytes, "output stage fits the rings");
+static_assert(32 * kStagePitch * 2 <= 2 * kTileV, "output stage fits the V ring");
 // Exponentials are taken against a per-row reference fixed by the first KV
 // tile; a later score may exceed it by a factor up to 2^64 (P stays finite in
 // bf16 and fp32).  Beyond that the block is recomputed exactly.
@@ -108,6 +111,10 @@ __device__ __forceinline__ u32x4_t ds_read_b128_at(uint32_t lds_addr) {
   u32x4_t r;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(lds_addr), "i"(kOff));
   return r;
+}
+template <int kOff>
+__device__ __forceinline__ void ds_write_b128_at(uint32_t lds_addr, const u32x4_t &v) {
+  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(lds_addr), "v"(v), "i"(kOff) : "memory");
 }
 template <int kN>
 __device__ __forceinline__ void lgkm_wait1(u32x4_t &a) {
@@ -238,72 +245,10 @@ void varlen_causal_prefill_kernel(
     if (ticket_order == 2) return (it & 1) ? n - 1 - (it >> 1) : (it >> 1);
     return it;
   };
-  for (;;) {
-  int b, h, qb;
-  if constexpr (kList) {
-    if (item >= n_items) {  // uniform: the queue is drained
-      // The last workgroup to get here leaves both counters at zero for the
-      // next launch (every workgroup has drawn its final ticket by then).
-      if (tid == 0 && atomicAdd(&counters[1], 1) == int(gridDim.x) - 1) {
-        __hip_atomic_store(&counters[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&counters[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      return;
-    }
-    const int tk = permute(item, n_items);
-    // slice: the last s with pre[s] <= tk (64-ary search, one probe per lane)
-    int lo = 0, hi = n_qblocks;
-    while (hi - lo > 1) {
-      const int step = (hi - lo + 63) / 64;
-      const int probe = lo + lane * step;
-      const bool le = probe < hi && pre[probe] <= tk;
-      const int k = 63 - __builtin_clzll(__ballot(le));  // lane 0 always qualifies
-      lo += k * step;
-      hi = min(lo + step, hi);
-    }
-    qb = n_qblocks - 1 - lo;
-    const int j = tk - pre[lo];
-    const int pair = j / n_kv_heads;
-    h = j - pair * n_kv_heads;
-    // b: the pair-th sequence (ascending) longer than 32 * qb
-    const int thr = qb * kBQ;
-    int seen = 0;
-    b = 0;
-    for (int b0 = 0; b0 < n_seq; b0 += 64) {
-      const uint64_t m = __ballot(b0 + lane < n_seq && lens[b0 + lane] > thr);
-      const int c = __popcll(m);
-      if (pair < seen + c) {
-        // position of the (pair - seen)-th set bit of m
-        const bool mine = ((m >> lane) & 1) &&
-                          __popcll(m & ((uint64_t(1) << lane) - 1)) == pair - seen;
-        b = b0 + (__builtin_ctzll(__ballot(mine)));
-        break;
-      }
-      seen += c;
-    }
-  } else {
-    const int it = permute(item, int(gridDim.x));
-    const int slice = it / bh_count;
-    const int bh = it - slice * bh_count;
-    b = bh / n_kv_heads;
-    h = bh - b * n_kv_heads;
-    qb = n_qblocks - 1 - slice;
-  }
-  int next_ticket = 0;
-  if (kList && tid == 0) next_ticket = atomicAdd(&counters[0], 1);
-  const int start = kList ? cu_l[b] : cu[b];
-  const int n = kList ? lens[b] : cu[b + 1] - start;
-  const int q0 = qb * kBQ;
-  if (q0 >= n) return;  // direct launch only (the queue holds active blocks only)
-
-  const int hq = h * kG + wave;
-  const int qrow = q0 + col;
-
-  const bf16_t *kseq = k + int64_t(start) * ks_t + h * ks_h;
-  const bf16_t *vseq = v + int64_t(start) * vs_t + h * vs_h;
-  const int kv_end = min(q0 + kBQ, n);  // exclusive bound of keys any row can see
-  const int n_tiles = (kv_end + kBN - 1) / kBN;
-
+#if WY_TRACE
+  int trace_k = 0;
+  unsigned long long tr0 = 0, tr1 = 0, tr2 = 0, trm = 0, trq = 0, tre = 0, trs = 0, tpf = 0, tsw = 0;
+#endif
   // DMA one tile into a ring slot as wave-wide 1 KiB blocks (lane j fills
   // 16-byte slot 64*blk + j; pad slots get the row's first chunk, unread).
   // Wave w issues blocks w, w+4, ...  The DMAs are buffer loads over the
@@ -333,29 +278,124 @@ void varlen_causal_prefill_kernel(
     const int c = sl - row * kVSlots;
     v_voff[i] = uint32_t(row) * v_row_bytes + uint32_t(c < kD / 8 ? c : 0) * 16u;
   }
-  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t *>(kseq), 0, int(uint32_t(n - 1) * k_row_bytes + kD * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<bf16_t *>(vseq), 0, int(uint32_t(n - 1) * v_row_bytes + kD * 2), 0x00020000);
-  // Issue K blocks [i0, i1) of this wave for tile t into `slot`.
-  auto issue_k = [&](int t, int slot, int i0, int i1) {
+  // Queue launch: ticket -> (sequence, KV head, query block).
+  auto map_ticket = [&](int it, int &b_, int &h_, int &qb_) {
+    const int tk = permute(it, n_items);
+    // slice: the last s with pre[s] <= tk (64-ary search, one probe per lane)
+    int lo = 0, hi = n_qblocks;
+    while (hi - lo > 1) {
+      const int step = (hi - lo + 63) / 64;
+      const int probe = lo + lane * step;
+      const bool le = probe < hi && pre[probe] <= tk;
+      const int k = 63 - __builtin_clzll(__ballot(le));  // lane 0 always qualifies
+      lo += k * step;
+      hi = min(lo + step, hi);
+    }
+    qb_ = n_qblocks - 1 - lo;
+    const int j = tk - pre[lo];
+    const int pair = j / n_kv_heads;
+    h_ = j - pair * n_kv_heads;
+    // b: the pair-th sequence (ascending) longer than 32 * qb
+    const int thr = qb_ * kBQ;
+    int seen = 0;
+    b_ = 0;
+    for (int b0 = 0; b0 < n_seq; b0 += 64) {
+      const uint64_t m = __ballot(b0 + lane < n_seq && lens[b0 + lane] > thr);
+      const int c = __popcll(m);
+      if (pair < seen + c) {
+        // position of the (pair - seen)-th set bit of m
+        const bool mine = ((m >> lane) & 1) &&
+                          __popcll(m & ((uint64_t(1) << lane) - 1)) == pair - seen;
+        b_ = b0 + (__builtin_ctzll(__ballot(mine)));
+        break;
+      }
+      seen += c;
+    }
+  };
+  // Block coordinates.  In the queue launch the epilogue of a block maps the
+  // next ticket and requests that block's q rows and first K tiles before
+  // its own output stores (`pf`): the memory counter completes in order, so
+  // requested after the stores they would wait for them.
+  int b = 0, h = 0, qb = 0;
+  bool pf = false;
+  u32x4_t xr_pf[16];
+  // q rows of a block in the row layout (rows past the sequence re-read its
+  // last row; zeroed after the regrouping).
+  auto load_q_rows = [&](int start_, int n_, int q0_, int h_) {
+    const int last = n_ - 1 - q0_;
+    const bf16_t *qp = q + (int64_t(start_) + q0_) * qs_t + (h_ * kG + wave) * qs_h + (lane & 31) * 8;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      xr_pf[i] = ld16(qp + int64_t(min(2 * i + (lane >> 5), last)) * qs_t);
+  };
+  auto mk_rsrc = [&](const bf16_t *base, int64_t st_t, int64_t st_h, int start_, int n_, int h_,
+                     uint32_t row_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t *>(base + int64_t(start_) * st_t + h_ * st_h), 0,
+        int(uint32_t(n_ - 1) * row_bytes + kD * 2), 0x00020000);
+  };
+  auto dma_k = [&](__amdgpu_buffer_rsrc_t rs, int t, int slot, int i0, int i1) {
     const uint32_t soff = uint32_t(t * kBN) * k_row_bytes;
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
       if (wave + 4 * i < kKDma)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            k_rsrc, (lds_void_t *)(k_ring + slot * kTileK + (wave + 4 * i) * 1024), 16,
-            k_voff[i], soff, 0, 0);
+            rs, (lds_void_t *)(k_ring + slot * kTileK + (wave + 4 * i) * 1024), 16, k_voff[i],
+            soff, 0, 0);
     }
   };
-  auto issue_v = [&](int t, int slot, int i0, int i1) {
+  auto dma_v = [&](__amdgpu_buffer_rsrc_t rs, int t, int slot, int i0, int i1) {
     const uint32_t soff = uint32_t(t * kBN) * v_row_bytes;
 #pragma unroll
     for (int i = i0; i < i1; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          v_rsrc, (lds_void_t *)(v_ring + slot * kTileV + (wave + 4 * i) * 1024), 16,
-          v_voff[i], soff, 0, 0);
+          rs, (lds_void_t *)(v_ring + slot * kTileV + (wave + 4 * i) * 1024), 16, v_voff[i],
+          soff, 0, 0);
   };
+  // the next ticket: every thread issues the atomic, only thread 0's offset
+  // lies inside the 4-byte range (a branch around it would make the merge of
+  // its result wait for every memory operation in flight)
+  const __amdgpu_buffer_rsrc_t ticket_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(counters, 0, 4, 0x00020000);
+  for (;;) {
+#if WY_TRACE
+  tr0 = __builtin_amdgcn_s_memrealtime();
+#endif
+  if constexpr (kList) {
+    if (item >= n_items) {  // uniform: the queue is drained
+      // The last workgroup to get here leaves both counters at zero for the
+      // next launch (every workgroup has drawn its final ticket by then).
+      if (tid == 0 && atomicAdd(&counters[1], 1) == int(gridDim.x) - 1) {
+        __hip_atomic_store(&counters[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&counters[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
+    if (!pf) map_ticket(item, b, h, qb);
+  } else {
+    const int it = permute(item, int(gridDim.x));
+    const int slice = it / bh_count;
+    const int bh = it - slice * bh_count;
+    b = bh / n_kv_heads;
+    h = bh - b * n_kv_heads;
+    qb = n_qblocks - 1 - slice;
+  }
+  const int start = kList ? cu_l[b] : cu[b];
+  const int n = kList ? lens[b] : cu[b + 1] - start;
+  const int q0 = qb * kBQ;
+  if (q0 >= n) return;  // direct launch only (the queue holds active blocks only)
+
+  const int hq = h * kG + wave;
+  const int qrow = q0 + col;
+
+  const int kv_end = min(q0 + kBQ, n);  // exclusive bound of keys any row can see
+  const int n_tiles = (kv_end + kBN - 1) / kBN;
+
+  const __amdgpu_buffer_rsrc_t k_rsrc = mk_rsrc(k, ks_t, ks_h, start, n, h, k_row_bytes);
+  const __amdgpu_buffer_rsrc_t v_rsrc = mk_rsrc(v, vs_t, vs_h, start, n, h, v_row_bytes);
+  // Issue K (V) blocks [i0, i1) of this wave for tile t into `slot`.
+  auto issue_k = [&](int t, int slot, int i0, int i1) { dma_k(k_rsrc, t, slot, i0, i1); };
+  auto issue_v = [&](int t, int slot, int i0, int i1) { dma_v(v_rsrc, t, slot, i0, i1); };
   auto issue_first = [&] {
     issue_k(0, 0, 0, kKPerWave);
     issue_v(0, 0, 0, kVPerWave);
@@ -365,7 +405,7 @@ void varlen_causal_prefill_kernel(
   // V rows past the sequence's end are not fetched; their P is 0, so their
   // LDS rows only need to hold finite values: zero the V ring once when the
   // last tile is partial.
-  if (n < n_tiles * kBN) {
+  if (!pf && n < n_tiles * kBN) {
     for (int o = tid * 16; o < 2 * kTileV; o += 256 * 16)
       st16(v_ring + o, u32x4_t{0u, 0u, 0u, 0u});
     __syncthreads();
@@ -378,6 +418,9 @@ void varlen_causal_prefill_kernel(
   // 32 rows whole (two 512-byte rows per load instruction) and regroups them
   // through LDS into the lanes' 16-byte slices: the V slot of tile 1, not
   // written before the first tile loop, holds two waves' rows at a time.
+#if WY_TRACE
+  trm = __builtin_amdgcn_s_memrealtime();
+#endif
   bf16x8_t qb_op[16];
   // Attention block: the gate values of the pieces this thread stores in the
   // epilogue (rows r0, r0 + 2, ..., 16 bytes at column c8 of the 4 heads'
@@ -387,19 +430,12 @@ void varlen_causal_prefill_kernel(
   const int r0 = tid >> 7, c8 = (tid & 127) * 8;
   u32x4_t gate_c[kRot > 0 ? kBQ / 2 : 1];
   {
-    const int qc = qrow < n ? qrow : n - 1;
-    u32x4_t xr[16];
-    {
-      // rows past the sequence re-read its last row (zeroed below)
-      const int last = n - 1 - q0;
-      const bf16_t *qp = q + (int64_t(start) + q0) * qs_t + hq * qs_h + (lane & 31) * 8;
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        xr[i] = ld16(qp + int64_t(min(2 * i + (lane >> 5), last)) * qs_t);
-    }
-    // the row's sin / cos for its rotary dims (written by the K/V launch)
+    // (a prefetched block's rows were requested by the previous epilogue)
+    if (!pf) load_q_rows(start, n, q0, h);
+    u32x4_t(&xr)[16] = xr_pf;
     f32x4_t tsn[kRot > 0 ? kRot / 16 : 1], tcs[kRot > 0 ? kRot / 16 : 1];
     if constexpr (kRot > 0) {
+      const int qc = qrow < n ? qrow : n - 1;
       const float *tr = blk.rope_tab + (int64_t(start) + qc) * kRot + 8 * g;
 #pragma unroll
       for (int kk = 0; kk < kRot / 32; ++kk)
@@ -409,7 +445,7 @@ void varlen_causal_prefill_kernel(
           tcs[2 * kk + u] = *reinterpret_cast<const f32x4_t *>(tr + kRot / 2 + 16 * kk + 4 * u);
         }
     }
-    issue_first();
+    if (!pf) issue_first();
     if constexpr (kRot > 0) {
       const int last = n - 1 - q0;   // rows past the sequence re-read its last row
       const bf16_t *gp = blk.gate + (int64_t(start) + q0) * blk.gs_t +
@@ -419,21 +455,36 @@ void varlen_causal_prefill_kernel(
         gate_c[i] = ld16(gp + int64_t(min(r0 + 2 * i, last)) * blk.gs_t);
     }
     {
-      unsigned char *const qst = v_ring + kTileV + (wave & 1) * (kBQ * kQPitch);
+      // LDS accesses as inline asm: a prefetched block's DMAs may be in
+      // flight, and the compiler would make compiler-visible accesses wait
+      // for them.
+      const uint32_t qst = lds_u32(v_ring + kTileV + (wave & 1) * (kBQ * kQPitch));
+      const uint32_t qw = qst + uint32_t((lane >> 5) * kQPitch + (lane & 31) * 16);
+      const uint32_t qr = qst + uint32_t(col * kQPitch + g * 16);
 #pragma unroll
       for (int round = 0; round < 2; ++round) {
         if ((wave >> 1) == round) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            st16(qst + (2 * i + (lane >> 5)) * kQPitch + (lane & 31) * 16, xr[i]);
-#pragma unroll
-          for (int kk = 0; kk < 16; ++kk) xr[kk] = ld16(qst + col * kQPitch + kk * 32 + g * 16);
+          static_for<0, 16>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            ds_write_b128_at<2 * i * kQPitch>(qw, xr[i]);
+          });
+          static_for<0, 16>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            xr[i] = ds_read_b128_at<i * 32>(qr);
+          });
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(xr[4]),
+                         "+v"(xr[5]), "+v"(xr[6]), "+v"(xr[7]), "+v"(xr[8]), "+v"(xr[9]),
+                         "+v"(xr[10]), "+v"(xr[11]), "+v"(xr[12]), "+v"(xr[13]), "+v"(xr[14]),
+                         "+v"(xr[15])::"memory");
           if (round == 1 && n < n_tiles * kBN) {
             // the slot must hold finite values past the sequence (see above)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-              st16(qst + (2 * i + (lane >> 5)) * kQPitch + (lane & 31) * 16,
-                   u32x4_t{0u, 0u, 0u, 0u});
+            const u32x4_t z = {0u, 0u, 0u, 0u};
+            static_for<0, 16>([&](auto ic) {
+              constexpr int i = decltype(ic)::value;
+              ds_write_b128_at<2 * i * kQPitch>(qw, z);
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           }
         }
         if (round == 0) __syncthreads();
@@ -476,6 +527,9 @@ void varlen_causal_prefill_kernel(
     }
   }
 
+#if WY_TRACE
+  trq = __builtin_amdgcn_s_memrealtime();
+#endif
   // S^T of the tile in K slot `slot`: register r of slab mt = token 32mt+16g+r.
   // dma(kb) is called after k-step block kb so the next tiles' DMA issue is
   // spread between the MFMAs instead of stalling the wave in one burst.
@@ -719,9 +773,20 @@ void varlen_causal_prefill_kernel(
     });
   };
   auto run_fast = [&] {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // K(0), V(0), K(1) landed
+    // K(0), V(0), K(1) landed.  A prefetched block's K tiles were requested
+    // before the previous block's 16 output stores; younger than them are
+    // those stores, V(0)'s DMA, (attention block) the sin / cos and gate
+    // loads, and the ticket atomic, which may still be in flight.
+    if (pf)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + kVDma / 4 + 1 + (kRot > 0 ? kRot / 8 + kBQ / 2 : 0))
+                   : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     f32x16_t s_cur[2], s_nxt[2];
+#if WY_TRACE
+    tr1 = __builtin_amdgcn_s_memrealtime();
+#endif
     qk(0, s_cur, zero16, no_dma);
     if (n_tiles == 1) mask_tile(s_cur, 0);
     {
@@ -745,18 +810,22 @@ void varlen_causal_prefill_kernel(
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K(t+1), V(t) landed
       __syncthreads();  // and every wave is done with S^T(t) and PV(t-1)
       const uint32_t kb = k_lane + uint32_t(((t + 1) & 1) * kTileK);
-      u32x4_t ka[8];
-      static_for<0, 8>([&](auto ic) { ka[ic] = k_read(kb, ic); });
+      constexpr int kKW = 8;  // K operands in flight (MFMAs ahead)
+      u32x4_t ka[kKW];
+      static_for<0, kKW>([&](auto ic) { ka[ic] = k_read(kb, ic); });
       u32x4_t pb[4];
       float psum = 0.f;
       const uint32_t vr0 = lds_u32(v_ring + (t & 1) * kTileV) + v_lane_off;
       static_for<0, 32>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         constexpr int ii = i & 7, mt = ii & 1, ks = 4 * (i >> 3) + (ii >> 1);
-        lgkm_wait1<(i < 24 ? 7 : 31 - i)>(ka[ii]);
+        constexpr int wi = i % kKW;
+        lgkm_wait1<(i + kKW <= 32 ? kKW - 1 : 31 - i)>(ka[wi]);
         s_nxt[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8_t, ka[ii]), qb_op[ks], s_nxt[mt], 0, 0, 0);
-        if constexpr (i + 8 < 32) ka[ii] = k_read(kb, std::integral_constant<int, i + 8>{});
+            __builtin_bit_cast(bf16x8_t, ka[wi]), qb_op[ks], s_nxt[mt], 0, 0, 0);
+        if constexpr (i + kKW < 32) ka[wi] = k_read(kb, std::integral_constant<int, i + kKW>{});
+        // one P pair per odd MFMA; the next tiles' DMA (K(t+2), then V(t+1))
+        // one block per MFMA
         if constexpr (i & 1) softmax_pair(s_cur, pb, psum, std::integral_constant<int, i / 2>{});
         if constexpr (i < 9) issue_k1(t + 2, t & 1, ic);
         else if constexpr (i < 18) issue_v1(t + 1, (t + 1) & 1, std::integral_constant<int, i - 9>{});
@@ -792,7 +861,16 @@ void varlen_causal_prefill_kernel(
   };
 
   zero_acc();
+  // The next ticket, drawn during the block (published to the workgroup
+  // through s_next_item before the barrier below).
+  int next_ticket = 0;
+  if constexpr (kList)
+    next_ticket = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, ticket_rsrc, tid * 4, 0, 0);
   run_fast();
+  if (kList && tid == 0) s_next_item = next_ticket;
+#if WY_TRACE
+  tr2 = __builtin_amdgcn_s_memrealtime();
+#endif
   float l = l_part + __shfl_xor(l_part, 32);
   // Some score exceeded its row's first-tile maximum by a factor over 2^64
   // (or is not finite): l is then at least 2^64.
@@ -816,7 +894,33 @@ void varlen_causal_prefill_kernel(
   // instruction then covers 1 KiB of one row instead of 32 rows.
   const float inv_l = 1.0f / l;
   __syncthreads();   // every wave is past its last K/V read of the rings
-  bf16_t *const stage = reinterpret_cast<bf16_t *>(smem);
+#if WY_TRACE
+  tre = __builtin_amdgcn_s_memrealtime();
+#endif
+  // Queue launch: the next block's coordinates and q rows, then its K tiles
+  // 0 and 1, go out before this block's output stores; V(0) follows the
+  // stores (its ring slot holds the output staging).  The LDS accesses the
+  // compiler sees (staging, gate pass, staging reads) all come before the
+  // first of these DMAs: the compiler cannot tell a DMA's LDS target from
+  // theirs and would make them wait for it.
+  int nitem = 0, nb = 0, nh = 0, nqb = 0, nn = 0, nstart = 0, ntiles = 0;
+  bool npf = false;
+  auto prefetch_q = [&] {
+    nitem = s_next_item;
+    if (nitem < n_items) {  // uniform
+      map_ticket(nitem, nb, nh, nqb);
+      nstart = cu_l[nb];
+      nn = lens[nb];
+      ntiles = (min(nqb * kBQ + kBQ, nn) + kBN - 1) / kBN;
+      load_q_rows(nstart, nn, nqb * kBQ, nh);
+      npf = true;
+    }
+  };
+  if constexpr (kList && kRot == 0) prefetch_q();
+#if WY_TRACE
+  tpf = __builtin_amdgcn_s_memrealtime();
+#endif
+  bf16_t *const stage = reinterpret_cast<bf16_t *>(v_ring);
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
@@ -825,35 +929,99 @@ void varlen_causal_prefill_kernel(
                          pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
       *reinterpret_cast<u32x2_t *>(stage + col * kStagePitch + wave * kD + dt * 32 + 8 * j + 4 * g) = w;
     }
+#if WY_TRACE
+  tsw = __builtin_amdgcn_s_memrealtime();
+#endif
   __syncthreads();
   {
     // 256 threads x 16 bytes = two rows per step; thread tid keeps its column
+#if WY_TRACE
+    trs = __builtin_amdgcn_s_memrealtime();
+#endif
     const int rows = min(kBQ, n - q0);
-    bf16_t *ob = out + (int64_t(start) + q0 + r0) * os_t + (h * kG + c8 / kD) * os_h + c8 % kD;
     const bf16_t *sp = stage + r0 * kStagePitch + c8;
+    u32x4_t wv[kBQ / 2];
 #pragma unroll
     for (int i = 0; i < kBQ / 2; ++i) {
-      u32x4_t w = ld16(sp);
+      wv[i] = ld16(sp + i * 2 * kStagePitch);
       if constexpr (kRot > 0) {
         // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
         // gate pack computes it
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          w[e] = pack_bf16x2(bf16_lo(w[e]) * gate_sigmoid(bf16_lo(gate_c[i][e])),
-                             bf16_hi(w[e]) * gate_sigmoid(bf16_hi(gate_c[i][e])));
+          wv[i][e] = pack_bf16x2(bf16_lo(wv[i][e]) * gate_sigmoid(bf16_lo(gate_c[i][e])),
+                                 bf16_hi(wv[i][e]) * gate_sigmoid(bf16_hi(gate_c[i][e])));
       }
-      if (r0 + 2 * i < rows) st16_nt(ob, w);
-      ob += 2 * os_t;
-      sp += 2 * kStagePitch;
+    }
+    if constexpr (kList && kRot > 0) prefetch_q();  // the gate registers are free now
+    if constexpr (kList) {
+      if (npf) {
+        const __amdgpu_buffer_rsrc_t nk = mk_rsrc(k, ks_t, ks_h, nstart, nn, nh, k_row_bytes);
+        dma_k(nk, 0, 0, 0, kKPerWave);
+        if (ntiles > 1) dma_k(nk, 1, 1, 0, kKPerWave);
+      }
+      // Buffer stores whose range ends after row `rows` - 1 (a row past it
+      // lies beyond the range, the launch checks the strides), so that every
+      // thread issues exactly 16 stores.
+      bf16_t *const ob0 = out + (int64_t(start) + q0) * os_t + (h * kG) * os_h;
+      const __amdgpu_buffer_rsrc_t o_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          ob0, 0,
+          int(uint32_t(rows - 1) * uint32_t(os_t) * 2u + uint32_t(kG - 1) * uint32_t(os_h) * 2u +
+              kD * 2),
+          0x00020000);
+      const uint32_t o_voff = uint32_t(r0) * uint32_t(os_t) * 2u +
+                              uint32_t(c8 / kD) * uint32_t(os_h) * 2u + uint32_t(c8 % kD) * 2u;
+#pragma unroll
+      for (int i = 0; i < kBQ / 2; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(wv[i], o_rsrc, o_voff,
+                                               uint32_t(2 * i) * uint32_t(os_t) * 2u, 2);
+    } else {
+      bf16_t *ob = out + (int64_t(start) + q0 + r0) * os_t + (h * kG + c8 / kD) * os_h + c8 % kD;
+#pragma unroll
+      for (int i = 0; i < kBQ / 2; ++i) {
+        if (r0 + 2 * i < rows) st16_nt(ob, wv[i]);
+        ob += 2 * os_t;
+      }
     }
   }
+#if WY_TRACE
+  if (tid == 0 && blockIdx.x < 256 && trace_k < 64) {
+    unsigned long long *tp = g_trace + (blockIdx.x * 64 + trace_k) * 8;
+    unsigned hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    tp[0] = tr0; tp[1] = tr1; tp[2] = tr2; tp[3] = __builtin_amdgcn_s_memrealtime();
+    tp[4] = (unsigned long long)(b) | ((unsigned long long)qb << 16) | ((unsigned long long)h << 32);
+    tp[5] = n_tiles | ((trm - tr0) << 8) | ((trq - tr0) << 24) | ((tre - tr2) << 40);
+    tp[6] = (trs - tr2) | ((tpf - tr2) << 16) | ((tsw - tr2) << 32); tp[7] = 1;
+  }
+  ++trace_k;
+#endif
   if constexpr (!kList) return;
-  // Every wave is past its last LDS read of this block before the next
-  // block's DMA refills the rings; s_next_item was last read before the
-  // barriers of this block's pass.
-  if (tid == 0) s_next_item = next_ticket;
-  __syncthreads();
-  item = s_next_item;
+  // Every wave is past its last read of the output staging before the next
+  // block's V(0) lands in its slot (zeroed first when that block's last tile
+  // is partial: rows past the sequence must hold finite values).  Only LDS
+  // order matters here: a bare barrier after the LDS counter, since a
+  // __syncthreads fence would also wait for the prefetched loads.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (npf) {
+    if (nn < ntiles * kBN) {
+      // as inline asm: the compiler would make these wait for the K DMAs
+      const uint32_t zb = lds_u32(v_ring) + uint32_t(tid * 16);
+      const u32x4_t z = {0u, 0u, 0u, 0u};
+      static_assert(2 * kTileV % (256 * 16) == 0 && 2 * kTileV / (256 * 16) == 18, "V ring zeroing");
+      static_for<0, 9>([&](auto ic) {
+        ds_write_b128_at<decltype(ic)::value * 4096>(zb, z);
+        ds_write_b128_at<decltype(ic)::value * 4096>(zb + 9 * 4096, z);
+      });
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    dma_v(mk_rsrc(v, vs_t, vs_h, nstart, nn, nh, v_row_bytes), 0, 0, 0, kVPerWave);
+  }
+  item = nitem;
+  b = nb;
+  h = nh;
+  qb = nqb;
+  pf = npf;
   }
 }
 
@@ -939,7 +1107,11 @@ int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_
   const int64_t need = wy_varlen_causal_prefill_workspace_bytes(batch, num_kv_heads, max_seqlen);
   int32_t *counters = nullptr;
   unsigned grid = unsigned(n_wg);
-  if (need > 0 && workspace_bytes >= need) {
+  // The queue launch's output stores run over a buffer range that ends
+  // after the block's last row: a row past it must lie beyond the range,
+  // i.e. the row stride covers the four heads' spans.
+  const bool rows_disjoint = os[0] >= (kG - 1) * os[1] + kD && os[0] * 2 * kBQ < INT32_MAX;
+  if (need > 0 && workspace_bytes >= need && rows_disjoint) {
     counters = static_cast<int32_t *>(workspace);
     grid = unsigned(device_cus());
   }
@@ -956,6 +1128,15 @@ int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_
 
 }  // namespace
 
+#if WY_TRACE
+extern "C" int wy_prefill_trace_read(void *host, size_t bytes, int clear) {
+  if (clear) {
+    static unsigned long long zeros[256 * 64 * 8];
+    return int(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), zeros, sizeof(zeros)));
+  }
+  return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes < sizeof(g_trace) ? bytes : sizeof(g_trace)));
+}
+#endif
 extern "C" void wy_prefill_set_ticket_order(int order) {
   g_ticket_order.store(order >= 0 && order <= 2 ? order : 0, std::memory_order_relaxed);
 }

@@ -76,8 +76,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 // partial_rope.py:97-98.
 __device__ __forceinline__ void rope_rotate(float x1, float x2, float c, float s, float &o1,
                                             float &o2) {
-  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  o2 = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
+  // Plain operators under contract(off): the _rn intrinsics come from the
+  // device library with contraction allowed, and after inlining the compiler
+  // fused one of the products into the add -- a different one depending on
+  // the calling kernel's schedule, so kernels rotating the same values
+  // (standalone partial RoPE, K/V fill, prefill and decode blocks) could
+  // round apart.
+#pragma clang fp contract(off)
+  o1 = x1 * c - x2 * s;
+  o2 = x1 * s + x2 * c;
 }
 // angle = float(pos) * inv_freq[j] in fp32 (partial_rope.py:74-75).
 __device__ __forceinline__ void rope_sincos(float pos, float inv_freq_j, float &s, float &c) {
