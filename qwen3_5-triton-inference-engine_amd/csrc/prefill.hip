@@ -772,17 +772,29 @@ void varlen_causal_prefill_kernel(
       __builtin_amdgcn_sched_barrier(0);
     });
   };
+  // Queue launch: the next ticket is drawn late in the block -- after the
+  // barrier of its last tile (right after the first wait in a one-tile
+  // block) -- early enough for the epilogue to map it and prefetch that
+  // block, late enough that the last tickets of the queue go to workgroups
+  // about to need them (drawn at the start of a long block, a light ticket
+  // waited for the whole block while other workgroups found the queue empty).
+  int next_ticket = 0;
+  auto draw_ticket = [&] {
+    if constexpr (kList)
+      next_ticket = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, ticket_rsrc, tid * 4, 0, 0);
+  };
   auto run_fast = [&] {
     // K(0), V(0), K(1) landed.  A prefetched block's K tiles were requested
     // before the previous block's 16 output stores; younger than them are
-    // those stores, V(0)'s DMA, (attention block) the sin / cos and gate
-    // loads, and the ticket atomic, which may still be in flight.
+    // those stores, V(0)'s DMA and (attention block) the sin / cos and gate
+    // loads, which may still be in flight.
     if (pf)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + kVDma / 4 + 1 + (kRot > 0 ? kRot / 8 + kBQ / 2 : 0))
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + kVDma / 4 + (kRot > 0 ? kRot / 8 + kBQ / 2 : 0))
                    : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (n_tiles == 1) draw_ticket();
     f32x16_t s_cur[2], s_nxt[2];
 #if WY_TRACE
     tr1 = __builtin_amdgcn_s_memrealtime();
@@ -843,6 +855,7 @@ void varlen_causal_prefill_kernel(
     if (n_tiles > 1) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V(t) landed
       __syncthreads();
+      draw_ticket();
       mask_tile(s_cur, t);
     }
     u32x4_t pb[4];
@@ -861,12 +874,8 @@ void varlen_causal_prefill_kernel(
   };
 
   zero_acc();
-  // The next ticket, drawn during the block (published to the workgroup
-  // through s_next_item before the barrier below).
-  int next_ticket = 0;
-  if constexpr (kList)
-    next_ticket = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, ticket_rsrc, tid * 4, 0, 0);
   run_fast();
+  // (published to the workgroup through s_next_item before the barrier below)
   if (kList && tid == 0) s_next_item = next_ticket;
 #if WY_TRACE
   tr2 = __builtin_amdgcn_s_memrealtime();
