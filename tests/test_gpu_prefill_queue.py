@@ -61,6 +61,7 @@ def counters(pkg, dev):
     [4096, 1, 33, 32, 31, 600, 2, 64, 65],
     [16] * 200,
     [257] * 40,
+    [16] * 1100,   # 2200 one-tile blocks, a plan of 2200 slices x sequences
 ])
 def test_queue_launch_equals_direct_launch(pkg, dev, lengths):
     say(f"prefill queue vs direct, lengths={lengths[:12]} (B={len(lengths)})")
