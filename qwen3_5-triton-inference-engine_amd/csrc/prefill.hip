@@ -192,15 +192,14 @@ void varlen_causal_prefill_kernel(
   // a CU that finishes early takes the next block at once instead of waiting
   // for the in-order dispatcher, and inactive blocks cost nothing.  Each
   // workgroup derives the ticket -> block map itself (sequence lengths and
-  // per-slice prefix counts in LDS); the next ticket is requested at the
-  // start of each block, so its latency hides behind the block.
+  // per-slice prefix counts in LDS); the next ticket is drawn late in each
+  // block, after its last tile's barrier, and mapped in the epilogue.
   int item = int(blockIdx.x);
   int n_items = 0;
   int *const lens = plan_lds;               // [n_seq] sequence lengths
   int *const cu_l = plan_lds + n_seq;       // [n_seq + 1] cu_seqlens
   int *const pre = cu_l + n_seq + 1;        // [n_qblocks + 1] tickets before slice s
   if constexpr (kList) {
-    if (tid == 0) s_next_item = atomicAdd(&counters[0], 1);
     for (int i = tid; i <= n_seq; i += 256) {
       const int c0 = cu[i];
       cu_l[i] = c0;
@@ -236,7 +235,9 @@ void varlen_causal_prefill_kernel(
     if (tid == 0) pre[0] = 0;
     __syncthreads();
     n_items = pre[n_qblocks];
-    item = s_next_item;
+    // The first ticket of workgroup i is i; the counter numbers the later
+    // draws (ticket gridDim.x + counter), so no workgroup starts behind 255
+    // others' atomics on one address.
   }
   // Test hook (wy_prefill_set_ticket_order): the same blocks in another
   // order.  0 heaviest first; 1 lightest first; 2 alternately from both ends.
@@ -876,7 +877,7 @@ void varlen_causal_prefill_kernel(
   zero_acc();
   run_fast();
   // (published to the workgroup through s_next_item before the barrier below)
-  if (kList && tid == 0) s_next_item = next_ticket;
+  if (kList && tid == 0) s_next_item = next_ticket + int(gridDim.x);
 #if WY_TRACE
   tr2 = __builtin_amdgcn_s_memrealtime();
 #endif
