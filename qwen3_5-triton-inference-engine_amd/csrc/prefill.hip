@@ -785,12 +785,12 @@ void varlen_causal_prefill_kernel(
       next_ticket = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, ticket_rsrc, tid * 4, 0, 0);
   };
   auto run_fast = [&] {
-    // K(0), V(0), K(1) landed.  A prefetched block's K tiles were requested
-    // before the previous block's 16 output stores; younger than them are
-    // those stores, V(0)'s DMA and (attention block) the sin / cos and gate
+    // K(0), V(0), K(1) landed.  A prefetched block's q rows and tiles were
+    // requested before the previous block's 16 output stores; younger than
+    // them are those stores and (attention block) the sin / cos and gate
     // loads, which may still be in flight.
     if (pf)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + kVDma / 4 + (kRot > 0 ? kRot / 8 + kBQ / 2 : 0))
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + (kRot > 0 ? kRot / 8 + kBQ / 2 : 0))
                    : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -908,8 +908,8 @@ void varlen_causal_prefill_kernel(
   tre = __builtin_amdgcn_s_memrealtime();
 #endif
   // Queue launch: the next block's coordinates and q rows, then its K tiles
-  // 0 and 1, go out before this block's output stores; V(0) follows the
-  // stores (its ring slot holds the output staging).  The LDS accesses the
+  // 0 and 1, then (once every wave has read the output staging out of its
+  // ring slot) its V tile 0 go out before this block's output stores.  The LDS accesses the
   // compiler sees (staging, gate pass, staging reads) all come before the
   // first of these DMAs: the compiler cannot tell a DMA's LDS target from
   // theirs and would make them wait for it.
@@ -981,6 +981,29 @@ void varlen_causal_prefill_kernel(
           0x00020000);
       const uint32_t o_voff = uint32_t(r0) * uint32_t(os_t) * 2u +
                               uint32_t(c8 / kD) * uint32_t(os_h) * 2u + uint32_t(c8 % kD) * 2u;
+      // Every wave is past its last read of the output staging before the
+      // next block's V(0) lands in its slot (zeroed first when that block's
+      // last tile is partial: rows past the sequence must hold finite
+      // values).  Only LDS order matters here: a bare barrier after the LDS
+      // counter, since a __syncthreads fence would also wait for the
+      // prefetched loads.  V(0) goes out before the stores, so the next
+      // block's first wait leaves only the stores in flight.
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (npf) {
+        if (nn < ntiles * kBN) {
+          // as inline asm: the compiler would make these wait for the K DMAs
+          const uint32_t zb = lds_u32(v_ring) + uint32_t(tid * 16);
+          const u32x4_t z = {0u, 0u, 0u, 0u};
+          static_assert(2 * kTileV % (256 * 16) == 0 && 2 * kTileV / (256 * 16) == 18,
+                        "V ring zeroing");
+          static_for<0, 9>([&](auto ic) {
+            ds_write_b128_at<decltype(ic)::value * 4096>(zb, z);
+            ds_write_b128_at<decltype(ic)::value * 4096>(zb + 9 * 4096, z);
+          });
+          asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+        dma_v(mk_rsrc(v, vs_t, vs_h, nstart, nn, nh, v_row_bytes), 0, 0, 0, kVPerWave);
+      }
 #pragma unroll
       for (int i = 0; i < kBQ / 2; ++i)
         __builtin_amdgcn_raw_buffer_store_b128(wv[i], o_rsrc, o_voff,
@@ -1007,26 +1030,6 @@ void varlen_causal_prefill_kernel(
   ++trace_k;
 #endif
   if constexpr (!kList) return;
-  // Every wave is past its last read of the output staging before the next
-  // block's V(0) lands in its slot (zeroed first when that block's last tile
-  // is partial: rows past the sequence must hold finite values).  Only LDS
-  // order matters here: a bare barrier after the LDS counter, since a
-  // __syncthreads fence would also wait for the prefetched loads.
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (npf) {
-    if (nn < ntiles * kBN) {
-      // as inline asm: the compiler would make these wait for the K DMAs
-      const uint32_t zb = lds_u32(v_ring) + uint32_t(tid * 16);
-      const u32x4_t z = {0u, 0u, 0u, 0u};
-      static_assert(2 * kTileV % (256 * 16) == 0 && 2 * kTileV / (256 * 16) == 18, "V ring zeroing");
-      static_for<0, 9>([&](auto ic) {
-        ds_write_b128_at<decltype(ic)::value * 4096>(zb, z);
-        ds_write_b128_at<decltype(ic)::value * 4096>(zb + 9 * 4096, z);
-      });
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    }
-    dma_v(mk_rsrc(v, vs_t, vs_h, nstart, nn, nh, v_row_bytes), 0, 0, 0, kVPerWave);
-  }
   item = nitem;
   b = nb;
   h = nh;
