@@ -320,14 +320,20 @@ void varlen_causal_prefill_kernel(
   int b = 0, h = 0, qb = 0;
   bool pf = false;
   u32x4_t xr_pf[16];
-  // q rows of a block in the row layout (rows past the sequence re-read its
-  // last row; zeroed after the regrouping).
+  // q rows of a block in the row layout: buffer loads over a range that ends
+  // after the sequence's last row, so rows past it read zeros; the row step
+  // is the scalar offset, the lane's place in a row pair the only vector
+  // offset (per-row clamped addresses were hoisted out of the block loop by
+  // the compiler and spilled).
   auto load_q_rows = [&](int start_, int n_, int q0_, int h_) {
-    const int last = n_ - 1 - q0_;
-    const bf16_t *qp = q + (int64_t(start_) + q0_) * qs_t + (h_ * kG + wave) * qs_h + (lane & 31) * 8;
+    const uint32_t row_b = uint32_t(qs_t) * 2u;
+    const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t *>(q + (int64_t(start_) + q0_) * qs_t + (h_ * kG + wave) * qs_h), 0,
+        int(uint32_t(n_ - 1 - q0_) * row_b + kD * 2), 0x00020000);
+    const uint32_t vo = uint32_t(lane >> 5) * row_b + uint32_t(lane & 31) * 16u;
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-      xr_pf[i] = ld16(qp + int64_t(min(2 * i + (lane >> 5), last)) * qs_t);
+      xr_pf[i] = __builtin_amdgcn_raw_buffer_load_b128(qr, vo, uint32_t(2 * i) * row_b, 0);
   };
   auto mk_rsrc = [&](const bf16_t *base, int64_t st_t, int64_t st_h, int start_, int n_, int h_,
                      uint32_t row_bytes) {
@@ -425,11 +431,27 @@ void varlen_causal_prefill_kernel(
   bf16x8_t qb_op[16];
   // Attention block: the gate values of the pieces this thread stores in the
   // epilogue (rows r0, r0 + 2, ..., 16 bytes at column c8 of the 4 heads'
-  // 2 KiB row), requested with q so that their latency is hidden behind the
-  // block; whole rows per load instruction.
+  // 2 KiB row), whole rows per load instruction.  Requested after the
+  // block's last QK, when the q operand's registers are free, so that the
+  // 64 registers they take are not held through the tile loop, and the last
+  // tile's softmax and PV hide their latency.
   static_assert(kG * kD == 1024, "two output rows per workgroup step");
   const int r0 = tid >> 7, c8 = (tid & 127) * 8;
   u32x4_t gate_c[kRot > 0 ? kBQ / 2 : 1];
+  auto load_gate = [&] {
+    if constexpr (kRot > 0) {
+      // (the range ends after the last row's fourth head: every byte in it
+      // lies inside the gate tensor; rows past the sequence are not stored)
+      const uint32_t row_b = uint32_t(blk.gs_t) * 2u, head_b = uint32_t(blk.gs_h) * 2u;
+      const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<bf16_t *>(blk.gate + (int64_t(start) + q0) * blk.gs_t + (h * kG) * blk.gs_h),
+          0, int(uint32_t(n - 1 - q0) * row_b + (kG - 1) * head_b + kD * 2), 0x00020000);
+      const uint32_t vo = uint32_t(r0) * row_b + uint32_t(c8 / kD) * head_b + uint32_t(c8 % kD) * 2u;
+#pragma unroll
+      for (int i = 0; i < kBQ / 2; ++i)
+        gate_c[i] = __builtin_amdgcn_raw_buffer_load_b128(gr, vo, uint32_t(2 * i) * row_b, 0);
+    }
+  };
   {
     // (a prefetched block's rows were requested by the previous epilogue)
     if (!pf) load_q_rows(start, n, q0, h);
@@ -447,14 +469,6 @@ void varlen_causal_prefill_kernel(
         }
     }
     if (!pf) issue_first();
-    if constexpr (kRot > 0) {
-      const int last = n - 1 - q0;   // rows past the sequence re-read its last row
-      const bf16_t *gp = blk.gate + (int64_t(start) + q0) * blk.gs_t +
-                         (h * kG + c8 / kD) * blk.gs_h + c8 % kD;
-#pragma unroll
-      for (int i = 0; i < kBQ / 2; ++i)
-        gate_c[i] = ld16(gp + int64_t(min(r0 + 2 * i, last)) * blk.gs_t);
-    }
     {
       // LDS accesses as inline asm: a prefetched block's DMAs may be in
       // flight, and the compiler would make compiler-visible accesses wait
@@ -787,11 +801,10 @@ void varlen_causal_prefill_kernel(
   auto run_fast = [&] {
     // K(0), V(0), K(1) landed.  A prefetched block's q rows and tiles were
     // requested before the previous block's 16 output stores; younger than
-    // them are those stores and (attention block) the sin / cos and gate
-    // loads, which may still be in flight.
+    // them are those stores and (attention block) the sin / cos loads,
+    // which may still be in flight.
     if (pf)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + (kRot > 0 ? kRot / 8 + kBQ / 2 : 0))
-                   : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + (kRot > 0 ? kRot / 8 : 0)) : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -859,6 +872,7 @@ void varlen_causal_prefill_kernel(
       draw_ticket();
       mask_tile(s_cur, t);
     }
+    load_gate();
     u32x4_t pb[4];
     float psum = 0.f;
     static_for<0, 16>([&](auto pc) { softmax_pair(s_cur, pb, psum, pc); });
@@ -924,6 +938,11 @@ void varlen_causal_prefill_kernel(
       ntiles = (min(nqb * kBQ + kBQ, nn) + kBN - 1) / kBN;
       load_q_rows(nstart, nn, nqb * kBQ, nh);
       npf = true;
+    } else {
+      // (defined on both paths: otherwise this block's q rows would stay
+      // live through its whole tile loop for the path without a next block)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xr_pf[i] = u32x4_t{0u, 0u, 0u, 0u};
     }
   };
   if constexpr (kList && kRot == 0) prefetch_q();
@@ -1112,7 +1131,10 @@ int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_
   const int64_t n_wg = prefill_blocks(batch, num_kv_heads, max_seqlen);
   if (n_wg > INT32_MAX) return WY_E_SHAPE;
   // per-sequence DMA ranges are 32-bit byte offsets
-  if (int64_t(max_seqlen) * ks[0] * 2 >= INT32_MAX || int64_t(max_seqlen) * vs[0] * 2 >= INT32_MAX)
+  if (int64_t(max_seqlen) * ks[0] * 2 >= INT32_MAX || int64_t(max_seqlen) * vs[0] * 2 >= INT32_MAX ||
+      int64_t(max_seqlen) * qs[0] * 2 >= INT32_MAX)
+    return WY_E_SHAPE;
+  if (kRot > 0 && int64_t(max_seqlen) * blk.gs_t * 2 + int64_t(kG) * blk.gs_h * 2 >= INT32_MAX)
     return WY_E_SHAPE;
   // Queue launch when the caller provides the two counters that
   // wy_varlen_causal_prefill_workspace_bytes asks for; otherwise one
