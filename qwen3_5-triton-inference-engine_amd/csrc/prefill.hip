@@ -153,6 +153,28 @@ struct BlockArgs {
   const float *rope_tab;  // [T][kRot]: sin of the kRot/2 angles, then cos
 };
 
+// One LDS DMA as inline asm: lane l's 16 bytes at buffer offset voff + soff
+// land at LDS address m0 + 16 l.  The compiler does not see it, so it inserts
+// no wait for it before its own LDS accesses; the kernel waits for it
+// explicitly (s_waitcnt vmcnt) before any read of its target.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_lds_asm(__amdgpu_buffer_rsrc_t rs, uint32_t m0, uint32_t voff,
+                                              uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %3 offen lds"
+               ::"v"(voff), "s"(rs), "s"(m0), "s"(soff)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int kOff>
+__device__ __forceinline__ void ds_write_b32_at(uint32_t addr, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(kOff) : "memory");
+}
+template <int kOff>
+__device__ __forceinline__ void ds_write_b64_at(uint32_t addr, u32x2_t v) {
+  asm volatile("ds_write_b64 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(kOff) : "memory");
+}
+
 template <bool kList, int kRot>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void varlen_causal_prefill_kernel(
@@ -165,6 +187,7 @@ void varlen_causal_prefill_kernel(
     int ticket_order) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int s_next_item;
+  __shared__ __align__(16) uint32_t s_over[4];
   __shared__ int s_scan[256];
   __shared__ int plan_lds[kPlanLds];
 
@@ -313,10 +336,10 @@ void varlen_causal_prefill_kernel(
       seen += c;
     }
   };
-  // Block coordinates.  In the queue launch the epilogue of a block maps the
-  // next ticket and requests that block's q rows and first K tiles before
-  // its own output stores (`pf`): the memory counter completes in order, so
-  // requested after the stores they would wait for them.
+  // Block coordinates.  In the queue launch a block maps the next ticket and
+  // requests that block's q rows and first tiles before its own output
+  // stores (`pf`): the memory counter completes in order, so requested after
+  // the stores they would wait for them.
   int b = 0, h = 0, qb = 0;
   bool pf = false;
   u32x4_t xr_pf[16];
@@ -787,24 +810,72 @@ void varlen_causal_prefill_kernel(
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  // Queue launch: the next ticket is drawn late in the block -- after the
-  // barrier of its last tile (right after the first wait in a one-tile
-  // block) -- early enough for the epilogue to map it and prefetch that
-  // block, late enough that the last tickets of the queue go to workgroups
-  // about to need them (drawn at the start of a long block, a light ticket
-  // waited for the whole block while other workgroups found the queue empty).
+  int nitem = 0, nb = 0, nh = 0, nqb = 0, nn = 0, nstart = 0, ntiles = 0;
+  bool npf = false;
+  auto prefetch_q = [&] {
+    nitem = s_next_item;
+    if (nitem < n_items) {  // uniform
+      map_ticket(nitem, nb, nh, nqb);
+      nstart = cu_l[nb];
+      nn = lens[nb];
+      ntiles = (min(nqb * kBQ + kBQ, nn) + kBN - 1) / kBN;
+      load_q_rows(nstart, nn, nqb * kBQ, nh);
+      npf = true;
+    } else {
+      // (defined on both paths: otherwise this block's q rows would stay
+      // live through its whole tile loop for the path without a next block)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xr_pf[i] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  // Plain queue launch (kEarly): the next block's coordinates, q rows and K
+  // tiles 0 and 1 are requested right after the barrier of this block's
+  // last tile -- the K ring is free once every wave has computed the last
+  // S^T -- so that their latency hides behind the last tile's softmax and PV
+  // and the epilogue.  Its K DMAs are inline asm, and every LDS access after
+  // them is too (the exact-fallback vote, the staging): the compiler would
+  // make a visible LDS access wait for a DMA it knows of, and with it, by
+  // the in-order memory counter, for the q rows.
+  constexpr bool kEarly = kList && kRot == 0;
+  auto prefetch_k = [&] {
+    if (npf) {
+      const __amdgpu_buffer_rsrc_t nk = mk_rsrc(k, ks_t, ks_h, nstart, nn, nh, k_row_bytes);
+#pragma unroll
+      for (int slot = 0; slot < 2; ++slot) {
+        if (slot == 1 && ntiles < 2) break;
+        const uint32_t soff = uint32_t(slot * kBN) * k_row_bytes;
+#pragma unroll
+        for (int i = 0; i < kKPerWave; ++i)
+          dma16_lds_asm(nk,
+                        wave + 4 * i < kKDma
+                            ? lds_u32(k_ring + slot * kTileK + (wave + 4 * i) * 1024)
+                            : lds_u32(smem + kRingBytes),
+                        k_voff[i], soff);
+      }
+    }
+  };
+  // Queue launch: the next ticket is drawn late in the block -- at the top
+  // of its last loop iteration (kEarly) or after the barrier of its last
+  // tile, right after the first wait in a one-tile block -- early enough to
+  // map it and prefetch that block, late enough that the last tickets of the
+  // queue go to workgroups about to need them (drawn at the start of a long
+  // block, a light ticket waited for the whole block while other workgroups
+  // found the queue empty).
   int next_ticket = 0;
   auto draw_ticket = [&] {
     if constexpr (kList)
       next_ticket = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, ticket_rsrc, tid * 4, 0, 0);
   };
   auto run_fast = [&] {
-    // K(0), V(0), K(1) landed.  A prefetched block's q rows and tiles were
-    // requested before the previous block's 16 output stores; younger than
-    // them are those stores and (attention block) the sin / cos loads,
-    // which may still be in flight.
+    // q, K(0), K(1) landed (and V(0), unless prefetched).  A prefetched
+    // block's q rows and K tiles were requested before the previous block's
+    // V(0) DMA and 16 output stores; younger than them are that DMA, the
+    // stores and (attention block) the sin / cos loads, which may still be
+    // in flight: V(0) is first read by PV(0), after the loop-top wait of
+    // tile 0, or in a one-tile block after the wait below.
     if (pf)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + (kRot > 0 ? kRot / 8 : 0)) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(16 + kVPerWave + (kRot > 0 ? kRot / 8 : 0))
+                   : "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -835,6 +906,9 @@ void varlen_causal_prefill_kernel(
     for (; t + 1 < n_tiles; ++t) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K(t+1), V(t) landed
       __syncthreads();  // and every wave is done with S^T(t) and PV(t-1)
+      if constexpr (kEarly) {
+        if (t + 2 == n_tiles) draw_ticket();  // a tile ahead of its use
+      }
       const uint32_t kb = k_lane + uint32_t(((t + 1) & 1) * kTileK);
       constexpr int kKW = 8;  // K operands in flight (MFMAs ahead)
       u32x4_t ka[kKW];
@@ -869,8 +943,22 @@ void varlen_causal_prefill_kernel(
     if (n_tiles > 1) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V(t) landed
       __syncthreads();
-      draw_ticket();
+      if constexpr (!kEarly) draw_ticket();
       mask_tile(s_cur, t);
+    }
+    // A prefetched one-tile block: its V(0) (every wave's part) has landed
+    // before PV(0) reads it; with kEarly the barrier below serves.
+    if (pf && n_tiles == 1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if constexpr (!kEarly) asm volatile("s_barrier" ::: "memory");
+    }
+    if constexpr (kEarly) {
+      // every wave is past its last S^T (the barrier above, or this one in
+      // a one-tile block) before the next block's K tiles land
+      if (tid == 0) s_next_item = next_ticket + int(gridDim.x);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      prefetch_q();
+      prefetch_k();
     }
     load_gate();
     u32x4_t pb[4];
@@ -891,7 +979,7 @@ void varlen_causal_prefill_kernel(
   zero_acc();
   run_fast();
   // (published to the workgroup through s_next_item before the barrier below)
-  if (kList && tid == 0) s_next_item = next_ticket + int(gridDim.x);
+  if (kList && !kEarly && tid == 0) s_next_item = next_ticket + int(gridDim.x);
 #if WY_TRACE
   tr2 = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -899,7 +987,13 @@ void varlen_causal_prefill_kernel(
   // Some score exceeded its row's first-tile maximum by a factor over 2^64
   // (or is not finite): l is then at least 2^64.
   const bool over = qrow < n && !(l < kHeadroomScale);
-  if (__syncthreads_or(over)) {
+  // workgroup vote: one flag per wave in LDS, as inline asm (see kEarly)
+  ds_write_b32_at<0>(lds_u32(reinterpret_cast<unsigned char *>(s_over)) + uint32_t(wave * 4),
+                     __ballot(over) != 0 ? 1u : 0u);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  u32x4_t votes = ds_read_b128_at<0>(lds_u32(reinterpret_cast<unsigned char *>(s_over)));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(votes)::"memory");
+  if (__builtin_amdgcn_readfirstlane(votes[0] | votes[1] | votes[2] | votes[3]) != 0) {
     // Cold path: some score exceeded the first tile's max by more than
     // 2^64.  Redo the block exactly: a max pass, then accumulation.
     issue_first();
@@ -909,6 +1003,13 @@ void varlen_causal_prefill_kernel(
     zero_acc();
     run_pass(std::integral_constant<int, 2>{});
     l = l_part + __shfl_xor(l_part, 32);
+    if constexpr (kEarly) {
+      // the passes reused the K ring and the q registers: request the next
+      // block's again
+      __syncthreads();
+      if (npf) load_q_rows(nstart, nn, nqb * kBQ, nh);
+      prefetch_k();
+    }
   }
 
   // ---- normalise and store: lane holds row qrow, dims dt*32 + 8j + 4g + i -------
@@ -917,62 +1018,58 @@ void varlen_causal_prefill_kernel(
   // instruction) are staged in LDS and written back as whole rows: each store
   // instruction then covers 1 KiB of one row instead of 32 rows.
   const float inv_l = 1.0f / l;
-  __syncthreads();   // every wave is past its last K/V read of the rings
+  // every wave is past its last K/V read of the rings (LDS order only)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #if WY_TRACE
   tre = __builtin_amdgcn_s_memrealtime();
 #endif
-  // Queue launch: the next block's coordinates and q rows, then its K tiles
-  // 0 and 1, then (once every wave has read the output staging out of its
-  // ring slot) its V tile 0 go out before this block's output stores.  The LDS accesses the
-  // compiler sees (staging, gate pass, staging reads) all come before the
-  // first of these DMAs: the compiler cannot tell a DMA's LDS target from
-  // theirs and would make them wait for it.
-  int nitem = 0, nb = 0, nh = 0, nqb = 0, nn = 0, nstart = 0, ntiles = 0;
-  bool npf = false;
-  auto prefetch_q = [&] {
-    nitem = s_next_item;
-    if (nitem < n_items) {  // uniform
-      map_ticket(nitem, nb, nh, nqb);
-      nstart = cu_l[nb];
-      nn = lens[nb];
-      ntiles = (min(nqb * kBQ + kBQ, nn) + kBN - 1) / kBN;
-      load_q_rows(nstart, nn, nqb * kBQ, nh);
-      npf = true;
-    } else {
-      // (defined on both paths: otherwise this block's q rows would stay
-      // live through its whole tile loop for the path without a next block)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) xr_pf[i] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  };
-  if constexpr (kList && kRot == 0) prefetch_q();
+  // Queue launch: the next block's coordinates, q rows and K tiles 0 and 1
+  // are requested before the last tile's PV (kEarly) or, in the attention
+  // block, after the staging reads (its gate registers are free then); its V
+  // tile 0 once every wave has read the output staging out of that ring
+  // slot; all before this block's output stores.  The staging's LDS accesses
+  // are inline asm: the compiler cannot tell a DMA's LDS target from theirs
+  // and would make them wait for it.
 #if WY_TRACE
   tpf = __builtin_amdgcn_s_memrealtime();
 #endif
   bf16_t *const stage = reinterpret_cast<bf16_t *>(v_ring);
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
-                         pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
-      *reinterpret_cast<u32x2_t *>(stage + col * kStagePitch + wave * kD + dt * 32 + 8 * j + 4 * g) = w;
-    }
+  {
+    const uint32_t sw = lds_u32(reinterpret_cast<unsigned char *>(stage + col * kStagePitch +
+                                                                  wave * kD + 4 * g));
+    static_for<0, 8>([&](auto dtc) {
+      constexpr int dt = decltype(dtc)::value;
+      static_for<0, 4>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
+                           pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
+        ds_write_b64_at<(dt * 32 + 8 * j) * 2>(sw, w);
+      });
+    });
+  }
 #if WY_TRACE
   tsw = __builtin_amdgcn_s_memrealtime();
 #endif
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   {
     // 256 threads x 16 bytes = two rows per step; thread tid keeps its column
 #if WY_TRACE
     trs = __builtin_amdgcn_s_memrealtime();
 #endif
     const int rows = min(kBQ, n - q0);
-    const bf16_t *sp = stage + r0 * kStagePitch + c8;
+    const uint32_t sp = lds_u32(reinterpret_cast<unsigned char *>(stage + r0 * kStagePitch + c8));
     u32x4_t wv[kBQ / 2];
+    static_assert(kBQ == 32, "16 staging reads");
+    static_for<0, kBQ / 2>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      wv[i] = ds_read_b128_at<i * 2 * kStagePitch * 2>(sp);
+    });
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(wv[0]), "+v"(wv[1]), "+v"(wv[2]), "+v"(wv[3]), "+v"(wv[4]), "+v"(wv[5]),
+                   "+v"(wv[6]), "+v"(wv[7]), "+v"(wv[8]), "+v"(wv[9]), "+v"(wv[10]), "+v"(wv[11]),
+                   "+v"(wv[12]), "+v"(wv[13]), "+v"(wv[14]), "+v"(wv[15])::"memory");
 #pragma unroll
     for (int i = 0; i < kBQ / 2; ++i) {
-      wv[i] = ld16(sp + i * 2 * kStagePitch);
       if constexpr (kRot > 0) {
         // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
         // gate pack computes it
@@ -984,7 +1081,7 @@ void varlen_causal_prefill_kernel(
     }
     if constexpr (kList && kRot > 0) prefetch_q();  // the gate registers are free now
     if constexpr (kList) {
-      if (npf) {
+      if (!kEarly && npf) {
         const __amdgpu_buffer_rsrc_t nk = mk_rsrc(k, ks_t, ks_h, nstart, nn, nh, k_row_bytes);
         dma_k(nk, 0, 0, 0, kKPerWave);
         if (ntiles > 1) dma_k(nk, 1, 1, 0, kKPerWave);
@@ -1021,7 +1118,13 @@ void varlen_causal_prefill_kernel(
           });
           asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
-        dma_v(mk_rsrc(v, vs_t, vs_h, nstart, nn, nh, v_row_bytes), 0, 0, 0, kVPerWave);
+        // as inline asm: the next block's prologue reads the plan in LDS,
+        // and the compiler would make those reads wait for this DMA (and, by
+        // the in-order counter, for everything requested before it)
+        const __amdgpu_buffer_rsrc_t nv = mk_rsrc(v, vs_t, vs_h, nstart, nn, nh, v_row_bytes);
+#pragma unroll
+        for (int i = 0; i < kVPerWave; ++i)
+          dma16_lds_asm(nv, lds_u32(v_ring + (wave + 4 * i) * 1024), v_voff[i], 0u);
       }
 #pragma unroll
       for (int i = 0; i < kBQ / 2; ++i)
