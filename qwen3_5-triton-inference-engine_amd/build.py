@@ -21,7 +21,13 @@ OBJ_DIR = PKG_DIR / "_build"
 ARCH = os.environ.get("WY_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["capi.hip", "kv_cache.hip", "rope_gate.hip", "rmsnorm.hip", "decode.hip", "prefill.hip",
-           "gemm.hip", "gdn.hip", "gdn_block.hip", "gdn_chunk.hip", "model_ops.hip"]
+           "prefill_direct.hip", "gemm.hip", "gdn.hip", "gdn_block.hip", "gdn_chunk.hip",
+           "model_ops.hip"]
+
+# Per-source extra flags.  The direct-launch prefill variants keep their MFMA
+# accumulators in VGPRs (faster there; the queue variants in prefill.hip are
+# slower with it).
+EXTRA_FLAGS = {"prefill_direct.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 # Packed fp32 VALU ops are disabled: their occasional silent miscompares on
 # this hardware pool are not worth the few percent they might buy.
@@ -47,7 +53,7 @@ def _hipcc() -> str:
 
 def _compile(hipcc: str, src: str) -> Path:
     obj = OBJ_DIR / (Path(src).stem + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
