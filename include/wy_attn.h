@@ -248,6 +248,16 @@ int64_t wy_varlen_causal_prefill_workspace_bytes(int batch, int num_kv_heads, in
 void wy_prefill_set_ticket_order(int order);
 
 /*
+ * Test hook, no counterpart in the reference: whether later
+ * wy_varlen_causal_prefill / wy_prefill_attention_block launches whose grid of
+ * query blocks fits the chip in one round and whose sequences are at most 128
+ * tokens take the eight-wave short-sequence kernel (1, the default) or the
+ * four-wave kernel (0).  The two agree within rounding, not bit for bit.
+ * Process-wide; not for concurrent use with running launches.
+ */
+void wy_prefill_set_short_path(int enable);
+
+/*
  * Prefill attention block: the reference's prefill attention sequence after
  * the q/k RMSNorm (engine/runner.py:336-384) in two launches, bit-identical
  * to it.  Replaces, in order:

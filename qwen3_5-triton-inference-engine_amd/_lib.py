@@ -95,7 +95,7 @@ _SIZE_QUERIES = ("wy_varlen_causal_prefill_workspace_bytes", "wy_gemm_2d_workspa
                  "wy_page_stream_read_waves")
 
 # test hooks returning nothing
-_HOOKS = ("wy_prefill_set_ticket_order",)
+_HOOKS = ("wy_prefill_set_ticket_order", "wy_prefill_set_short_path")
 
 EXPORTED = ("wy_status_string", "wy_build_info", *_SIGNATURES, *_SIZE_QUERIES, *_HOOKS)
 
@@ -131,6 +131,8 @@ def load() -> ctypes.CDLL:
         fn.restype = ctypes.c_int64
     lib.wy_prefill_set_ticket_order.argtypes = [_i]
     lib.wy_prefill_set_ticket_order.restype = None
+    lib.wy_prefill_set_short_path.argtypes = [_i]
+    lib.wy_prefill_set_short_path.restype = None
     _lib = lib
     return lib
 

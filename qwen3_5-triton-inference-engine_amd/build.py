@@ -21,13 +21,14 @@ OBJ_DIR = PKG_DIR / "_build"
 ARCH = os.environ.get("WY_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["capi.hip", "kv_cache.hip", "rope_gate.hip", "rmsnorm.hip", "decode.hip", "prefill.hip",
-           "prefill_direct.hip", "gemm.hip", "gdn.hip", "gdn_block.hip", "gdn_chunk.hip",
+           "prefill_direct.hip", "prefill_short.hip", "gemm.hip", "gdn.hip", "gdn_block.hip", "gdn_chunk.hip",
            "model_ops.hip"]
 
 # Per-source extra flags.  The direct-launch prefill variants keep their MFMA
 # accumulators in VGPRs (faster there; the queue variants in prefill.hip are
 # slower with it).
-EXTRA_FLAGS = {"prefill_direct.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+EXTRA_FLAGS = {"prefill_direct.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "prefill_short.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 # Packed fp32 VALU ops are disabled: their occasional silent miscompares on
 # this hardware pool are not worth the few percent they might buy.

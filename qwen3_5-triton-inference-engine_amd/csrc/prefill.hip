@@ -22,6 +22,21 @@ extern template __global__ void varlen_causal_prefill_kernel<false, 64>(
     int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
     int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters, const BlockArgs blk,
     int ticket_order);
+template <int kRot>
+__global__ void short_prefill_kernel(
+    const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h, const bf16_t *__restrict__ k,
+    int64_t ks_t, int64_t ks_h, const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h,
+    bf16_t *__restrict__ out, int64_t os_t, int64_t os_h, const int32_t *__restrict__ cu,
+    float qk_scale_log2, int n_seq, int n_kv_heads, int n_qblocks, const BlockArgs blk,
+    int ticket_order);
+extern template __global__ void short_prefill_kernel<0>(
+    const bf16_t *__restrict__, int64_t, int64_t, const bf16_t *__restrict__, int64_t, int64_t,
+    const bf16_t *__restrict__, int64_t, int64_t, bf16_t *__restrict__, int64_t, int64_t,
+    const int32_t *__restrict__, float, int, int, int, const BlockArgs, int);
+extern template __global__ void short_prefill_kernel<64>(
+    const bf16_t *__restrict__, int64_t, int64_t, const bf16_t *__restrict__, int64_t, int64_t,
+    const bf16_t *__restrict__, int64_t, int64_t, bf16_t *__restrict__, int64_t, int64_t,
+    const int32_t *__restrict__, float, int, int, int, const BlockArgs, int);
 }  // namespace wy_prefill
 
 namespace {
@@ -81,6 +96,17 @@ bool prefill_layout_ok(const void *q, const int64_t *qs, const void *k, const in
 // Order in which the launches hand out query blocks (see the kernel's
 // permute); 0 outside tests.
 std::atomic<int> g_ticket_order{0};
+// Whether one-round grids of short sequences take the eight-wave kernel
+// (prefill_short.hip); 1 outside tests.
+std::atomic<int> g_short_path{1};
+
+template <int kRot>
+int set_short_lds() {
+  static const hipError_t rc = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&short_prefill_kernel<kRot>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+  return rc == hipSuccess ? WY_OK : int(rc);
+}
 
 // Validated arguments -> one launch (direct or queue).
 template <int kRot>
@@ -115,9 +141,22 @@ int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_
     counters = static_cast<int32_t *>(workspace);
     grid = unsigned(device_cus());
   }
+  const int order = g_ticket_order.load(std::memory_order_relaxed);
+  // A one-round grid of sequences of at most two KV tiles: the eight-wave
+  // kernel (chosen by the shape alone, so an input always takes the same one).
+  if (!counters && max_seqlen <= 2 * kBN && n_wg <= device_cus() &&
+      g_short_path.load(std::memory_order_relaxed)) {
+    rc = set_short_lds<kRot>();
+    if (rc != WY_OK) return rc;
+    short_prefill_kernel<kRot><<<dim3(grid), 512, kLdsBytes, s>>>(
+        static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
+        ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],
+        os[1], cu_seqlens, kLog2e / sqrtf(float(head_dim)), batch, num_kv_heads, n_qblocks, blk,
+        order);
+    return wyh::launch_status();
+  }
   auto *kern = counters ? varlen_causal_prefill_kernel<true, kRot>
                         : varlen_causal_prefill_kernel<false, kRot>;
-  const int order = g_ticket_order.load(std::memory_order_relaxed);
   kern<<<dim3(grid), 256, kLdsBytes, s>>>(
       static_cast<const bf16_t *>(q), qs[0], qs[1], static_cast<const bf16_t *>(k), ks[0],
       ks[1], static_cast<const bf16_t *>(v), vs[0], vs[1], static_cast<bf16_t *>(out), os[0],
@@ -137,6 +176,9 @@ extern "C" int wy_prefill_trace_read(void *host, size_t bytes, int clear) {
   return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes < sizeof(g_trace) ? bytes : sizeof(g_trace)));
 }
 #endif
+extern "C" void wy_prefill_set_short_path(int enable) {
+  g_short_path.store(enable ? 1 : 0, std::memory_order_relaxed);
+}
 extern "C" void wy_prefill_set_ticket_order(int order) {
   g_ticket_order.store(order >= 0 && order <= 2 ? order : 0, std::memory_order_relaxed);
 }

@@ -23,3 +23,13 @@ template __global__ void varlen_causal_prefill_kernel<false, 64>(
     int n_kv_heads, int n_qblocks, int32_t *__restrict__ counters, const BlockArgs blk,
     int ticket_order);
 }  // namespace wy_prefill
+
+#if WY_TRACE
+extern "C" int wy_prefill_direct_trace_read(void *host, size_t bytes, int clear) {
+  if (clear) {
+    static unsigned long long zeros[256 * 64 * 8];
+    return int(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), zeros, sizeof(zeros)));
+  }
+  return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), bytes < sizeof(g_trace) ? bytes : sizeof(g_trace)));
+}
+#endif

@@ -1,0 +1,575 @@
+// Packed varlen causal GQA prefill for short sequences (every sequence at
+// most two 64-token KV tiles long) whose query blocks fit the chip in one
+// round: the direct launch of 32 x 128-token prompts and the like.
+//
+// Such a launch is latency-bound, not MFMA- or HBM-bound: every CU holds one
+// block, every block loads its q rows and K/V at once, computes, and stores,
+// and the four-wave kernel runs its block's QK -> softmax -> PV chain on one
+// wave per SIMD with the memory system idle meanwhile.  Here a block (the same
+// sequence, KV head and 32-token query block as in prefill_kernel.h) runs on
+// eight waves, a pair per query head, so each SIMD holds two waves whose
+// chains interleave:
+//   * S^T: the block's score slabs (two 32-token slabs per KV tile) are dealt
+//     to the pair -- one-tile blocks: slab mt to wave half mt; two-tile
+//     blocks: tile t to half t -- so each wave runs half of the block's QK
+//     MFMAs (K from LDS, q straight from global memory in the MFMA B layout);
+//   * the row max is exact over the whole block (the halves swap their
+//     partial maxima through LDS), so no score can outgrow the reference and
+//     the four-wave kernel's exact two-pass path is not needed;
+//   * the scores come out of the MFMAs unscaled (raw q rows as the B
+//     operand); 1/sqrt(D) in log2 units enters the exponentials' fused
+//     multiply-add, so the VALU never rescales q (a wave64 VALU instruction
+//     takes four cycles: rescaling and re-rounding q cost more than the
+//     block's MFMAs);
+//   * P (bf16, exactly as the reference rounds it) is swapped through LDS, and
+//     each half accumulates O^T for 128 of the 256 dims over every tile;
+//   * the row sum l is the halves' partial sums added in half order, so both
+//     waves of a pair normalise with the same l.
+// Results agree with the four-wave kernel to rounding (the same math, with
+// the scale applied to the scores instead of to a bf16-rounded q, and an
+// exact row max as the exponentials' reference); the launch chooses this kernel
+// by the shape alone, so a given input always takes the same kernel.
+//
+// Same LDS rings and DMA layout as prefill_kernel.h (K rows token-permuted,
+// V rows padded for the transposing reads); K/V tiles land by LDS DMA, and
+// every LDS access is inline asm with explicit waits, so the compiler adds
+// no wait for the DMAs before them.
+#include "prefill_kernel.h"
+
+namespace wy_prefill {
+
+constexpr int kSWaves = 8;
+constexpr int kSKPerWave = (kKDma + kSWaves - 1) / kSWaves;  // 5 (40 >= 33 blocks)
+constexpr int kSVPerWave = (kVDma + kSWaves - 1) / kSWaves;  // 5 (40 >= 36 blocks)
+// q staging: 4 heads x 32 rows in K-row layout, in the V ring
+constexpr int kQRows = kG * kBQ;
+constexpr int kQDma = (kQRows * kKPitch + 1023) / 1024;        // 66 blocks
+constexpr int kSQPerWave = (kQDma + kSWaves - 1) / kSWaves;    // 9
+static_assert(kQDma * 1024 <= 2 * kTileV, "q staging fits the V ring");
+// P exchange in the K ring once every wave is past its S^T: per wave two
+// units of two 1 KiB k-step blocks.
+constexpr int kXchWave = 4096;
+
+#if WY_TRACE
+// per-block phase stamps (s_memrealtime, 100 MHz), 16 per block
+namespace {
+__device__ unsigned long long g_strace[4096 * 32];
+}  // namespace
+#define WY_STAMP(i)                                                     \
+  do {                                                                  \
+    unsigned long long t_ = __builtin_amdgcn_s_memrealtime();           \
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(t_)::"memory");          \
+    unsigned long long c_ = __builtin_amdgcn_s_memtime();               \
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c_)::"memory");          \
+    if (tid == 0 && blockIdx.x < 4096) {                                \
+      g_strace[blockIdx.x * 32 + (i)] = t_;                             \
+      if ((i) >= 2 && (i) <= 5) g_strace[blockIdx.x * 32 + 7 + (i)] = c_; \
+    }                                                                   \
+  } while (0)
+#define WY_CSTAMP(i)                                                    \
+  do {                                                                  \
+    unsigned long long c_ = __builtin_amdgcn_s_memtime();               \
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(c_)::"memory");          \
+    if (tid == 0 && blockIdx.x < 4096) g_strace[blockIdx.x * 32 + (i)] = c_; \
+  } while (0)
+#else
+#define WY_CSTAMP(i) \
+  do {               \
+  } while (0)
+#define WY_STAMP(i) \
+  do {              \
+  } while (0)
+#endif
+
+__device__ __forceinline__ uint32_t ds_read_b32_at(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
+  return r;
+}
+static_assert(kSWaves * kXchWave <= 2 * kTileK, "P exchange fits the K ring");
+
+template <int kRot>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void short_prefill_kernel(
+    const bf16_t *__restrict__ q, int64_t qs_t, int64_t qs_h,
+    const bf16_t *__restrict__ k, int64_t ks_t, int64_t ks_h,
+    const bf16_t *__restrict__ v, int64_t vs_t, int64_t vs_h, bf16_t *__restrict__ out,
+    int64_t os_t, int64_t os_h, const int32_t *__restrict__ cu, float qk_scale_log2, int n_seq,
+    int n_kv_heads, int n_qblocks, const BlockArgs blk, int ticket_order) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ __align__(16) float s_mx[kSWaves * 64];
+  __shared__ __align__(16) float s_ps[kSWaves * 64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hd = wave & 3;   // query head within the GQA group
+  const int hf = wave >> 2;  // half of the pair
+  const int g = lane >> 5;
+  const int col = lane & 31;
+
+  unsigned char *const k_ring = smem;
+  unsigned char *const v_ring = smem + 2 * kTileK;
+
+  // Block of this workgroup: heaviest first, as the four-wave direct launch
+  // (test hook: ticket_order permutes the same blocks).
+  const int bh_count = n_seq * n_kv_heads;
+  int it = int(blockIdx.x);
+  const int n_items = int(gridDim.x);
+  if (ticket_order == 1) it = n_items - 1 - it;
+  else if (ticket_order == 2) it = (it & 1) ? n_items - 1 - (it >> 1) : (it >> 1);
+  const int slice = it / bh_count;
+  const int bh = it - slice * bh_count;
+  const int b = bh / n_kv_heads;
+  const int h = bh - b * n_kv_heads;
+  const int qb = n_qblocks - 1 - slice;
+  const int start = cu[b];
+  const int n = cu[b + 1] - start;
+  const int q0 = qb * kBQ;
+  if (q0 >= n) return;  // uniform over the workgroup
+  WY_STAMP(0);
+  const int qrow = q0 + col;
+  const int kv_end = min(q0 + kBQ, n);
+  const int n_tiles = (kv_end + kBN - 1) / kBN;  // 1 or 2 (the launch checks)
+  const int row_lim = min(qrow, n - 1);
+
+  // ---- requests: (RoPE table,) q rows, K tiles, V tiles -------------------
+  // Issued in this order with a fixed count per wave, so that each wait
+  // below counts exactly the younger requests it leaves in flight.
+  // Attention block: sin / cos of the q rows' RoPE (the K/V launch's table).
+  f32x4_t tsn[kRot > 0 ? kRot / 16 : 1], tcs[kRot > 0 ? kRot / 16 : 1];
+  if constexpr (kRot > 0) {
+    const int qc = qrow < n ? qrow : n - 1;
+    const float *tr = blk.rope_tab + (int64_t(start) + qc) * kRot + 8 * g;
+#pragma unroll
+    for (int kk = 0; kk < kRot / 32; ++kk)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        tsn[2 * kk + u] = *reinterpret_cast<const f32x4_t *>(tr + 16 * kk + 4 * u);
+        tcs[2 * kk + u] = *reinterpret_cast<const f32x4_t *>(tr + kRot / 2 + 16 * kk + 4 * u);
+      }
+  }
+  // q: the block's 32 rows of its 4 heads, whole rows by LDS DMA into the V
+  // ring (128 rows padded like K rows: the slice reads below are then
+  // conflict-free), read back as each lane's 16-byte slices; the V tiles
+  // follow once every wave has read its slices.  (Loaded straight into the
+  // lanes' slices, each q load instruction touched 32 rows, and the K DMAs
+  // queued behind them.)  The buffer range ends after the last row's fourth
+  // head: rows past the sequence read bytes of q that are never used.
+  const uint32_t q_row_b = uint32_t(qs_t) * 2u, q_head_b = uint32_t(qs_h) * 2u;
+  const __amdgpu_buffer_rsrc_t q_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(q + (int64_t(start) + q0) * qs_t + (h * kG) * qs_h), 0,
+      int(uint32_t(n - 1 - q0) * q_row_b + uint32_t(kG - 1) * q_head_b + kD * 2), 0x00020000);
+  unsigned char *const dummy = smem + kRingBytes;
+#pragma unroll
+  for (int i = 0; i < kSQPerWave; ++i) {
+    const int blk_i = wave + kSWaves * i;
+    const int sl = 64 * blk_i + lane;
+    const int row = sl / kKSlots;  // head (row / 32), token (row % 32)
+    const int c = sl - row * kKSlots;
+    const int rr = row < kQRows ? row : kQRows - 1;
+    const uint32_t voff = uint32_t(rr & 31) * q_row_b + uint32_t(rr >> 5) * q_head_b +
+                          uint32_t(c < kD / 8 ? c : 0) * 16u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        q_rsrc, (lds_void_t *)(blk_i < kQDma ? v_ring + blk_i * 1024 : dummy), 16, voff, 0u, 0,
+        0);
+  }
+  const uint32_t k_row_bytes = uint32_t(ks_t) * 2u;
+  const uint32_t v_row_bytes = uint32_t(vs_t) * 2u;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(k + int64_t(start) * ks_t + h * ks_h), 0,
+      int(uint32_t(n - 1) * k_row_bytes + kD * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t *>(v + int64_t(start) * vs_t + h * vs_h), 0,
+      int(uint32_t(n - 1) * v_row_bytes + kD * 2), 0x00020000);
+  // Both tiles' DMAs are always issued (a fixed request count); in a
+  // one-tile block the second tile's offset lies past the buffer range, so
+  // nothing is fetched (and its ring slots are not read).
+  static_for<0, 2>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    const uint32_t soff = t < n_tiles ? uint32_t(t * kBN) * k_row_bytes : 0x40000000u;
+#pragma unroll
+    for (int i = 0; i < kSKPerWave; ++i) {
+      const int blk_i = wave + kSWaves * i;
+      const int sl = 64 * blk_i + lane;
+      const int row = sl / kKSlots;
+      const int c = sl - row * kKSlots;
+      const uint32_t voff = uint32_t(k_row_token(row < kBN ? row : kBN - 1)) * k_row_bytes +
+                            uint32_t(c < kD / 8 ? c : 0) * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          k_rsrc, (lds_void_t *)(blk_i < kKDma ? k_ring + t * kTileK + blk_i * 1024 : dummy), 16,
+          voff, soff, 0, 0);
+    }
+  });
+  // q rows and K tiles landed (this wave's DMAs), then every wave's
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  WY_STAMP(1);
+  u32x4_t xr[16];
+  {
+    const uint32_t qr = lds_u32(v_ring) + uint32_t((hd * kBQ + col) * kKPitch + g * 16);
+    static_for<0, 16>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      xr[i] = ds_read_b128_at<i * 32>(qr);
+    });
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(xr[0]), "+v"(xr[1]), "+v"(xr[2]), "+v"(xr[3]), "+v"(xr[4]), "+v"(xr[5]),
+                   "+v"(xr[6]), "+v"(xr[7]), "+v"(xr[8]), "+v"(xr[9]), "+v"(xr[10]), "+v"(xr[11]),
+                   "+v"(xr[12]), "+v"(xr[13]), "+v"(xr[14]), "+v"(xr[15])::"memory");
+  }
+  // every wave has its slices: the V tiles may land in the ring
+  asm volatile("s_barrier" ::: "memory");
+  // The V rows past the sequence's end are not fetched; their P is 0 but
+  // their LDS rows must hold finite values: this wave zeroes the blocks it
+  // is about to fill of a partial last tile (its own zero writes complete
+  // before its DMA is issued).
+  if (n < n_tiles * kBN) {
+    const uint32_t vz = lds_u32(v_ring + (n_tiles - 1) * kTileV) + uint32_t(lane * 16);
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < kSVPerWave; ++i)
+      if (wave + kSWaves * i < kVDma)
+        asm volatile("ds_write_b128 %0, %1 offset:0" ::"v"(vz + uint32_t((wave + kSWaves * i) * 1024)),
+                     "v"(z)
+                     : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  static_for<0, 2>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+    const uint32_t soff = t < n_tiles ? uint32_t(t * kBN) * v_row_bytes : 0x40000000u;
+#pragma unroll
+    for (int i = 0; i < kSVPerWave; ++i) {
+      const int blk_i = wave + kSWaves * i;
+      const int sl = 64 * blk_i + lane;
+      const int row = sl / kVSlots;
+      const int c = sl - row * kVSlots;
+      const uint32_t voff = uint32_t(row < kBN ? row : kBN - 1) * v_row_bytes +
+                            uint32_t(c < kD / 8 ? c : 0) * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          v_rsrc, (lds_void_t *)(blk_i < kVDma ? v_ring + t * kTileV + blk_i * 1024 : dummy), 16,
+          voff, soff, 0, 0);
+    }
+  });
+
+  WY_STAMP(2);
+
+  if constexpr (kRot > 0) {
+    // the standalone kernel's device math and bf16 rounding
+    // (partial_rope.py:74-98): k-step kk < kRot/32 holds dims 16kk + 8g .. +7
+    // of the first half, k-step kk + kRot/32 their partners
+    static_assert(kRot % 32 == 0 && kRot <= kD, "rotary dims in whole k-step pairs");
+    constexpr int kH = kRot / 32;
+#pragma unroll
+    for (int kk = 0; kk < kH; ++kk) {
+      u32x4_t a = xr[kk], bb = xr[kk + kH];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const f32x4_t &sv = tsn[2 * kk + w / 2], &cv = tcs[2 * kk + w / 2];
+        const float s0 = sv[2 * (w & 1)], s1 = sv[2 * (w & 1) + 1];
+        const float c0 = cv[2 * (w & 1)], c1 = cv[2 * (w & 1) + 1];
+        float o1l, o2l, o1h, o2h;
+        rope_rotate(bf16_lo(a[w]), bf16_lo(bb[w]), c0, s0, o1l, o2l);
+        rope_rotate(bf16_hi(a[w]), bf16_hi(bb[w]), c1, s1, o1h, o2h);
+        a[w] = pack_bf16x2(o1l, o1h);
+        bb[w] = pack_bf16x2(o2l, o2h);
+      }
+      xr[kk] = a;
+      xr[kk + kH] = bb;
+    }
+  }
+  // The q rows enter the MFMAs as they are; the scale (1/sqrt(D) in log2
+  // units) is applied to the scores inside the exponentials' fused
+  // multiply-add.  (Scaling and re-rounding the q slices cost ~1300 VALU
+  // cycles per wave -- a wave64 VALU instruction takes 4 -- twice per head
+  // here, more than the block's MFMAs.)  Rows past the sequence hold finite
+  // q bytes (or zeros) and only reach their own, unstored, output rows.
+  bf16x8_t qop[16];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) qop[kk] = __builtin_bit_cast(bf16x8_t, xr[kk]);
+
+  WY_CSTAMP(16);
+  // ---- S^T of this wave's slabs ----------------------------------------------
+  // unit u of this wave: (tile tu, slab mtu); one-tile blocks have one unit
+  const int n_units = n_tiles;  // 1 or 2
+  const int tu0 = n_tiles == 2 ? hf : 0;
+  const int mt0 = n_tiles == 2 ? 0 : hf;
+  f32x16_t s[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[u][e] = 0.f;
+  {
+    const uint32_t kr = lds_u32(k_ring + tu0 * kTileK) + uint32_t((32 * mt0 + col) * kKPitch + g * 16);
+    if (n_units == 2) {
+      // slabs 0 and 1 of tile tu0 alternate (independent accumulators)
+      u32x4_t ka[8];
+      auto rd = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;  // MFMA i: slab i & 1, k-step i >> 1
+        constexpr int off = (i & 1) * 32 * kKPitch + (i >> 1) * 32;
+        return ds_read_b128_at<off>(kr);
+      };
+      static_for<0, 8>([&](auto ic) { ka[ic] = rd(ic); });
+      static_for<0, 32>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        lgkm_wait1<(i + 8 <= 32 ? 7 : 31 - i)>(ka[i & 7]);
+        s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ka[i & 7]),
+                                                           qop[i >> 1], s[i & 1], 0, 0, 0);
+        if constexpr (i + 8 < 32) ka[i & 7] = rd(std::integral_constant<int, i + 8>{});
+      });
+    } else {
+      u32x4_t ka[16];
+      static_for<0, 16>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        ka[i] = ds_read_b128_at<i * 32>(kr);
+      });
+      static_for<0, 16>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        lgkm_wait1<15 - i>(ka[i]);
+        s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ka[i]),
+                                                       qop[i], s[0], 0, 0, 0);
+      });
+    }
+  }
+  // mask keys past the row's causal limit (or the sequence end), row max
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    if (u < n_units) {
+      const int tu = n_tiles == 2 ? tu0 : 0;
+      const int mtu = n_tiles == 2 ? u : mt0;
+      const int thr = row_lim - (tu * kBN + 32 * mtu + 16 * g);  // keep registers e <= thr
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        s[u][e] = e > thr ? -INFINITY : s[u][e];
+        mx = fmaxf(mx, s[u][e]);
+      }
+    }
+  }
+  WY_CSTAMP(17);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  WY_CSTAMP(18);
+  // (LDS accesses as inline asm here and below: the compiler would make a
+  // visible one wait for every DMA it knows of, the V tiles included)
+  const uint32_t mx_a = lds_u32(reinterpret_cast<unsigned char *>(s_mx));
+  ds_write_b32_at<0>(mx_a + uint32_t((wave * 64 + lane) * 4), __float_as_uint(mx));
+  // every wave's partial max written, and every wave past its last K read
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  WY_CSTAMP(19);
+  uint32_t mx_o = ds_read_b32_at(mx_a + uint32_t(((wave ^ 4) * 64 + lane) * 4));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(mx_o)::"memory");
+  const float m = fmaxf(mx, __uint_as_float(mx_o));  // raw score units
+  const float neg_ms = -(m * qk_scale_log2);
+  WY_STAMP(3);
+
+  // ---- P (bf16) of this wave's units, its row sum; swap P with the pair -----
+  // Unit u's P^T B operands: k-steps kk = 0, 1 of slab mtu = tokens
+  // 32 mtu + 16 g + 8 kk .. +7 of tile tu.
+  u32x4_t pown[2][2];
+  float psum = 0.f;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    if (u < n_units) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float a = __builtin_amdgcn_exp2f(__fmaf_rn(s[u][8 * kk + 2 * w], qk_scale_log2, neg_ms));
+          const float c =
+              __builtin_amdgcn_exp2f(__fmaf_rn(s[u][8 * kk + 2 * w + 1], qk_scale_log2, neg_ms));
+          psum += a + c;
+          pown[u][kk][w] = pack_bf16x2(a, c);
+        }
+    } else {
+      pown[u][0] = pown[u][1] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  const uint32_t ps_a = lds_u32(reinterpret_cast<unsigned char *>(s_ps));
+  ds_write_b32_at<0>(ps_a + uint32_t((wave * 64 + lane) * 4), __float_as_uint(psum));
+  const uint32_t xw = lds_u32(k_ring) + uint32_t(wave * kXchWave + lane * 16);
+  ds_write_b128_at<0>(xw, pown[0][0]);
+  ds_write_b128_at<1024>(xw, pown[0][1]);
+  if (n_units == 2) {
+    ds_write_b128_at<2048>(xw, pown[1][0]);
+    ds_write_b128_at<3072>(xw, pown[1][1]);
+  }
+  // V tiles landed (this wave's DMAs), the P and psum writes done; then every
+  // wave's
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const uint32_t xp = lds_u32(k_ring) + uint32_t((wave ^ 4) * kXchWave + lane * 16);
+  u32x4_t poth[2][2];
+  poth[0][0] = ds_read_b128_at<0>(xp);
+  poth[0][1] = ds_read_b128_at<1024>(xp);
+  if (n_units == 2) {
+    poth[1][0] = ds_read_b128_at<2048>(xp);
+    poth[1][1] = ds_read_b128_at<3072>(xp);
+  } else {
+    poth[1][0] = poth[1][1] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+  uint32_t ps_ob = ds_read_b32_at(ps_a + uint32_t(((wave ^ 4) * 64 + lane) * 4));
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(poth[0][0]), "+v"(poth[0][1]), "+v"(poth[1][0]), "+v"(poth[1][1]),
+                 "+v"(ps_ob)::"memory");
+  const float ps_o = __uint_as_float(ps_ob);
+  WY_STAMP(4);
+  // l: the halves' partial sums in half order (the same bits in both waves)
+  float l = hf == 0 ? psum + ps_o : ps_o + psum;
+  l += __shfl_xor(l, 32);
+
+  // P^T operand of tile t, k-step ks (= 2 slab + kk)
+  //   two-tile block: tile hf is this wave's, tile 1 - hf the pair's;
+  //   one-tile block: slab hf is this wave's, slab 1 - hf the pair's.
+  u32x4_t pb[2][4];
+  if (n_tiles == 2) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4_t mine = pown[ks >> 1][ks & 1], other = poth[ks >> 1][ks & 1];
+      pb[0][ks] = hf == 0 ? mine : other;
+      pb[1][ks] = hf == 0 ? other : mine;
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4_t mine = pown[0][ks & 1], other = poth[0][ks & 1];
+      pb[0][ks] = (ks >> 1) == hf ? mine : other;
+      pb[1][ks] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // ---- O^T += V^T P^T over the block's tiles, dims 128 hf .. +127 ----------
+  // A operand of k-step ks, dim block dt: lane (m = lane % 32, g) needs
+  // V[32(ks/2) + 16g + 8(ks%2) + 0..7][32dt + m] (transposing reads, as in
+  // prefill_kernel.h).
+  const int l16 = lane & 15;
+  const uint32_t v_lane_off =
+      uint32_t((16 * g + (l16 >> 2)) * kVPitch + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2) +
+      uint32_t(hf * 4 * 64);
+  f32x16_t o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  auto pv_tile = [&](int t, const u32x4_t(&pbt)[4]) {
+    const uint32_t vr = lds_u32(v_ring + t * kTileV) + v_lane_off;
+    // 7 MFMAs' operands in flight (14 reads: lgkmcnt counts to 15)
+    constexpr int kW = 7;
+    u32x2_t va[8][2];
+    auto rd = [&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int ks = j >> 2, dt = j & 3;
+      constexpr int off = (32 * (ks >> 1) + 8 * (ks & 1)) * kVPitch + dt * 64;
+      va[j & 7][0] = ds_read_tr16<off>(vr);
+      va[j & 7][1] = ds_read_tr16<off + 4 * kVPitch>(vr);
+    };
+    static_for<0, kW>([&](auto jc) { rd(jc); });
+    static_for<0, 16>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      constexpr int ks = j >> 2, dt = j & 3;
+      constexpr int issued = j + kW < 16 ? j + kW : 16;
+      lgkm_wait2<2 * (issued - j - 1)>(va[j & 7][0], va[j & 7][1]);
+      const u32x4_t a = {va[j & 7][0][0], va[j & 7][0][1], va[j & 7][1][0], va[j & 7][1][1]};
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                      __builtin_bit_cast(bf16x8_t, pbt[ks]), o[dt],
+                                                      0, 0, 0);
+      if constexpr (j + kW < 16) rd(std::integral_constant<int, j + kW>{});
+    });
+  };
+  pv_tile(0, pb[0]);
+  if (n_tiles == 2) pv_tile(1, pb[1]);
+
+  // ---- normalise, stage the rows in LDS, store whole rows ------------------
+  static_assert(kG * kD == 1024, "row layout of the staging");
+  const int r0 = tid >> 7, c8 = (tid & 127) * 8;  // 4 rows per step, 8 steps
+  u32x4_t gate_c[kRot > 0 ? kBQ / 4 : 1];
+  if constexpr (kRot > 0) {
+    const uint32_t row_b = uint32_t(blk.gs_t) * 2u, head_b = uint32_t(blk.gs_h) * 2u;
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t *>(blk.gate + (int64_t(start) + q0) * blk.gs_t + (h * kG) * blk.gs_h), 0,
+        int(uint32_t(n - 1 - q0) * row_b + (kG - 1) * head_b + kD * 2), 0x00020000);
+    const uint32_t vo = uint32_t(r0) * row_b + uint32_t(c8 / kD) * head_b + uint32_t(c8 % kD) * 2u;
+#pragma unroll
+    for (int i = 0; i < kBQ / 4; ++i)
+      gate_c[i] = __builtin_amdgcn_raw_buffer_load_b128(gr, vo, uint32_t(4 * i) * row_b, 0);
+  }
+  const float inv_l = 1.0f / l;
+  // every wave is past its last V read
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  WY_STAMP(5);
+  bf16_t *const stage = reinterpret_cast<bf16_t *>(v_ring);
+  {
+    const uint32_t sw = lds_u32(reinterpret_cast<unsigned char *>(
+        stage + col * kStagePitch + hd * kD + hf * 128 + 4 * g));
+    static_for<0, 4>([&](auto dtc) {
+      constexpr int dt = decltype(dtc)::value;
+      static_for<0, 4>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const u32x2_t w = {pack_bf16x2(o[dt][4 * j] * inv_l, o[dt][4 * j + 1] * inv_l),
+                           pack_bf16x2(o[dt][4 * j + 2] * inv_l, o[dt][4 * j + 3] * inv_l)};
+        ds_write_b64_at<(dt * 32 + 8 * j) * 2>(sw, w);
+      });
+    });
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  {
+    WY_STAMP(6);
+    const int rows = min(kBQ, n - q0);
+    const uint32_t sp = lds_u32(reinterpret_cast<unsigned char *>(stage + r0 * kStagePitch + c8));
+    u32x4_t wv[kBQ / 4];
+    static_for<0, kBQ / 4>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      wv[i] = ds_read_b128_at<i * 4 * kStagePitch * 2>(sp);
+    });
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(wv[0]), "+v"(wv[1]), "+v"(wv[2]), "+v"(wv[3]), "+v"(wv[4]), "+v"(wv[5]),
+                   "+v"(wv[6]), "+v"(wv[7])::"memory");
+    if constexpr (kRot > 0) {
+#pragma unroll
+      for (int i = 0; i < kBQ / 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          // bf16(ctx * sigmoid(gate)), ctx the bf16 attention output, as the
+          // gate pack computes it
+          wv[i][e] = pack_bf16x2(bf16_lo(wv[i][e]) * gate_sigmoid(bf16_lo(gate_c[i][e])),
+                                 bf16_hi(wv[i][e]) * gate_sigmoid(bf16_hi(gate_c[i][e])));
+    }
+    bf16_t *ob = out + (int64_t(start) + q0 + r0) * os_t + (h * kG + c8 / kD) * os_h + c8 % kD;
+#pragma unroll
+    for (int i = 0; i < kBQ / 4; ++i) {
+      if (r0 + 4 * i < rows) st16_nt(ob, wv[i]);
+      ob += 4 * os_t;
+    }
+#if WY_TRACE
+    WY_STAMP(7);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    WY_STAMP(8);
+    if (tid == 0) {
+      unsigned hw, xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      g_strace[blockIdx.x * 32 + 14] = (unsigned long long)n_tiles | ((unsigned long long)qb << 8) |
+                                       ((unsigned long long)b << 16);
+      g_strace[blockIdx.x * 32 + 15] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
+    }
+#endif
+  }
+}
+
+template __global__ void short_prefill_kernel<0>(
+    const bf16_t *__restrict__, int64_t, int64_t, const bf16_t *__restrict__, int64_t, int64_t,
+    const bf16_t *__restrict__, int64_t, int64_t, bf16_t *__restrict__, int64_t, int64_t,
+    const int32_t *__restrict__, float, int, int, int, const BlockArgs, int);
+template __global__ void short_prefill_kernel<64>(
+    const bf16_t *__restrict__, int64_t, int64_t, const bf16_t *__restrict__, int64_t, int64_t,
+    const bf16_t *__restrict__, int64_t, int64_t, bf16_t *__restrict__, int64_t, int64_t,
+    const int32_t *__restrict__, float, int, int, int, const BlockArgs, int);
+
+}  // namespace wy_prefill
+
+#if WY_TRACE
+extern "C" int wy_prefill_short_trace_read(void *host, size_t bytes, int clear) {
+  if (clear) {
+    static unsigned long long zeros[4096 * 32];
+    return int(hipMemcpyToSymbol(HIP_SYMBOL(wy_prefill::g_strace), zeros, sizeof(zeros)));
+  }
+  return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(wy_prefill::g_strace),
+                                 bytes < sizeof(wy_prefill::g_strace) ? bytes : sizeof(wy_prefill::g_strace)));
+}
+#endif
