@@ -288,23 +288,27 @@ void short_prefill_kernel(
 
   WY_CSTAMP(16);
   // ---- S^T of this wave's slabs ----------------------------------------------
-  // unit u of this wave: (tile tu, slab mtu); one-tile blocks have one unit
-  const int n_units = n_tiles;  // 1 or 2
-  const int tu0 = n_tiles == 2 ? hf : 0;
-  const int mt0 = n_tiles == 2 ? 0 : hf;
+  // Score slabs: slab j holds keys 32j .. 32j + 31 (tile j / 2, rows 32 (j % 2)
+  // .. of its K slot).  The block's rows see slabs 0 .. qb; slab qb holds the
+  // diagonal (and the sequence end), the earlier ones are fully visible, the
+  // later ones fully masked and skipped (their P is exactly 0, so skipping
+  // their MFMAs changes no bit).  Wave half hf takes slabs hf and hf + 2:
+  // unit u = slab hf + 2u = (tile u, K rows 32 hf ..).
+  const int n_own = hf <= qb ? (qb - hf) / 2 + 1 : 0;  // 0, 1 or 2 (uniform)
+  const int n_oth = (1 - hf) <= qb ? (qb - 1 + hf) / 2 + 1 : 0;
   f32x16_t s[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u)
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[u][e] = 0.f;
   {
-    const uint32_t kr = lds_u32(k_ring + tu0 * kTileK) + uint32_t((32 * mt0 + col) * kKPitch + g * 16);
-    if (n_units == 2) {
-      // slabs 0 and 1 of tile tu0 alternate (independent accumulators)
+    const uint32_t kr = lds_u32(k_ring) + uint32_t((32 * hf + col) * kKPitch + g * 16);
+    if (n_own == 2) {
+      // the two units alternate (independent accumulators)
       u32x4_t ka[8];
       auto rd = [&](auto ic) {
-        constexpr int i = decltype(ic)::value;  // MFMA i: slab i & 1, k-step i >> 1
-        constexpr int off = (i & 1) * 32 * kKPitch + (i >> 1) * 32;
+        constexpr int i = decltype(ic)::value;  // MFMA i: unit i & 1, k-step i >> 1
+        constexpr int off = (i & 1) * kTileK + (i >> 1) * 32;
         return ds_read_b128_at<off>(kr);
       };
       static_for<0, 8>([&](auto ic) { ka[ic] = rd(ic); });
@@ -315,7 +319,7 @@ void short_prefill_kernel(
                                                            qop[i >> 1], s[i & 1], 0, 0, 0);
         if constexpr (i + 8 < 32) ka[i & 7] = rd(std::integral_constant<int, i + 8>{});
       });
-    } else {
+    } else if (n_own == 1) {
       u32x4_t ka[16];
       static_for<0, 16>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -329,22 +333,22 @@ void short_prefill_kernel(
       });
     }
   }
-  // mask keys past the row's causal limit (or the sequence end), row max
+  WY_CSTAMP(17);
+  // mask the diagonal slab (keys past the row's causal limit or the sequence
+  // end); row max over this wave's slabs
   float mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    if (u < n_units) {
-      const int tu = n_tiles == 2 ? tu0 : 0;
-      const int mtu = n_tiles == 2 ? u : mt0;
-      const int thr = row_lim - (tu * kBN + 32 * mtu + 16 * g);  // keep registers e <= thr
+    if (u < n_own) {
+      if (hf + 2 * u == qb) {
+        const int thr = row_lim - (32 * qb + 16 * g);  // keep registers e <= thr
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[u][e] = e > thr ? -INFINITY : s[u][e];
-        mx = fmaxf(mx, s[u][e]);
+        for (int e = 0; e < 16; ++e) s[u][e] = e > thr ? -INFINITY : s[u][e];
       }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[u][e]);
     }
   }
-  WY_CSTAMP(17);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   WY_CSTAMP(18);
   // (LDS accesses as inline asm here and below: the compiler would make a
@@ -361,13 +365,13 @@ void short_prefill_kernel(
   WY_STAMP(3);
 
   // ---- P (bf16) of this wave's units, its row sum; swap P with the pair -----
-  // Unit u's P^T B operands: k-steps kk = 0, 1 of slab mtu = tokens
-  // 32 mtu + 16 g + 8 kk .. +7 of tile tu.
+  // Unit u's P^T B operands: k-steps kk = 0, 1 = keys 32 j + 16 g + 8 kk .. +7
+  // of its slab j.
   u32x4_t pown[2][2];
   float psum = 0.f;
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    if (u < n_units) {
+    if (u < n_own) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -385,9 +389,11 @@ void short_prefill_kernel(
   const uint32_t ps_a = lds_u32(reinterpret_cast<unsigned char *>(s_ps));
   ds_write_b32_at<0>(ps_a + uint32_t((wave * 64 + lane) * 4), __float_as_uint(psum));
   const uint32_t xw = lds_u32(k_ring) + uint32_t(wave * kXchWave + lane * 16);
-  ds_write_b128_at<0>(xw, pown[0][0]);
-  ds_write_b128_at<1024>(xw, pown[0][1]);
-  if (n_units == 2) {
+  if (n_own >= 1) {
+    ds_write_b128_at<0>(xw, pown[0][0]);
+    ds_write_b128_at<1024>(xw, pown[0][1]);
+  }
+  if (n_own == 2) {
     ds_write_b128_at<2048>(xw, pown[1][0]);
     ds_write_b128_at<3072>(xw, pown[1][1]);
   }
@@ -396,13 +402,15 @@ void short_prefill_kernel(
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const uint32_t xp = lds_u32(k_ring) + uint32_t((wave ^ 4) * kXchWave + lane * 16);
   u32x4_t poth[2][2];
-  poth[0][0] = ds_read_b128_at<0>(xp);
-  poth[0][1] = ds_read_b128_at<1024>(xp);
-  if (n_units == 2) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) poth[u][0] = poth[u][1] = u32x4_t{0u, 0u, 0u, 0u};
+  if (n_oth >= 1) {
+    poth[0][0] = ds_read_b128_at<0>(xp);
+    poth[0][1] = ds_read_b128_at<1024>(xp);
+  }
+  if (n_oth == 2) {
     poth[1][0] = ds_read_b128_at<2048>(xp);
     poth[1][1] = ds_read_b128_at<3072>(xp);
-  } else {
-    poth[1][0] = poth[1][1] = u32x4_t{0u, 0u, 0u, 0u};
   }
   uint32_t ps_ob = ds_read_b32_at(ps_a + uint32_t(((wave ^ 4) * 64 + lane) * 4));
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -414,30 +422,10 @@ void short_prefill_kernel(
   float l = hf == 0 ? psum + ps_o : ps_o + psum;
   l += __shfl_xor(l, 32);
 
-  // P^T operand of tile t, k-step ks (= 2 slab + kk)
-  //   two-tile block: tile hf is this wave's, tile 1 - hf the pair's;
-  //   one-tile block: slab hf is this wave's, slab 1 - hf the pair's.
-  u32x4_t pb[2][4];
-  if (n_tiles == 2) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const u32x4_t mine = pown[ks >> 1][ks & 1], other = poth[ks >> 1][ks & 1];
-      pb[0][ks] = hf == 0 ? mine : other;
-      pb[1][ks] = hf == 0 ? other : mine;
-    }
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const u32x4_t mine = pown[0][ks & 1], other = poth[0][ks & 1];
-      pb[0][ks] = (ks >> 1) == hf ? mine : other;
-      pb[1][ks] = u32x4_t{0u, 0u, 0u, 0u};
-    }
-  }
-
-  // ---- O^T += V^T P^T over the block's tiles, dims 128 hf .. +127 ----------
-  // A operand of k-step ks, dim block dt: lane (m = lane % 32, g) needs
-  // V[32(ks/2) + 16g + 8(ks%2) + 0..7][32dt + m] (transposing reads, as in
-  // prefill_kernel.h).
+  // ---- O^T += V^T P^T over the visible slabs, dims 128 hf .. +127 ----------
+  // A operand of slab j, k-step kk, dim block dt: lane (m = lane % 32, g)
+  // needs V[32 j + 16 g + 8 kk + 0..7][32 dt + m] of tile j / 2 (transposing
+  // reads, as in prefill_kernel.h).
   const int l16 = lane & 15;
   const uint32_t v_lane_off =
       uint32_t((16 * g + (l16 >> 2)) * kVPitch + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2) +
@@ -447,33 +435,41 @@ void short_prefill_kernel(
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
-  auto pv_tile = [&](int t, const u32x4_t(&pbt)[4]) {
-    const uint32_t vr = lds_u32(v_ring + t * kTileV) + v_lane_off;
-    // 7 MFMAs' operands in flight (14 reads: lgkmcnt counts to 15)
-    constexpr int kW = 7;
+  const uint32_t vr = lds_u32(v_ring) + v_lane_off;
+  auto pv_slab = [&](auto jc, const u32x4_t(&pj)[2]) {
+    constexpr int j = decltype(jc)::value;
+    // 8 MFMAs (kk, dt), 6 operands in flight (12 reads: lgkmcnt counts to 15)
+    constexpr int kW = 6;
     u32x2_t va[8][2];
-    auto rd = [&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      constexpr int ks = j >> 2, dt = j & 3;
-      constexpr int off = (32 * (ks >> 1) + 8 * (ks & 1)) * kVPitch + dt * 64;
-      va[j & 7][0] = ds_read_tr16<off>(vr);
-      va[j & 7][1] = ds_read_tr16<off + 4 * kVPitch>(vr);
+    auto rd = [&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      constexpr int kk = x >> 2, dt = x & 3;
+      constexpr int off = (j >> 1) * kTileV + (32 * (j & 1) + 8 * kk) * kVPitch + dt * 64;
+      va[x][0] = ds_read_tr16<off>(vr);
+      va[x][1] = ds_read_tr16<off + 4 * kVPitch>(vr);
     };
-    static_for<0, kW>([&](auto jc) { rd(jc); });
-    static_for<0, 16>([&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      constexpr int ks = j >> 2, dt = j & 3;
-      constexpr int issued = j + kW < 16 ? j + kW : 16;
-      lgkm_wait2<2 * (issued - j - 1)>(va[j & 7][0], va[j & 7][1]);
-      const u32x4_t a = {va[j & 7][0][0], va[j & 7][0][1], va[j & 7][1][0], va[j & 7][1][1]};
+    static_for<0, kW>([&](auto xc) { rd(xc); });
+    static_for<0, 8>([&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      constexpr int kk = x >> 2, dt = x & 3;
+      constexpr int issued = x + kW < 8 ? x + kW : 8;
+      lgkm_wait2<2 * (issued - x - 1)>(va[x][0], va[x][1]);
+      const u32x4_t a = {va[x][0][0], va[x][0][1], va[x][1][0], va[x][1][1]};
       o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                      __builtin_bit_cast(bf16x8_t, pbt[ks]), o[dt],
+                                                      __builtin_bit_cast(bf16x8_t, pj[kk]), o[dt],
                                                       0, 0, 0);
-      if constexpr (j + kW < 16) rd(std::integral_constant<int, j + kW>{});
+      if constexpr (x + kW < 8) rd(std::integral_constant<int, x + kW>{});
     });
   };
-  pv_tile(0, pb[0]);
-  if (n_tiles == 2) pv_tile(1, pb[1]);
+  // slab j's P: this wave's unit j / 2 when j % 2 == hf, else the pair's
+  static_for<0, 4>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if (j <= qb) {
+      const u32x4_t pj[2] = {(j & 1) == hf ? pown[j >> 1][0] : poth[j >> 1][0],
+                             (j & 1) == hf ? pown[j >> 1][1] : poth[j >> 1][1]};
+      pv_slab(jc, pj);
+    }
+  });
 
   // ---- normalise, stage the rows in LDS, store whole rows ------------------
   static_assert(kG * kD == 1024, "row layout of the staging");
