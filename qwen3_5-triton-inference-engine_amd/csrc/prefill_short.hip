@@ -46,6 +46,9 @@ constexpr int kQRows = kG * kBQ;
 constexpr int kQDma = (kQRows * kKPitch + 1023) / 1024;        // 66 blocks
 constexpr int kSQPerWave = (kQDma + kSWaves - 1) / kSWaves;    // 9
 static_assert(kQDma * 1024 <= 2 * kTileV, "q staging fits the V ring");
+static_assert(64 * kSWaves * kSQPerWave <= 4608 && 64 * kSWaves * kSKPerWave <= 4608 &&
+                  64 * kSWaves * kSVPerWave <= 2560,
+              "DMA slot indices in the range where div33 / div36 are exact");
 // P exchange in the K ring once every wave is past its S^T: per wave two
 // units of two 1 KiB k-step blocks.
 constexpr int kXchWave = 4096;
@@ -80,6 +83,13 @@ __device__ unsigned long long g_strace[4096 * 32];
   do {              \
   } while (0)
 #endif
+
+// Per-lane DMA offsets with 24-bit multiplies (full rate; a 32-bit multiply
+// takes four VALU slots): the launch checks that every row and head stride
+// is below 2^24 bytes.  x / 33 (exact for x < 4608) and x / 36 (exact for
+// x < 2560) as multiply-shifts.
+__device__ __forceinline__ uint32_t div33(uint32_t x) { return __umul24(x, 1986u) >> 16; }
+__device__ __forceinline__ uint32_t div36(uint32_t x) { return __umul24(x, 1821u) >> 16; }
 
 __device__ __forceinline__ uint32_t ds_read_b32_at(uint32_t addr) {
   uint32_t r;
@@ -164,12 +174,12 @@ void short_prefill_kernel(
 #pragma unroll
   for (int i = 0; i < kSQPerWave; ++i) {
     const int blk_i = wave + kSWaves * i;
-    const int sl = 64 * blk_i + lane;
-    const int row = sl / kKSlots;  // head (row / 32), token (row % 32)
-    const int c = sl - row * kKSlots;
-    const int rr = row < kQRows ? row : kQRows - 1;
-    const uint32_t voff = uint32_t(rr & 31) * q_row_b + uint32_t(rr >> 5) * q_head_b +
-                          uint32_t(c < kD / 8 ? c : 0) * 16u;
+    const uint32_t sl = uint32_t(64 * blk_i + lane);
+    const uint32_t row = div33(sl);  // head (row / 32), token (row % 32)
+    const uint32_t c = sl - row * kKSlots;
+    const uint32_t rr = row < kQRows ? row : kQRows - 1;
+    const uint32_t voff = __umul24(rr & 31, q_row_b) + __umul24(rr >> 5, q_head_b) +
+                          (c < kD / 8 ? c : 0) * 16u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         q_rsrc, (lds_void_t *)(blk_i < kQDma ? v_ring + blk_i * 1024 : dummy), 16, voff, 0u, 0,
         0);
@@ -191,11 +201,12 @@ void short_prefill_kernel(
 #pragma unroll
     for (int i = 0; i < kSKPerWave; ++i) {
       const int blk_i = wave + kSWaves * i;
-      const int sl = 64 * blk_i + lane;
-      const int row = sl / kKSlots;
-      const int c = sl - row * kKSlots;
-      const uint32_t voff = uint32_t(k_row_token(row < kBN ? row : kBN - 1)) * k_row_bytes +
-                            uint32_t(c < kD / 8 ? c : 0) * 16u;
+      const uint32_t sl = uint32_t(64 * blk_i + lane);
+      const uint32_t row = div33(sl);
+      const uint32_t c = sl - row * kKSlots;
+      const uint32_t voff =
+          __umul24(uint32_t(k_row_token(row < kBN ? int(row) : kBN - 1)), k_row_bytes) +
+          (c < kD / 8 ? c : 0) * 16u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           k_rsrc, (lds_void_t *)(blk_i < kKDma ? k_ring + t * kTileK + blk_i * 1024 : dummy), 16,
           voff, soff, 0, 0);
@@ -239,11 +250,11 @@ void short_prefill_kernel(
 #pragma unroll
     for (int i = 0; i < kSVPerWave; ++i) {
       const int blk_i = wave + kSWaves * i;
-      const int sl = 64 * blk_i + lane;
-      const int row = sl / kVSlots;
-      const int c = sl - row * kVSlots;
-      const uint32_t voff = uint32_t(row < kBN ? row : kBN - 1) * v_row_bytes +
-                            uint32_t(c < kD / 8 ? c : 0) * 16u;
+      const uint32_t sl = uint32_t(64 * blk_i + lane);
+      const uint32_t row = div36(sl);
+      const uint32_t c = sl - row * kVSlots;
+      const uint32_t voff = __umul24(row < kBN ? row : kBN - 1, v_row_bytes) +
+                            (c < kD / 8 ? c : 0) * 16u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           v_rsrc, (lds_void_t *)(blk_i < kVDma ? v_ring + t * kTileV + blk_i * 1024 : dummy), 16,
           voff, soff, 0, 0);
