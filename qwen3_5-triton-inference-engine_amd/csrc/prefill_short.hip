@@ -482,16 +482,25 @@ void short_prefill_kernel(
     }
   });
 
-  // ---- normalise, stage the rows in LDS, store whole rows ------------------
-  static_assert(kG * kD == 1024, "row layout of the staging");
-  const int r0 = tid >> 7, c8 = (tid & 127) * 8;  // 4 rows per step, 8 steps
+  // ---- normalise, stage, store ----------------------------------------------
+  // Each wave stages its own 32 rows x 128 dims (256-byte row pieces, padded
+  // by 16 bytes against bank conflicts) in its own part of the V ring and
+  // stores them back as whole pieces: 4 pieces per store instruction, so no
+  // second barrier (a wave reads only what it wrote; LDS accesses of one
+  // wave complete in order).
+  constexpr int kSPitch = 128 * 2 + 16;  // bytes per staged row piece
+  static_assert(kSWaves * kBQ * kSPitch <= 2 * kTileV, "per-wave staging fits the V ring");
+  const int pr = lane >> 4, pc = (lane & 15) * 8;  // piece row (+ 4 i), column (bf16)
   u32x4_t gate_c[kRot > 0 ? kBQ / 4 : 1];
   if constexpr (kRot > 0) {
-    const uint32_t row_b = uint32_t(blk.gs_t) * 2u, head_b = uint32_t(blk.gs_h) * 2u;
+    // (the range ends after the last row's piece: every byte in it lies
+    // inside the gate tensor; rows past the sequence are not stored)
+    const uint32_t row_b = uint32_t(blk.gs_t) * 2u;
     const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<bf16_t *>(blk.gate + (int64_t(start) + q0) * blk.gs_t + (h * kG) * blk.gs_h), 0,
-        int(uint32_t(n - 1 - q0) * row_b + (kG - 1) * head_b + kD * 2), 0x00020000);
-    const uint32_t vo = uint32_t(r0) * row_b + uint32_t(c8 / kD) * head_b + uint32_t(c8 % kD) * 2u;
+        const_cast<bf16_t *>(blk.gate + (int64_t(start) + q0) * blk.gs_t + (h * kG + hd) * blk.gs_h +
+                             hf * 128),
+        0, int(uint32_t(n - 1 - q0) * row_b + 128 * 2), 0x00020000);
+    const uint32_t vo = uint32_t(pr) * row_b + uint32_t(pc) * 2u;
 #pragma unroll
     for (int i = 0; i < kBQ / 4; ++i)
       gate_c[i] = __builtin_amdgcn_raw_buffer_load_b128(gr, vo, uint32_t(4 * i) * row_b, 0);
@@ -500,10 +509,9 @@ void short_prefill_kernel(
   // every wave is past its last V read
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   WY_STAMP(5);
-  bf16_t *const stage = reinterpret_cast<bf16_t *>(v_ring);
+  unsigned char *const stage = v_ring + wave * (kBQ * kSPitch);
   {
-    const uint32_t sw = lds_u32(reinterpret_cast<unsigned char *>(
-        stage + col * kStagePitch + hd * kD + hf * 128 + 4 * g));
+    const uint32_t sw = lds_u32(stage + col * kSPitch + 4 * g * 2);
     static_for<0, 4>([&](auto dtc) {
       constexpr int dt = decltype(dtc)::value;
       static_for<0, 4>([&](auto jc) {
@@ -514,15 +522,14 @@ void short_prefill_kernel(
       });
     });
   }
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   {
     WY_STAMP(6);
     const int rows = min(kBQ, n - q0);
-    const uint32_t sp = lds_u32(reinterpret_cast<unsigned char *>(stage + r0 * kStagePitch + c8));
+    const uint32_t sp = lds_u32(stage + pr * kSPitch + pc * 2);
     u32x4_t wv[kBQ / 4];
     static_for<0, kBQ / 4>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      wv[i] = ds_read_b128_at<i * 4 * kStagePitch * 2>(sp);
+      wv[i] = ds_read_b128_at<i * 4 * kSPitch>(sp);
     });
     asm volatile("s_waitcnt lgkmcnt(0)"
                  : "+v"(wv[0]), "+v"(wv[1]), "+v"(wv[2]), "+v"(wv[3]), "+v"(wv[4]), "+v"(wv[5]),
@@ -537,10 +544,10 @@ void short_prefill_kernel(
           wv[i][e] = pack_bf16x2(bf16_lo(wv[i][e]) * gate_sigmoid(bf16_lo(gate_c[i][e])),
                                  bf16_hi(wv[i][e]) * gate_sigmoid(bf16_hi(gate_c[i][e])));
     }
-    bf16_t *ob = out + (int64_t(start) + q0 + r0) * os_t + (h * kG + c8 / kD) * os_h + c8 % kD;
+    bf16_t *ob = out + (int64_t(start) + q0 + pr) * os_t + (h * kG + hd) * os_h + hf * 128 + pc;
 #pragma unroll
     for (int i = 0; i < kBQ / 4; ++i) {
-      if (r0 + 4 * i < rows) st16_nt(ob, wv[i]);
+      if (pr + 4 * i < rows) st16_nt(ob, wv[i]);
       ob += 4 * os_t;
     }
 #if WY_TRACE
