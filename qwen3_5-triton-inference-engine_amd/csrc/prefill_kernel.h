@@ -425,7 +425,6 @@ void varlen_causal_prefill_kernel(
   const int q0 = qb * kBQ;
   if (q0 >= n) return;  // direct launch only (the queue holds active blocks only)
 
-  const int hq = h * kG + wave;
   const int qrow = q0 + col;
 
   const int kv_end = min(q0 + kBQ, n);  // exclusive bound of keys any row can see

@@ -307,11 +307,11 @@ void short_prefill_kernel(
   // unit u = slab hf + 2u = (tile u, K rows 32 hf ..).
   const int n_own = hf <= qb ? (qb - hf) / 2 + 1 : 0;  // 0, 1 or 2 (uniform)
   const int n_oth = (1 - hf) <= qb ? (qb - 1 + hf) / 2 + 1 : 0;
+  // (accumulators are not zeroed: each chain's first MFMA takes a zero C
+  // operand -- a wave64 VALU instruction costs four cycles, and zeroing the
+  // S and O accumulators took about 100 of them)
   f32x16_t s[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s[u][e] = 0.f;
+  const f32x16_t zacc = {};
   {
     const uint32_t kr = lds_u32(k_ring) + uint32_t((32 * hf + col) * kKPitch + g * 16);
     if (n_own == 2) {
@@ -327,7 +327,8 @@ void short_prefill_kernel(
         constexpr int i = decltype(ic)::value;
         lgkm_wait1<(i + 8 <= 32 ? 7 : 31 - i)>(ka[i & 7]);
         s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ka[i & 7]),
-                                                           qop[i >> 1], s[i & 1], 0, 0, 0);
+                                                           qop[i >> 1], i < 2 ? zacc : s[i & 1],
+                                                           0, 0, 0);
         if constexpr (i + 8 < 32) ka[i & 7] = rd(std::integral_constant<int, i + 8>{});
       });
     } else if (n_own == 1) {
@@ -340,7 +341,7 @@ void short_prefill_kernel(
         constexpr int i = decltype(ic)::value;
         lgkm_wait1<15 - i>(ka[i]);
         s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ka[i]),
-                                                       qop[i], s[0], 0, 0, 0);
+                                                       qop[i], i == 0 ? zacc : s[0], 0, 0, 0);
       });
     }
   }
@@ -393,8 +394,6 @@ void short_prefill_kernel(
           psum += a + c;
           pown[u][kk][w] = pack_bf16x2(a, c);
         }
-    } else {
-      pown[u][0] = pown[u][1] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
   const uint32_t ps_a = lds_u32(reinterpret_cast<unsigned char *>(s_ps));
@@ -413,8 +412,6 @@ void short_prefill_kernel(
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const uint32_t xp = lds_u32(k_ring) + uint32_t((wave ^ 4) * kXchWave + lane * 16);
   u32x4_t poth[2][2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) poth[u][0] = poth[u][1] = u32x4_t{0u, 0u, 0u, 0u};
   if (n_oth >= 1) {
     poth[0][0] = ds_read_b128_at<0>(xp);
     poth[0][1] = ds_read_b128_at<1024>(xp);
@@ -441,11 +438,7 @@ void short_prefill_kernel(
   const uint32_t v_lane_off =
       uint32_t((16 * g + (l16 >> 2)) * kVPitch + (16 * ((lane >> 4) & 1) + 4 * (l16 & 3)) * 2) +
       uint32_t(hf * 4 * 64);
-  f32x16_t o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  f32x16_t o[4];  // first written by slab 0 (always visible) from a zero C
   const uint32_t vr = lds_u32(v_ring) + v_lane_off;
   auto pv_slab = [&](auto jc, const u32x4_t(&pj)[2]) {
     constexpr int j = decltype(jc)::value;
@@ -466,21 +459,23 @@ void short_prefill_kernel(
       constexpr int issued = x + kW < 8 ? x + kW : 8;
       lgkm_wait2<2 * (issued - x - 1)>(va[x][0], va[x][1]);
       const u32x4_t a = {va[x][0][0], va[x][0][1], va[x][1][0], va[x][1][1]};
-      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                      __builtin_bit_cast(bf16x8_t, pj[kk]), o[dt],
-                                                      0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          __builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, pj[kk]),
+          j == 0 && kk == 0 ? zacc : o[dt], 0, 0, 0);
       if constexpr (x + kW < 8) rd(std::integral_constant<int, x + kW>{});
     });
   };
   // slab j's P: this wave's unit j / 2 when j % 2 == hf, else the pair's
-  static_for<0, 4>([&](auto jc) {
-    constexpr int j = decltype(jc)::value;
-    if (j <= qb) {
-      const u32x4_t pj[2] = {(j & 1) == hf ? pown[j >> 1][0] : poth[j >> 1][0],
-                             (j & 1) == hf ? pown[j >> 1][1] : poth[j >> 1][1]};
-      pv_slab(jc, pj);
-    }
-  });
+  // (a branch on the wave-uniform half, not a per-register select)
+  auto pv_all = [&](auto hc) {
+    constexpr int H = decltype(hc)::value;
+    static_for<0, 4>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if (j <= qb) pv_slab(jc, (j & 1) == H ? pown[j >> 1] : poth[j >> 1]);
+    });
+  };
+  if (hf == 0) pv_all(std::integral_constant<int, 0>{});
+  else pv_all(std::integral_constant<int, 1>{});
 
   // ---- normalise, stage, store ----------------------------------------------
   // Each wave stages its own 32 rows x 128 dims (256-byte row pieces, padded
