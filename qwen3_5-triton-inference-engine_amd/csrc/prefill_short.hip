@@ -39,16 +39,25 @@
 namespace wy_prefill {
 
 constexpr int kSWaves = 8;
-constexpr int kSKPerWave = (kKDma + kSWaves - 1) / kSWaves;  // 5 (40 >= 33 blocks)
 constexpr int kSVPerWave = (kVDma + kSWaves - 1) / kSWaves;  // 5 (40 >= 36 blocks)
-// q staging: 4 heads x 32 rows in K-row layout, in the V ring
+// q and K rows in LDS: groups of 32 rows; rows r and r + 16 of a group share
+// one 1040-byte pair slot (r at +0, r + 16 at +512), pair slots of a group
+// 1040 bytes apart.  One 1 KiB LDS DMA then fills a pair slot with lane-
+// invariant offsets (lane l: row r + 16 (l / 32), chunk l % 32), and the
+// operand reads of 16 consecutive rows start 65 16-byte bank groups apart
+// (conflict-free).
+constexpr int kPairPitch = 1040;
+constexpr int kGroupBytes = 16 * kPairPitch;  // 32 rows
+static_assert(2 * kGroupBytes <= kTileK, "a K tile of two row groups fits its slot");
+// q staging: 4 heads x 32 rows, one group per head, in the V ring
 constexpr int kQRows = kG * kBQ;
-constexpr int kQDma = (kQRows * kKPitch + 1023) / 1024;        // 66 blocks
-constexpr int kSQPerWave = (kQDma + kSWaves - 1) / kSWaves;    // 9
-static_assert(kQDma * 1024 <= 2 * kTileV, "q staging fits the V ring");
-static_assert(64 * kSWaves * kSQPerWave <= 4608 && 64 * kSWaves * kSKPerWave <= 4608 &&
-                  64 * kSWaves * kSVPerWave <= 2560,
-              "DMA slot indices in the range where div33 / div36 are exact");
+static_assert(kG * kGroupBytes <= 2 * kTileV, "q staging fits the V ring");
+// LDS offset of row r of a group-layout tile
+__host__ __device__ constexpr int grow_off(int r) {
+  return (r >> 5) * kGroupBytes + (r & 15) * kPairPitch + ((r >> 4) & 1) * 512;
+}
+static_assert(64 * kSWaves * kSVPerWave <= 2560,
+              "V DMA slot indices in the range where div36 is exact");
 // P exchange in the K ring once every wave is past its S^T: per wave two
 // units of two 1 KiB k-step blocks.
 constexpr int kXchWave = 4096;
@@ -84,11 +93,9 @@ __device__ unsigned long long g_strace[4096 * 32];
   } while (0)
 #endif
 
-// Per-lane DMA offsets with 24-bit multiplies (full rate; a 32-bit multiply
-// takes four VALU slots): the launch checks that every row and head stride
-// is below 2^24 bytes.  x / 33 (exact for x < 4608) and x / 36 (exact for
-// x < 2560) as multiply-shifts.
-__device__ __forceinline__ uint32_t div33(uint32_t x) { return __umul24(x, 1986u) >> 16; }
+// Per-lane V DMA offsets with 24-bit multiplies (full rate; a 32-bit
+// multiply takes four VALU slots): the launch checks that the V row stride
+// is below 2^24 bytes.  x / 36 as a multiply-shift, exact for x < 2560.
 __device__ __forceinline__ uint32_t div36(uint32_t x) { return __umul24(x, 1821u) >> 16; }
 
 __device__ __forceinline__ uint32_t ds_read_b32_at(uint32_t addr) {
@@ -171,18 +178,15 @@ void short_prefill_kernel(
       const_cast<bf16_t *>(q + (int64_t(start) + q0) * qs_t + (h * kG) * qs_h), 0,
       int(uint32_t(n - 1 - q0) * q_row_b + uint32_t(kG - 1) * q_head_b + kD * 2), 0x00020000);
   unsigned char *const dummy = smem + kRingBytes;
+  // pair slot p of head group hq: rows (tokens) p and p + 16
+  const uint32_t lane_chunk = uint32_t(lane & 31) * 16u;
+  const uint32_t q_voff = uint32_t(lane >> 5) * 16u * q_row_b + lane_chunk;
 #pragma unroll
-  for (int i = 0; i < kSQPerWave; ++i) {
-    const int blk_i = wave + kSWaves * i;
-    const uint32_t sl = uint32_t(64 * blk_i + lane);
-    const uint32_t row = div33(sl);  // head (row / 32), token (row % 32)
-    const uint32_t c = sl - row * kKSlots;
-    const uint32_t rr = row < kQRows ? row : kQRows - 1;
-    const uint32_t voff = __umul24(rr & 31, q_row_b) + __umul24(rr >> 5, q_head_b) +
-                          (c < kD / 8 ? c : 0) * 16u;
+  for (int i = 0; i < kQRows / 2 / kSWaves; ++i) {
+    const int ps = wave + kSWaves * i;  // pair slot 0..63: head ps / 16, token ps % 16
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        q_rsrc, (lds_void_t *)(blk_i < kQDma ? v_ring + blk_i * 1024 : dummy), 16, voff, 0u, 0,
-        0);
+        q_rsrc, (lds_void_t *)(v_ring + (ps >> 4) * kGroupBytes + (ps & 15) * kPairPitch), 16,
+        q_voff, uint32_t(ps & 15) * q_row_b + uint32_t(ps >> 4) * q_head_b, 0, 0);
   }
   const uint32_t k_row_bytes = uint32_t(ks_t) * 2u;
   const uint32_t v_row_bytes = uint32_t(vs_t) * 2u;
@@ -194,22 +198,20 @@ void short_prefill_kernel(
       int(uint32_t(n - 1) * v_row_bytes + kD * 2), 0x00020000);
   // Both tiles' DMAs are always issued (a fixed request count); in a
   // one-tile block the second tile's offset lies past the buffer range, so
-  // nothing is fetched (and its ring slots are not read).
+  // nothing is fetched (and its ring slots are not read).  K row r of a tile
+  // holds token k_row_token(r); rows r and r + 16 of a group hold tokens 8
+  // apart.
+  const uint32_t k_voff = uint32_t(lane >> 5) * 8u * k_row_bytes + lane_chunk;
   static_for<0, 2>([&](auto tc) {
     constexpr int t = decltype(tc)::value;
-    const uint32_t soff = t < n_tiles ? uint32_t(t * kBN) * k_row_bytes : 0x40000000u;
 #pragma unroll
-    for (int i = 0; i < kSKPerWave; ++i) {
-      const int blk_i = wave + kSWaves * i;
-      const uint32_t sl = uint32_t(64 * blk_i + lane);
-      const uint32_t row = div33(sl);
-      const uint32_t c = sl - row * kKSlots;
-      const uint32_t voff =
-          __umul24(uint32_t(k_row_token(row < kBN ? int(row) : kBN - 1)), k_row_bytes) +
-          (c < kD / 8 ? c : 0) * 16u;
+    for (int i = 0; i < kBN / 2 / kSWaves; ++i) {
+      const int ps = wave + kSWaves * i;  // pair slot 0..31: group ps / 16, rows ps % 16 (+16)
+      const int r = 32 * (ps >> 4) + (ps & 15);
+      const uint32_t soff =
+          t < n_tiles ? uint32_t(t * kBN + k_row_token(r)) * k_row_bytes : 0x40000000u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          k_rsrc, (lds_void_t *)(blk_i < kKDma ? k_ring + t * kTileK + blk_i * 1024 : dummy), 16,
-          voff, soff, 0, 0);
+          k_rsrc, (lds_void_t *)(k_ring + t * kTileK + grow_off(r)), 16, k_voff, soff, 0, 0);
     }
   });
   // q rows and K tiles landed (this wave's DMAs), then every wave's
@@ -217,7 +219,7 @@ void short_prefill_kernel(
   WY_STAMP(1);
   u32x4_t xr[16];
   {
-    const uint32_t qr = lds_u32(v_ring) + uint32_t((hd * kBQ + col) * kKPitch + g * 16);
+    const uint32_t qr = lds_u32(v_ring) + uint32_t(grow_off(hd * kBQ + col) + g * 16);
     static_for<0, 16>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       xr[i] = ds_read_b128_at<i * 32>(qr);
@@ -313,7 +315,7 @@ void short_prefill_kernel(
   f32x16_t s[2];
   const f32x16_t zacc = {};
   {
-    const uint32_t kr = lds_u32(k_ring) + uint32_t((32 * hf + col) * kKPitch + g * 16);
+    const uint32_t kr = lds_u32(k_ring) + uint32_t(grow_off(32 * hf + col) + g * 16);
     if (n_own == 2) {
       // the two units alternate (independent accumulators)
       u32x4_t ka[8];
