@@ -214,6 +214,20 @@ void short_prefill_kernel(
           k_rsrc, (lds_void_t *)(k_ring + t * kTileK + grow_off(r)), 16, k_voff, soff, 0, 0);
     }
   });
+  // The V DMAs' per-lane offsets, computed while the q rows and K tiles are
+  // in flight (the asm pins them here, off the path from the q slices to
+  // the first S^T MFMA).
+  uint32_t v_voff[kSVPerWave];
+#pragma unroll
+  for (int i = 0; i < kSVPerWave; ++i) {
+    const uint32_t sl = uint32_t(64 * (wave + kSWaves * i) + lane);
+    const uint32_t row = div36(sl);
+    const uint32_t c = sl - row * kVSlots;
+    v_voff[i] = __umul24(row < kBN ? row : kBN - 1, v_row_bytes) + (c < kD / 8 ? c : 0) * 16u;
+  }
+  static_assert(kSVPerWave == 5, "pinned V offsets");
+  asm volatile("" : "+v"(v_voff[0]), "+v"(v_voff[1]), "+v"(v_voff[2]), "+v"(v_voff[3]),
+               "+v"(v_voff[4]));
   // q rows and K tiles landed (this wave's DMAs), then every wave's
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   WY_STAMP(1);
@@ -252,14 +266,9 @@ void short_prefill_kernel(
 #pragma unroll
     for (int i = 0; i < kSVPerWave; ++i) {
       const int blk_i = wave + kSWaves * i;
-      const uint32_t sl = uint32_t(64 * blk_i + lane);
-      const uint32_t row = div36(sl);
-      const uint32_t c = sl - row * kVSlots;
-      const uint32_t voff = __umul24(row < kBN ? row : kBN - 1, v_row_bytes) +
-                            (c < kD / 8 ? c : 0) * 16u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           v_rsrc, (lds_void_t *)(blk_i < kVDma ? v_ring + t * kTileV + blk_i * 1024 : dummy), 16,
-          voff, soff, 0, 0);
+          v_voff[i], soff, 0, 0);
     }
   });
 
