@@ -98,6 +98,17 @@ __device__ unsigned long long g_strace[4096 * 32];
 // is below 2^24 bytes.  x / 36 as a multiply-shift, exact for x < 2560.
 __device__ __forceinline__ uint32_t div36(uint32_t x) { return __umul24(x, 1821u) >> 16; }
 
+// A row's values in lanes l and l + 32 (the two k-groups of the MFMA
+// layouts): lo = the value of lane l % 32, hi = that of lane l % 32 + 32, in
+// every lane, by one v_permlane32_swap (a VALU op; a shuffle through
+// ds_bpermute waits in the LDS queue behind the operand reads).
+__device__ __forceinline__ void row_halves(float v, float &lo, float &hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ uint32_t ds_read_b32_at(uint32_t addr) {
   uint32_t r;
   asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
@@ -372,7 +383,11 @@ void short_prefill_kernel(
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[u][e]);
     }
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  {
+    float lo, hi;
+    row_halves(mx, lo, hi);
+    mx = fmaxf(lo, hi);
+  }
   WY_CSTAMP(18);
   // (LDS accesses as inline asm here and below: the compiler would make a
   // visible one wait for every DMA it knows of, the V tiles included)
@@ -439,7 +454,11 @@ void short_prefill_kernel(
   WY_STAMP(4);
   // l: the halves' partial sums in half order (the same bits in both waves)
   float l = hf == 0 ? psum + ps_o : ps_o + psum;
-  l += __shfl_xor(l, 32);
+  {
+    float lo, hi;
+    row_halves(l, lo, hi);
+    l = lo + hi;
+  }
 
   // ---- O^T += V^T P^T over the visible slabs, dims 128 hf .. +127 ----------
   // A operand of slab j, k-step kk, dim block dt: lane (m = lane % 32, g)
