@@ -654,7 +654,7 @@ def main():
     c3 = extra.get("config3_prefill_32x128")
     if c3:
         rp["config3"] = {
-            "kernel": "varlen_causal_prefill_kernel (direct launch)",
+            "kernel": "short_prefill_kernel (eight waves per block, one-round grid of sequences <= 128 tokens)",
             "bound": "hbm (arithmetic intensity 51.6 flop/B < ridge 312)",
             "achieved": c3["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": c3["frac_of_mfma_peak"],
