@@ -338,20 +338,21 @@ void short_prefill_kernel(
     const uint32_t kr = lds_u32(k_ring) + uint32_t(grow_off(32 * hf + col) + g * 16);
     if (n_own == 2) {
       // the two units alternate (independent accumulators)
-      u32x4_t ka[8];
+      constexpr int kKW = 8;  // K operands in flight (12 and 15 measured no faster)
+      u32x4_t ka[kKW];
       auto rd = [&](auto ic) {
         constexpr int i = decltype(ic)::value;  // MFMA i: unit i & 1, k-step i >> 1
         constexpr int off = (i & 1) * kTileK + (i >> 1) * 32;
         return ds_read_b128_at<off>(kr);
       };
-      static_for<0, 8>([&](auto ic) { ka[ic] = rd(ic); });
+      static_for<0, kKW>([&](auto ic) { ka[ic] = rd(ic); });
       static_for<0, 32>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        lgkm_wait1<(i + 8 <= 32 ? 7 : 31 - i)>(ka[i & 7]);
-        s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ka[i & 7]),
+        lgkm_wait1<(i + kKW <= 32 ? kKW - 1 : 31 - i)>(ka[i % kKW]);
+        s[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, ka[i % kKW]),
                                                            qop[i >> 1], i < 2 ? zacc : s[i & 1],
                                                            0, 0, 0);
-        if constexpr (i + 8 < 32) ka[i & 7] = rd(std::integral_constant<int, i + 8>{});
+        if constexpr (i + kKW < 32) ka[i % kKW] = rd(std::integral_constant<int, i + kKW>{});
       });
     } else if (n_own == 1) {
       u32x4_t ka[16];
@@ -473,7 +474,7 @@ void short_prefill_kernel(
   auto pv_slab = [&](auto jc, const u32x4_t(&pj)[2]) {
     constexpr int j = decltype(jc)::value;
     // 8 MFMAs (kk, dt), 6 operands in flight (12 reads: lgkmcnt counts to 15)
-    constexpr int kW = 6;
+    constexpr int kW = 6;  // (4 and 7 measured no faster)
     u32x2_t va[8][2];
     auto rd = [&](auto xc) {
       constexpr int x = decltype(xc)::value;
