@@ -144,9 +144,9 @@ int launch_prefill(const void *q, const int64_t *qs, const void *k, const int64_
   const int order = g_ticket_order.load(std::memory_order_relaxed);
   // A one-round grid of sequences of at most two KV tiles: the eight-wave
   // kernel (chosen by the shape alone, so an input always takes the same one).
-  // (its per-lane DMA offsets use 24-bit multiplies: strides below 2^24 bytes)
-  const bool small_strides = qs[0] < (1 << 23) && qs[1] < (1 << 23) && ks[0] < (1 << 23) &&
-                             vs[0] < (1 << 23);
+  // (its per-lane V DMA offsets use 24-bit multiplies: V row stride below
+  // 2^24 bytes)
+  const bool small_strides = vs[0] < (1 << 23);
   if (!counters && max_seqlen <= 2 * kBN && n_wg <= device_cus() && small_strides &&
       g_short_path.load(std::memory_order_relaxed)) {
     rc = set_short_lds<kRot>();

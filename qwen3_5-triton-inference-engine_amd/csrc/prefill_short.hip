@@ -9,10 +9,10 @@
 // sequence, KV head and 32-token query block as in prefill_kernel.h) runs on
 // eight waves, a pair per query head, so each SIMD holds two waves whose
 // chains interleave:
-//   * S^T: the block's score slabs (two 32-token slabs per KV tile) are dealt
-//     to the pair -- one-tile blocks: slab mt to wave half mt; two-tile
-//     blocks: tile t to half t -- so each wave runs half of the block's QK
-//     MFMAs (K from LDS, q straight from global memory in the MFMA B layout);
+//   * S^T: score slab j holds keys 32j .. 32j+31; query block qb sees slabs
+//     0 .. qb (slab qb is the diagonal one, the later ones are fully masked
+//     and skipped), and wave half hf scores slabs hf and hf + 2 (K from LDS,
+//     q from LDS, where the block's rows were staged by DMA);
 //   * the row max is exact over the whole block (the halves swap their
 //     partial maxima through LDS), so no score can outgrow the reference and
 //     the four-wave kernel's exact two-pass path is not needed;
@@ -22,7 +22,8 @@
 //     takes four cycles: rescaling and re-rounding q cost more than the
 //     block's MFMAs);
 //   * P (bf16, exactly as the reference rounds it) is swapped through LDS, and
-//     each half accumulates O^T for 128 of the 256 dims over every tile;
+//     each half accumulates O^T for 128 of the 256 dims over every visible
+//     slab;
 //   * the row sum l is the halves' partial sums added in half order, so both
 //     waves of a pair normalise with the same l.
 // Results agree with the four-wave kernel to rounding (the same math, with
@@ -30,10 +31,10 @@
 // exact row max as the exponentials' reference); the launch chooses this kernel
 // by the shape alone, so a given input always takes the same kernel.
 //
-// Same LDS rings and DMA layout as prefill_kernel.h (K rows token-permuted,
-// V rows padded for the transposing reads); K/V tiles land by LDS DMA, and
-// every LDS access is inline asm with explicit waits, so the compiler adds
-// no wait for the DMAs before them.
+// The LDS holds the rings of prefill_kernel.h (two K slots, two V slots; V
+// rows padded for the transposing reads), with q and K rows in the paired
+// layout below; tiles land by LDS DMA, and every LDS access is inline asm with
+// explicit waits, so the compiler adds no wait for the DMAs before them.
 #include "prefill_kernel.h"
 
 namespace wy_prefill {
@@ -63,7 +64,7 @@ static_assert(64 * kSWaves * kSVPerWave <= 2560,
 constexpr int kXchWave = 4096;
 
 #if WY_TRACE
-// per-block phase stamps (s_memrealtime, 100 MHz), 16 per block
+// per-block phase stamps (s_memrealtime at 100 MHz; s_memtime cycles), 32 slots per block
 namespace {
 __device__ unsigned long long g_strace[4096 * 32];
 }  // namespace
