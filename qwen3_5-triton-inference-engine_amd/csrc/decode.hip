@@ -55,6 +55,20 @@ using namespace wy;
 
 namespace {
 
+#if WY_TRACE
+// per-workgroup phase stamps of the split kernel (s_memrealtime, 100 MHz)
+__device__ unsigned long long g_dtrace[1024 * 16];
+#define WY_DSTAMP(i)                                                        \
+  do {                                                                      \
+    unsigned long long t_ = __builtin_amdgcn_s_memrealtime();               \
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+s"(t_)::"memory");              \
+    if (threadIdx.x == 0 && blockIdx.x < 1024) g_dtrace[blockIdx.x * 16 + (i)] = t_; \
+  } while (0)
+#else
+#define WY_DSTAMP(i) \
+  do {               \
+  } while (0)
+#endif
 constexpr int kD = 256;   // head_dim
 constexpr int kG = 4;     // query heads per KV head
 constexpr int kWaves = 4; // wavefronts per split workgroup
@@ -444,6 +458,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
         : "memory");
     seq_len = pos_lo + 1;
   }
+  WY_DSTAMP(1);
   const int npg = (seq_len + kPage - 1) / kPage;
   const int pps = split_pps(npg, min_pps);
   const int nact = (npg + pps - 1) / pps;
@@ -632,6 +647,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   }
   __syncthreads();
 
+  WY_DSTAMP(2);
   f32x4_t sc_new = {0.f, 0.f, 0.f, 0.f};
   u32x2_t vnew = {0u, 0u};
   bool owns_new = false;
@@ -763,6 +779,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
     page(npw - 1, std::false_type{});
   }
 
+  WY_DSTAMP(3);
   // ---- merge the four wave states through LDS ---------------------------------
 #pragma unroll
   for (int r = 0; r < kG; ++r)
@@ -776,6 +793,7 @@ void paged_decode_split_kernel(const DecodeArgs a) {
   }
   __syncthreads();
 
+  WY_DSTAMP(4);
   // waves 0..3 finish one query head each
   const int r = wave & (kG - 1);
   const bool head_wave = wave < kG;
@@ -847,12 +865,32 @@ void paged_decode_split_kernel(const DecodeArgs a) {
       return sm.last != 0;
     };
     publish(adst, mdst, ldst, A, M, L);
+    WY_DSTAMP(5);
     int *top = a.counters + b * a.hkv + h;
     const int ng = a.two_level ? (nact + kMergeGroup - 1) / kMergeGroup : 1;
     if (ng == 1) {
-      if (!count(top, nact) || !head_wave) return;
+      const bool lastc = count(top, nact);
+      WY_DSTAMP(6);
+#if WY_TRACE
+      if (threadIdx.x == 0 && blockIdx.x < 1024) {
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        g_dtrace[blockIdx.x * 16 + 12] = (unsigned long long)b | ((unsigned long long)h << 8) |
+                                         ((unsigned long long)s << 16) |
+                                         ((unsigned long long)nact << 24) |
+                                         ((unsigned long long)(p1 - p0) << 32) |
+                                         ((unsigned long long)lastc << 48) |
+                                         ((unsigned long long)(xcc & 15) << 52);
+      }
+#endif
+      if (!lastc || !head_wave) return;
       const Merged mr = merge_slots<true>(a, b, hq, 0, 1, nact, lane);
+      WY_DSTAMP(7);
       store_out4(a, b, hq, lane * 4, mr.A, mr.L, &gate_pre);
+#if WY_TRACE
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      WY_DSTAMP(8);
+#endif
       return;
     }
     const int g = s / kMergeGroup;
@@ -1381,3 +1419,14 @@ extern "C" int wy_page_stream_read(const void *k_cache, const void *v_cache,
       vcs[0], vcs[1], block_table, bt_stride0, pos, batch, num_kv_heads, sums);
   return wyh::launch_status();
 }
+
+#if WY_TRACE
+extern "C" int wy_decode_trace_read(void *host, size_t bytes, int clear) {
+  if (clear) {
+    static unsigned long long zeros[1024 * 16];
+    return int(hipMemcpyToSymbol(HIP_SYMBOL(g_dtrace), zeros, sizeof(zeros)));
+  }
+  return int(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_dtrace),
+                                 bytes < sizeof(g_dtrace) ? bytes : sizeof(g_dtrace)));
+}
+#endif
