@@ -142,6 +142,28 @@ __device__ __forceinline__ void lgkm_wait(u32x2_t (&a)[4], u32x2_t (&b)[4]) {
                : "n"(kN));
 }
 
+// A row's values in lanes l and l + 32 (the two k-groups of the MFMA
+// layouts): lo = the value of lane l % 32, hi = that of lane l % 32 + 32, in
+// every lane, by one v_permlane32_swap (a VALU op; a shuffle through
+// ds_bpermute waits in the LDS queue behind the operand reads and DMAs).
+__device__ __forceinline__ void row_halves(float v, float &lo, float &hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_max2(float v) {
+  float lo, hi;
+  row_halves(v, lo, hi);
+  return fmaxf(lo, hi);
+}
+// lo + hi: the same sum, operand for operand, in both lanes of the row
+__device__ __forceinline__ float row_sum2(float v) {
+  float lo, hi;
+  row_halves(v, lo, hi);
+  return lo + hi;
+}
+
 // Token held by LDS row `row` of a K tile (see the header comment).
 __device__ __forceinline__ int k_row_token(int row) {
   const int mt = row >> 5, r = row & 31;
@@ -673,7 +695,7 @@ void varlen_causal_prefill_kernel(
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[mt][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = row_max2(mx);
         if constexpr (kMode == 1) m_acc = fmaxf(m_acc, mx);
         else {
           m_ref = mx;
@@ -901,7 +923,7 @@ void varlen_causal_prefill_kernel(
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[mt][e]);
-      m_ref = fmaxf(mx, __shfl_xor(mx, 32));
+      m_ref = row_max2(mx);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -992,7 +1014,7 @@ void varlen_causal_prefill_kernel(
 #if WY_TRACE
   tr2 = __builtin_amdgcn_s_memrealtime();
 #endif
-  float l = l_part + __shfl_xor(l_part, 32);
+  float l = row_sum2(l_part);
   // Some score exceeded its row's first-tile maximum by a factor over 2^64
   // (or is not finite): l is then at least 2^64.
   const bool over = qrow < n && !(l < kHeadroomScale);
@@ -1011,7 +1033,7 @@ void varlen_causal_prefill_kernel(
     issue_first();
     zero_acc();
     run_pass(std::integral_constant<int, 2>{});
-    l = l_part + __shfl_xor(l_part, 32);
+    l = row_sum2(l_part);
     if constexpr (kEarly) {
       // the passes reused the K ring and the q registers: request the next
       // block's again

@@ -99,17 +99,6 @@ __device__ unsigned long long g_strace[4096 * 32];
 // is below 2^24 bytes.  x / 36 as a multiply-shift, exact for x < 2560.
 __device__ __forceinline__ uint32_t div36(uint32_t x) { return __umul24(x, 1821u) >> 16; }
 
-// A row's values in lanes l and l + 32 (the two k-groups of the MFMA
-// layouts): lo = the value of lane l % 32, hi = that of lane l % 32 + 32, in
-// every lane, by one v_permlane32_swap (a VALU op; a shuffle through
-// ds_bpermute waits in the LDS queue behind the operand reads).
-__device__ __forceinline__ void row_halves(float v, float &lo, float &hi) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  lo = __uint_as_float(r[0]);
-  hi = __uint_as_float(r[1]);
-}
-
 __device__ __forceinline__ uint32_t ds_read_b32_at(uint32_t addr) {
   uint32_t r;
   asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(addr));
