@@ -76,6 +76,10 @@ def test_short_kernel_vs_oracle_and_four_wave(pkg, dev, lengths):
     # the same math to rounding (the scale on the scores instead of on a
     # bf16-rounded q): a few bf16 ulps at most
     assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3, (d.max().item(), d.mean().item())
+    if sum(lengths) >= 1024:
+        # the two kernels round apart: equal outputs would mean the launch did
+        # not take the eight-wave kernel
+        assert d.max().item() > 0
     again = pkg.gqa_attention_varlen_causal(qd, kd, vd, cud, max(lengths))
     assert torch.equal(again, got)
 
