@@ -74,16 +74,31 @@ __global__ __launch_bounds__(256) void paged_kv_fill_varlen_kernel(
   const bf16_t *ksrc = k + h * k_h + tok0 * k_t;
   const bf16_t *vsrc = v + h * v_h + tok0 * v_t;
   if constexpr (kVec) {
+    // Each thread requests its K and V chunks of a round (two of each)
+    // before it stores any: one memory round trip per round instead of one
+    // per chunk (a full page of D = 256 is one round).
+    constexpr int kU = 2;
     const int cpr = D / 8;  // 16-byte chunks per row
     const int total = rows * cpr;
-    for (int i = threadIdx.x; i < 2 * total; i += 256) {
-      const bool is_v = i >= total;
-      const int j = is_v ? i - total : i;
-      const int r = j / cpr, c = (j - r * cpr) * 8;
-      if (!is_v)
-        st16_nt(kdst + r * kc_s + c, ld16(ksrc + r * k_t + c));
-      else
-        st16_nt(vdst + r * vc_s + c, ld16(vsrc + r * v_t + c));
+    for (int i0 = threadIdx.x; i0 < total; i0 += 256 * kU) {
+      u32x4_t xk[kU], xv[kU];
+      int ro[kU], co[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = i0 + 256 * u;
+        ro[u] = i / cpr;
+        co[u] = (i - ro[u] * cpr) * 8;
+        if (i < total) {
+          xk[u] = ld16(ksrc + ro[u] * k_t + co[u]);
+          xv[u] = ld16(vsrc + ro[u] * v_t + co[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (i0 + 256 * u < total) {
+          st16_nt(kdst + ro[u] * kc_s + co[u], xk[u]);
+          st16_nt(vdst + ro[u] * vc_s + co[u], xv[u]);
+        }
     }
   } else {
     const int total = rows * D;
