@@ -10,14 +10,18 @@ namespace {
 
 
 // ------------------------------------------------------------ partial RoPE --
-// Fast path.  The grid's first part rotates: a lane owns chunk c (8 dims) of
-// the first rotary half of one (b, t) row for two heads, so its 8 sin/cos
-// pairs (which depend on (b, t, j) only) serve both; each head's chunk c and
-// partner chunk c + R/16 are rotated together.
+// Fast path.  The grid's first part rotates: a lane owns dims 2c, 2c + 1 of
+// the first rotary half of one (b, t) row for two heads, so its 2 sin/cos
+// pairs (which depend on (b, t, j) only) serve both; each head's pair and
+// partner pair (dims + R/2) are rotated together.  (Two dims per lane rather
+// than a 16-byte chunk of eight: the accurate sin/cos cost tens of VALU
+// instructions each, and eight in a row made the rotating lanes the launch's
+// critical path when there are few heads.)
 // The second part copies the tail chunks [R/8, D/8) of every (b, t, h) row.
 // The two kinds of work sit in different wavefronts, so neither waits on the
 // other's branch.  Reference: partial_rope.py:34-132.
 constexpr int kRopeHeads = 2;  // heads per rotating lane
+constexpr int kRopeDims = 2;   // first-half dims per rotating lane
 
 __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
     const bf16_t *__restrict__ x, int64_t xs_b, int64_t xs_h, int64_t xs_t,
@@ -26,45 +30,42 @@ __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
     const float *__restrict__ inv_freq, int H, int T, int D, int R, uint32_t bt_rows) {
   // index math in 32 bits: the host launches this kernel only when the grid
   // and row counts fit
-  const uint32_t half_chunks = uint32_t(R) / 16u;
+  const uint32_t half_units = uint32_t(R) / (2u * kRopeDims);
   const uint32_t hgroups = uint32_t(H + kRopeHeads - 1) / kRopeHeads;
-  const uint32_t n_rot = bt_rows * half_chunks * hgroups;
+  const uint32_t n_rot = bt_rows * half_units * hgroups;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
   if (gid < n_rot) {
-    // lane -> (b, t, head group, chunk), chunk fastest
-    const uint32_t q1 = gid / half_chunks;
-    const int c = int(gid - q1 * half_chunks);
+    // lane -> (b, t, head group, unit), unit fastest
+    const uint32_t q1 = gid / half_units;
+    const int c = int(gid - q1 * half_units);
     const uint32_t bt = q1 / hgroups;
     const int h0 = int(q1 - bt * hgroups) * kRopeHeads;
     const int t = int(bt % uint32_t(T)), b = int(bt / uint32_t(T));
     const bf16_t *xr = x + b * xs_b + t * xs_t;
     bf16_t *orow = out + b * os_b + t * os_t;
     const float p = load_pos(pos, b * ps_b + int64_t(t) * ps_t, pos64 != 0);
-    u32x4_t a[kRopeHeads], bb[kRopeHeads];
+    uint32_t a[kRopeHeads], bb[kRopeHeads];
 #pragma unroll
     for (int i = 0; i < kRopeHeads; ++i) {
       const int h = min(h0 + i, H - 1);
-      a[i] = ld16(xr + h * xs_h + c * 8);
-      bb[i] = ld16(xr + h * xs_h + R / 2 + c * 8);
+      a[i] = *reinterpret_cast<const uint32_t *>(xr + h * xs_h + c * kRopeDims);
+      bb[i] = *reinterpret_cast<const uint32_t *>(xr + h * xs_h + R / 2 + c * kRopeDims);
     }
-    float sn[8], cs[8];
+    float sn[kRopeDims], cs[kRopeDims];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) rope_sincos(p, inv_freq[c * 8 + e], sn[e], cs[e]);
+    for (int e = 0; e < kRopeDims; ++e)
+      rope_sincos(p, inv_freq[c * kRopeDims + e], sn[e], cs[e]);
 #pragma unroll
     for (int i = 0; i < kRopeHeads; ++i) {
       if (h0 + i >= H) break;
-      u32x4_t oa, ob;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        float o1l, o2l, o1h, o2h;
-        rope_rotate(bf16_lo(a[i][w]), bf16_lo(bb[i][w]), cs[2 * w], sn[2 * w], o1l, o2l);
-        rope_rotate(bf16_hi(a[i][w]), bf16_hi(bb[i][w]), cs[2 * w + 1], sn[2 * w + 1], o1h,
-                    o2h);
-        oa[w] = pack_bf16x2(o1l, o1h);
-        ob[w] = pack_bf16x2(o2l, o2h);
-      }
-      st16_nt(orow + (h0 + i) * os_h + c * 8, oa);
-      st16_nt(orow + (h0 + i) * os_h + R / 2 + c * 8, ob);
+      float o1l, o2l, o1h, o2h;
+      rope_rotate(bf16_lo(a[i]), bf16_lo(bb[i]), cs[0], sn[0], o1l, o2l);
+      rope_rotate(bf16_hi(a[i]), bf16_hi(bb[i]), cs[1], sn[1], o1h, o2h);
+      __builtin_nontemporal_store(pack_bf16x2(o1l, o1h),
+                                  reinterpret_cast<uint32_t *>(orow + (h0 + i) * os_h + c * kRopeDims));
+      __builtin_nontemporal_store(
+          pack_bf16x2(o2l, o2h),
+          reinterpret_cast<uint32_t *>(orow + (h0 + i) * os_h + R / 2 + c * kRopeDims));
     }
     return;
   }
@@ -72,6 +73,7 @@ __global__ __launch_bounds__(256) void partial_rope_vec_kernel(
   // one (the [T, H, D] buffer the prefill passes as a permuted view), tokens
   // fastest otherwise
   const uint32_t tail = uint32_t(D - R) / 8u;
+  if (tail == 0) return;  // R == D: no tail (and no division by zero)
   const uint32_t k = gid - n_rot;
   const uint32_t row = k / tail;
   if (row >= bt_rows * uint32_t(H)) return;
@@ -179,17 +181,18 @@ extern "C" int wy_partial_rope(const void *x, const int64_t *xs, void *out,
   const int64_t rows = int64_t(batch) * num_heads * num_tokens;
   if (rows == 0) return WY_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // fast path: rotating lanes (2 dims x 2 heads each) + tail lanes (one
+  // 16-byte chunk each), counted in 32 bits
+  const int64_t bt_rows = int64_t(batch) * num_tokens;
+  const int64_t n_vec = bt_rows * (rotary_dim / 4) * ((num_heads + 1) / 2) +
+                        bt_rows * num_heads * (head_dim / 8 - rotary_dim / 8);
   const bool vec = head_dim % 8 == 0 && rotary_dim % 16 == 0 && xs[3] == 1 &&
-                   rows * (head_dim / 8) + 256 < int64_t(INT32_MAX) &&
+                   n_vec + 256 < int64_t(INT32_MAX) &&
                    os[3] == 1 && xs[0] % 8 == 0 && xs[1] % 8 == 0 && xs[2] % 8 == 0 &&
                    os[0] % 8 == 0 && os[1] % 8 == 0 && os[2] % 8 == 0 &&
                    wyh::aligned16(x) && wyh::aligned16(out);
   if (vec) {
-    const int64_t bt_rows = int64_t(batch) * num_tokens;
-    // rotating lanes walk the heads; tail lanes copy one chunk each
-    const int64_t n = bt_rows * (rotary_dim / 16) * ((num_heads + 1) / 2) +
-                      bt_rows * num_heads * (head_dim / 8 - rotary_dim / 8);
-    partial_rope_vec_kernel<<<blocks_for(n), 256, 0, s>>>(
+    partial_rope_vec_kernel<<<blocks_for(n_vec), 256, 0, s>>>(
         static_cast<const bf16_t *>(x), xs[0], xs[1], xs[2], static_cast<bf16_t *>(out),
         os[0], os[1], os[2], position_ids, ps[0], ps[1], pos_is_int64, inv_freq,
         num_heads, num_tokens, head_dim, rotary_dim, uint32_t(bt_rows));

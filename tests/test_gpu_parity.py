@@ -169,7 +169,10 @@ def test_rope_golden(pkg, dev):
                                                ((1, 2, 17, 256), 64, torch.int32),
                                                ((2, 3, 65, 128), 64, torch.int32),
                                                ((1, 4, 33, 160), 96, torch.int64),
-                                               ((32, 8, 1, 256), 64, torch.int64)])
+                                               ((32, 8, 1, 256), 64, torch.int64),
+                                               # rotary over the whole head: no tail
+                                               ((3, 5, 19, 64), 64, torch.int32),
+                                               ((1, 2, 17, 128), 128, torch.int64)])
 def test_rope_shapes(pkg, dev, shape, R, pos_dtype):
     say(f"rope shape={shape} R={R}")
     gen = torch.Generator().manual_seed(R + shape[2])
